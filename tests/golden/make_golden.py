@@ -1,0 +1,44 @@
+"""Writes tests/golden/digests.json from the reference's own C runtime.
+
+Run in the build container only (it needs /root/reference): `make -C oracle`
+first builds oracle/_ref/libpresk_ref.so from the reference's
+crates/presk-export-c/c/presk_rt.h and presk_libm.c.  The digests are data:
+per function, the order-free digest (oracle/digest.c) of each of its 256
+blocks of inputs (every f32 for the f32 functions and conversions, every code
+for the widenings, a fixed sample for the narrowings from f64), plus a few
+hundred sample input/output pairs per function for readable failures.
+
+    python tests/golden/make_golden.py
+"""
+import ctypes
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+from tests.golden import spec  # noqa: E402
+
+
+def main():
+    lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "_ref", "libpresk_ref.so"))
+    lib.pd_digest.restype = ctypes.c_uint64
+    lib.pd_digest.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64]
+    lib.pd_eval.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32), ctypes.c_size_t]
+    out = {"about": "digests of the reference's presk_rt.h / presk_libm.c (crates/presk-export-c/c), see oracle/digest.c", "functions": {}}
+    for name, (fid, domain) in spec.FUNCTIONS.items():
+        blocks = spec.blocks(domain)
+        digs = [format(lib.pd_digest(fid, lo, hi), "016x") for lo, hi in blocks]
+        ins = spec.sample_inputs(domain)
+        arr_in = (ctypes.c_uint64 * len(ins))(*ins)
+        arr_out = (ctypes.c_uint32 * len(ins))()
+        assert lib.pd_eval(fid, arr_in, arr_out, len(ins)) == 0
+        out["functions"][name] = {"id": fid, "domain": domain, "blocks": digs, "samples": [[i, o] for i, o in zip(ins, arr_out)]}
+        print(name, digs[0], flush=True)
+    with open(os.path.join(HERE, "digests.json"), "w") as f:
+        json.dump(out, f, indent=0)
+
+
+if __name__ == "__main__":
+    main()
