@@ -1,0 +1,136 @@
+/* presk_hip.h -- the C ABI of the MI355X (gfx950) executor of Presk's realized
+ * loop nests: a drop-in `KernelExec` for `--backend hip`.
+ *
+ * The reference's seam is `trait KernelExec` (crates/presk-kernel/src/host.rs:
+ * 28-95), whose native implementations compile each `Kernel` once
+ * (`trait KernelCompiler`, crates/presk-cranelift/src/lib.rs:48-53) into a
+ * `KernelFn = unsafe extern "C" fn(bufs: *const *mut u8, lo: i64, hi: i64)`
+ * (crates/presk-cranelift/src/lib.rs:38-42) and call it over a pointer table
+ * [inputs..., output, overflow flag iff the kernel stores f16/e8m15]
+ * (crates/presk-cranelift/src/lib.rs:1609-1629).  This ABI keeps that shape,
+ * with device pointers and a HIP stream:
+ *
+ *   presk_hip_compile  <->  KernelCompiler::compile(&Kernel) -> KernelFn
+ *   presk_hip_run      <->  the KernelFn call f(bufs, lo, hi)
+ *   presk_hip_alloc/free/h2d/d2h/sync
+ *                      <->  the host's `Buf`s made device-resident
+ *                           (crates/presk-rt/src/lib.rs:760-915)
+ *
+ * A kernel arrives as its text (`impl Display for Kernel`,
+ * crates/presk-kernel/src/ir.rs:495-595) plus the two facts the text does not
+ * carry: its storage type (`Kernel::dtype`) and its lane width
+ * (`Kernel::lanes`).
+ *
+ * Errors: every function returns 0 on success and a negative code otherwise;
+ * presk_hip_last_error() then gives the message, which starts with the
+ * reference's code: "E10001" for an executor error
+ * (crates/presk-cranelift/src/lib.rs:34-36), "E7005" for a kernel whose
+ * formats the executor does not compute (crates/presk-rt/src/lib.rs:567-591),
+ * "E7007" for the overflow guard (crates/presk-kernel/src/host.rs:140-177).
+ *
+ * Threading: one host thread drives a device (as `KernelBackend` is
+ * single-threaded, crates/presk-kernel/src/host.rs:256); launches are
+ * asynchronous on the given stream, and a buffer is read on the host only
+ * after presk_hip_sync on that stream.
+ */
+#ifndef PRESK_HIP_H
+#define PRESK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PRESK_HIP_OK 0
+#define PRESK_HIP_ERR (-1)       /* E10001: executor or HIP error */
+#define PRESK_HIP_REFUSED (-2)   /* E7005: formats not computed natively */
+#define PRESK_HIP_OVERFLOW (-3)  /* E7007: a narrowing store overflowed */
+
+/* How a kernel's reductions are ordered.
+ * EXACT: every sum in index order, bit-identical to `--backend kernel`
+ *        (ReductionOrder::Sequential, crates/presk-rt/src/lib.rs:251-285).
+ * FAST:  contractions on MFMA tiles with f32 accumulation, a reassociating
+ *        order the kernel's info names (the declared-order rule of
+ *        crates/presk-rt/src/lib.rs:262-268); every other nest as in EXACT.  */
+#define PRESK_HIP_EXACT 0
+#define PRESK_HIP_FAST 1
+
+typedef struct presk_hip_kernel presk_hip_kernel;
+
+/* What a compiled kernel is: no counterpart in the reference beyond
+ * `KernelExec::name` and the launch log (host.rs:317-321); used by the
+ * harness to report the class chosen and the roofline of each launch. */
+typedef struct {
+    char kind[32];        /* "gemm", "rows", "generic", ... */
+    char order[32];       /* "sequential", "mfma-k32", ... */
+    int32_t guarded;      /* the pointer table ends with a u32 flag */
+    int32_t n_inputs;
+    int64_t split_bound;  /* the [lo,hi) range of presk_hip_run, or -1 */
+    double flops;         /* algorithmic flops of one launch (2*I*J*K for a contraction) */
+    double bytes;         /* algorithmic bytes: inputs once + output once, at storage width
+                             (crates/presk-kernel/src/cost.rs:26-95) */
+} presk_hip_info;
+
+/* Selects the device and sets the executor up.  No counterpart in the
+ * reference (its executors need none); must be called before any other
+ * function that touches the device. */
+int presk_hip_init(int device);
+
+/* The message of the calling thread's last failed call ("" if none). */
+const char *presk_hip_last_error(void);
+
+/* KernelCompiler::compile (crates/presk-cranelift/src/lib.rs:48-53): reads the
+ * kernel's text, chooses its HIP kernel, builds it.  `dtype` is "f64", "f32",
+ * "bf16", "f16" or "e8m15"; `lanes` is Kernel::lanes; `mode` is
+ * PRESK_HIP_EXACT or PRESK_HIP_FAST.  Refuses (PRESK_HIP_REFUSED) a kernel
+ * whose formats are not its storage type's arithmetic (ir.rs:204-259) and
+ * quantised inputs, as the native backend's `prepare` does (host.rs:416-434). */
+int presk_hip_compile(const char *text, const char *dtype, int lanes, int mode, presk_hip_kernel **out);
+
+/* The KernelFn call (crates/presk-cranelift/src/lib.rs:38-42): `bufs` holds
+ * device pointers [inputs..., output, overflow flag iff guarded]; [lo, hi) is
+ * the range of the outermost loop when Kernel::parallel_outer holds
+ * (ir.rs:336-373), else it is ignored.  `stream` is a hipStream_t (NULL: the
+ * null stream).  Asynchronous: the overflow flag, a device u32 the caller
+ * zeroes, is read after presk_hip_sync (E7007 if set). */
+int presk_hip_run(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi, void *stream);
+
+int presk_hip_kernel_info(const presk_hip_kernel *k, presk_hip_info *info);
+void presk_hip_release(presk_hip_kernel *k);
+
+/* The kernel's text as the executor read it, printed back as the reference
+ * prints a kernel (ir.rs:495-595): the round trip that pins the reader.
+ * Writes at most `cap` bytes including the terminator; returns the full
+ * length, or a negative code. */
+int64_t presk_hip_kernel_text(const presk_hip_kernel *k, char *buf, size_t cap);
+
+/* Device memory and streams: the host's buffers made resident
+ * (crates/presk-rt/src/lib.rs:760-915 holds them in host memory). */
+int presk_hip_alloc(size_t bytes, void **dev);
+int presk_hip_free(void *dev);
+int presk_hip_h2d(void *dev, const void *host, size_t bytes, void *stream);
+int presk_hip_d2h(void *host, const void *dev, size_t bytes, void *stream);
+int presk_hip_memset(void *dev, int value, size_t bytes, void *stream);
+int presk_hip_sync(void *stream);
+int presk_hip_stream_create(void **stream);
+int presk_hip_stream_destroy(void *stream);
+
+/* Timing of launches with HIP events on the launch stream, in the shape of the
+ * reference's per-launch `TimedExec` (crates/presk-kernel/src/cost.rs:719-780):
+ * runs `k` `reps` times on `stream` after `warmup` untimed runs and stores the
+ * mean milliseconds per launch. */
+int presk_hip_time(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi, void *stream, int warmup,
+                   int reps, double *ms_per_launch);
+
+/* Self-test of the device's scalar functions over a domain block: the digest
+ * (sum of splitmix64 finalizers of (i << 32 | out_i)) of function `fn` over
+ * inputs [lo, hi), as tests/golden/digests.json holds the reference's.  No
+ * counterpart in the reference; for the exhaustive device checks. */
+int presk_hip_scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t *digest);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

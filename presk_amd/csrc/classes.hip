@@ -1,0 +1,362 @@
+// The recognizer: which hand-written kernel runs a nest.  A nest is matched
+// by what it computes -- its primitive (the kernel's name, as the lowering
+// names it, crates/presk-kernel/src/lower.rs:250-297), its buffers' shapes,
+// and, where the primitive leaves the operands' roles open (`ein`), the index
+// pattern of its loads -- never by its layout, since every layout point of a
+// nest computes the same values (lower.rs:846-905).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <functional>
+#include <mutex>
+
+#include "devfmt.hpp"
+#include "executor.hpp"
+#include "gemm.hpp"
+#include "presk_hip.h"
+
+namespace presk {
+
+namespace {
+
+// `align` (lower.rs:37-55): where each axis of `src` sits in `target`.
+bool align(const BufSpec& src, const BufSpec& target, std::vector<int>* out) {
+    out->clear();
+    if (src.dims.size() > target.dims.size()) return false;
+    const size_t off = target.dims.size() - src.dims.size();
+    bool positional = true;
+    for (size_t i = 0; i < src.dims.size(); ++i) {
+        const std::string &a = src.names[i], &t = target.names[off + i];
+        if (src.dims[i] != target.dims[off + i] || !(a.empty() || t.empty() || a == t)) positional = false;
+    }
+    if (positional) {
+        for (size_t i = 0; i < src.dims.size(); ++i) out->push_back((int)(off + i));
+        return true;
+    }
+    for (size_t i = 0; i < src.dims.size(); ++i) {
+        if (src.names[i].empty()) return false;
+        int p = -1;
+        for (size_t j = 0; j < target.dims.size(); ++j)
+            if (target.names[j] == src.names[i] && target.dims[j] == src.dims[i]) { p = (int)j; break; }
+        if (p < 0) return false;
+        out->push_back(p);
+    }
+    return true;
+}
+
+int64_t prod(const std::vector<int64_t>& d, size_t from, size_t to) {
+    int64_t p = 1;
+    for (size_t i = from; i < to && i < d.size(); ++i) p *= d[i];
+    return p;
+}
+
+// The operands of the product in a contraction nest's innermost statement:
+// `acc = acc + x * Load(1, ix1)` with x a Load(0, ix0) or a scalar set from
+// one just before.  Fills the loop variables of each load's index.
+bool product_pattern(const Kernel& k, std::vector<int>* vars0, std::vector<int>* vars1, std::vector<int>* out_vars) {
+    const Expr* load0 = nullptr;
+    const Expr* load1 = nullptr;
+    const std::vector<const Stmt*>* innermost = nullptr;
+    std::function<void(const std::vector<const Stmt*>&)> walk = [&](const std::vector<const Stmt*>& body) {
+        for (auto s : body) {
+            if (s->kind == Stmt::For) walk(s->body);
+            if (s->kind == Stmt::Store && s->buf == k.out_buf()) {
+                out_vars->clear();
+                for (auto e : s->index) out_vars->push_back(e->kind == Expr::Iv ? e->id : -1);
+            }
+        }
+        for (size_t i = 0; i < body.size(); ++i) {
+            const Stmt* s = body[i];
+            if (s->kind != Stmt::Set || s->value->kind != Expr::Bin || s->value->op != Op::Add) continue;
+            const Expr* a = s->value->kids[0];
+            const Expr* m = s->value->kids[1];
+            if (a->kind != Expr::Sv || a->id != s->var || m->kind != Expr::Bin || m->op != Op::Mul) continue;
+            const Expr* x = m->kids[0];
+            const Expr* w = m->kids[1];
+            if (w->kind != Expr::Load || w->id != 1) continue;
+            if (x->kind == Expr::Sv && i > 0 && body[i - 1]->kind == Stmt::Set && body[i - 1]->var == x->id &&
+                body[i - 1]->value->kind == Expr::Load && body[i - 1]->value->id == 0)
+                x = body[i - 1]->value;
+            if (x->kind != Expr::Load || x->id != 0) continue;
+            load0 = x;
+            load1 = w;
+            innermost = &body;
+        }
+    };
+    walk(k.body);
+    if (!load0 || !load1 || !innermost) return false;
+    auto vars = [](const Expr* l, std::vector<int>* v) {
+        v->clear();
+        for (auto e : l->kids) {
+            if (e->kind != Expr::Iv) return false;
+            v->push_back(e->id);
+        }
+        return true;
+    };
+    return vars(load0, vars0) && vars(load1, vars1);
+}
+
+// ---- the contraction class ---------------------------------------------------------
+struct GemmPlan : ClassPlan {
+    GemmArgs g{};          // pointers filled at launch
+    std::string name;
+    int storage = kF32;
+    bool epilogue = false;
+    int n_in = 2;
+    bool guarded = false;
+    int64_t split_bound = -1;  // the KernelFn split loop's bound
+    bool split_on_batch = false;
+    long long rows_per_iter = 0;   // M rows (or batch entries) one outer iteration covers
+    mutable float* work = nullptr;
+    mutable size_t work_floats = 0;
+
+    const char* kind() const override { return "gemm"; }
+    std::string order() const override {
+        std::string o = storage == kF32 ? "mfma-f32-k4" : "mfma-k32";
+        if (g.splits > 1) o += "-split" + std::to_string(g.splits);
+        return o;
+    }
+
+    hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, hipStream_t stream) const override {
+        GemmArgs a = g;
+        a.A = bufs[0];
+        a.B = bufs[1];
+        a.bias = epilogue ? bufs[2] : nullptr;
+        a.C = bufs[n_in];
+        a.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
+        const int esz = storage == kF32 ? 4 : 2;
+        if (split_bound >= 0 && !(lo == 0 && hi == split_bound)) {
+            if (lo < 0 || hi > split_bound || lo > hi) return hipErrorInvalidValue;
+            if (lo == hi) return hipSuccess;
+            if (split_on_batch) {
+                a.A = (const char*)a.A + lo * a.sa_b[0] * esz;
+                a.B = (const char*)a.B + lo * a.sb_b[0] * esz;
+                a.C = (char*)a.C + lo * a.sc_b[0] * esz;
+                a.batch = a.batch / a.bdim[0] * (hi - lo);
+                a.bdim[0] = hi - lo;
+            } else {
+                const long long m0 = lo * rows_per_iter;
+                a.A = (const char*)a.A + m0 * a.sa_m * esz;
+                a.C = (char*)a.C + m0 * a.N * esz;
+                a.M = (hi - lo) * rows_per_iter;
+                a.tiles_m = (int)((a.M + gemm_tile_m() - 1) / gemm_tile_m());
+                if (a.bias && a.sbias_m) a.bias = (const char*)a.bias + ((m0 / a.bias_div) % a.bias_mod) * a.sbias_m * esz;
+                if (a.splits > 1) return hipErrorInvalidValue;  // a partial range of a split-K plan
+            }
+        }
+        // 16-byte loads need aligned rows
+        const int vec = storage == kF32 ? 4 : 8;
+        auto aligned = [&](const void* p, long long row_stride, const long long* bs) {
+            if ((uintptr_t)p % 16) return false;
+            if (row_stride % vec) return false;
+            for (int d = 0; d < a.nbatch; ++d)
+                if (bs[d] % vec) return false;
+            return true;
+        };
+        a.a_vec = aligned(a.A, a.a_kcontig ? a.sa_m : a.sa_k, a.sa_b);
+        a.b_vec = aligned(a.B, a.b_kcontig ? a.sb_n : a.sb_k, a.sb_b);
+        if (a.splits > 1) {
+            const size_t need = (size_t)a.splits * a.M * a.N;
+            if (need > work_floats) {
+                if (work) hipFree(work);
+                work = nullptr;
+                hipError_t e = hipMalloc(&work, need * sizeof(float));
+                if (e != hipSuccess) return e;
+                work_floats = need;
+            }
+            a.work = work;
+        }
+        return gemm_launch(a, stream);
+    }
+
+    ~GemmPlan() override {
+        if (work) hipFree(work);
+    }
+};
+
+int storage_of(Ty t) {
+    switch (t) {
+        case Ty::F32: return kF32;
+        case Ty::BF16: return kBF16;
+        case Ty::F16: return kF16;
+        default: return -1;
+    }
+}
+
+void plan_tiles(GemmArgs& g) {
+    g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
+    g.tiles_n = (int)((g.N + gemm_tile_n() - 1) / gemm_tile_n());
+    g.splits = 1;
+    g.k_per_split = g.K;
+    const long long tiles = (long long)g.tiles_m * g.tiles_n * g.batch;
+    const int bk = gemm_block_k(g.storage);
+    // fewer tiles than compute units and a long K: split K across workgroups
+    if (g.batch == 1 && tiles < 256 && g.K >= 8 * bk) {
+        long long s = (512 + tiles - 1) / tiles;
+        long long maxs = g.K / (4 * bk);
+        if (s > maxs) s = maxs;
+        if (s > 64) s = 64;
+        if (s > 1) {
+            long long per = (g.K + s - 1) / s;
+            per = (per + bk - 1) / bk * bk;
+            g.splits = (int)((g.K + per - 1) / per);
+            g.k_per_split = per;
+        }
+    }
+}
+
+std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
+    const std::string& n = k.name;
+    const bool is_dot = n == "dot" || n == "dot+add";
+    const bool is_l = n == "dot_vjp_l", is_r = n == "dot_vjp_r";
+    const bool is_ein = n.compare(0, 4, "ein[") == 0;
+    if (!(is_dot || is_l || is_r || is_ein)) return nullptr;
+    const int st = storage_of(k.dtype);
+    if (st < 0 || k.output.ty != k.dtype) return nullptr;
+    for (auto& b : k.inputs)
+        if (b.ty != k.dtype) return nullptr;       // indices or widened parameters: generic
+    const bool epi = n == "dot+add";
+    if ((int)k.inputs.size() != (epi ? 3 : 2)) return nullptr;
+    const BufSpec &x = k.inputs[0], &w = k.inputs[1], &o = k.output;
+    auto p = std::make_unique<GemmPlan>();
+    GemmArgs& g = p->g;
+    g.storage = st;
+    g.batch = 1;
+    g.nbatch = 0;
+    g.bias_div = 1;
+    g.bias_mod = 1;
+    p->name = n;
+    p->storage = st;
+    p->epilogue = epi;
+    p->n_in = (int)k.inputs.size();
+    p->guarded = k.guarded();
+    p->split_bound = parallel_outer(k);
+    if (is_dot) {
+        // x[outer..., I, K] . w[K, J] -> [outer..., I, J]   (Contraction::of, lower.rs:700-711)
+        if (w.dims.size() != 2 || x.dims.size() < 2 || x.dims.back() != w.dims[0]) return nullptr;
+        g.K = w.dims[0];
+        g.N = w.dims[1];
+        g.M = x.numel() / g.K;
+        if (o.numel() != g.M * g.N || o.dims.back() != g.N) return nullptr;
+        g.sa_m = g.K; g.sa_k = 1; g.sb_k = g.N; g.sb_n = 1;
+        p->rows_per_iter = x.dims.size() >= 1 ? g.M / x.dims[0] : 0;
+    } else if (is_l) {
+        // ct[outer..., I, N] . b[J, N]^T -> [outer..., I, J]   (lower.rs:715-726)
+        if (w.dims.size() != 2 || x.dims.size() < 2 || x.dims.back() != w.dims[1]) return nullptr;
+        g.K = w.dims[1];
+        g.N = w.dims[0];
+        g.M = x.numel() / g.K;
+        if (o.numel() != g.M * g.N) return nullptr;
+        g.sa_m = g.K; g.sa_k = 1; g.sb_k = 1; g.sb_n = g.K;
+        p->rows_per_iter = g.M / x.dims[0];
+    } else if (is_r) {
+        // a[lead..., I], ct[lead..., J] -> [I, J], summed over lead   (lower.rs:730-739)
+        if (x.dims.size() < 2 || x.dims.size() != w.dims.size()) return nullptr;
+        for (size_t i = 0; i + 1 < x.dims.size(); ++i)
+            if (x.dims[i] != w.dims[i]) return nullptr;
+        g.M = x.dims.back();
+        g.N = w.dims.back();
+        g.K = prod(x.dims, 0, x.dims.size() - 1);
+        if (o.dims.size() != 2 || o.dims[0] != g.M || o.dims[1] != g.N) return nullptr;
+        g.sa_m = 1; g.sa_k = g.M; g.sb_k = g.N; g.sb_n = 1;
+        p->rows_per_iter = 1;
+    } else {
+        // ein: the roles of the operands' axes from the product's index pattern
+        std::vector<int> v0, v1, vo;
+        if (!product_pattern(k, &v0, &v1, &vo)) return nullptr;
+        if (vo.size() < 2 || v0.size() != x.dims.size() || v1.size() != w.dims.size() || vo.size() != o.dims.size()) return nullptr;
+        for (int v : vo)
+            if (v < 0) return nullptr;
+        const int vi = vo[vo.size() - 2], vj = vo.back();
+        const size_t nouter = vo.size() - 2;
+        int vk = -1;
+        for (int v : v0) {
+            bool in_out = false;
+            for (int u : vo) in_out |= u == v;
+            if (!in_out) {
+                if (vk >= 0 && vk != v) return nullptr;   // one summed axis
+                vk = v;
+            }
+        }
+        if (vk < 0) return nullptr;
+        auto pos = [](const std::vector<int>& v, int var) {
+            int p = -1, c = 0;
+            for (size_t i = 0; i < v.size(); ++i)
+                if (v[i] == var) { p = (int)i; ++c; }
+            return c == 1 ? p : -1;
+        };
+        const auto s0 = x.strides(), s1 = w.strides(), so = o.strides();
+        const int a_i = pos(v0, vi), a_k = pos(v0, vk), b_j = pos(v1, vj), b_k = pos(v1, vk);
+        if (a_i < 0 || a_k < 0 || b_j < 0 || b_k < 0 || pos(v0, vj) >= 0 || pos(v1, vi) >= 0) return nullptr;
+        if (v0.size() != nouter + 2 || v1.size() != nouter + 2) return nullptr;
+        g.M = x.dims[a_i];
+        g.K = x.dims[a_k];
+        g.N = w.dims[b_j];
+        if (w.dims[b_k] != g.K || o.dims[nouter] != g.M || o.dims[nouter + 1] != g.N) return nullptr;
+        g.sa_m = s0[a_i]; g.sa_k = s0[a_k]; g.sb_k = s1[b_k]; g.sb_n = s1[b_j];
+        // outer axes, collapsed where all three operands allow it
+        std::vector<long long> bd, sa, sb, sc;
+        for (size_t q = 0; q < nouter; ++q) {
+            const int pa = pos(v0, vo[q]), pb = pos(v1, vo[q]);
+            if (pa < 0 || pb < 0 || x.dims[pa] != o.dims[q] || w.dims[pb] != o.dims[q]) return nullptr;
+            if (bd.size() > 1 && sa.back() == s0[pa] * o.dims[q] && sb.back() == s1[pb] * o.dims[q] && sc.back() == so[q] * o.dims[q]) {
+                bd.back() *= o.dims[q];
+                sa.back() = s0[pa];
+                sb.back() = s1[pb];
+                sc.back() = so[q];
+            } else {
+                bd.push_back(o.dims[q]);
+                sa.push_back(s0[pa]);
+                sb.push_back(s1[pb]);
+                sc.push_back(so[q]);
+            }
+        }
+        if (bd.size() > 3) return nullptr;
+        g.nbatch = (int)bd.size();
+        for (size_t q = 0; q < bd.size(); ++q) {
+            g.bdim[q] = bd[q];
+            g.sa_b[q] = sa[q];
+            g.sb_b[q] = sb[q];
+            g.sc_b[q] = sc[q];
+            g.batch *= bd[q];
+        }
+        p->split_on_batch = nouter > 0;
+        p->rows_per_iter = nouter > 0 ? 0 : 1;
+    }
+    if (epi) {
+        std::vector<int> m;
+        const BufSpec& b = k.inputs[2];
+        if (!align(b, o, &m)) return nullptr;
+        // supported broadcasts: the bias over the last axis (J), over every axis, or a scalar
+        const size_t r = o.dims.size();
+        if (m.empty()) {
+            g.sbias_m = 0; g.sbias_n = 0;
+        } else if (m.size() == 1 && m[0] == (int)r - 1) {
+            g.sbias_m = 0; g.sbias_n = 1;
+        } else if (m.size() == r) {
+            for (size_t i = 0; i < r; ++i)
+                if (m[i] != (int)i) return nullptr;
+            g.sbias_m = g.N; g.sbias_n = 1; g.bias_mod = g.M;
+        } else {
+            return nullptr;
+        }
+        if (g.bias_mod == 0) g.bias_mod = 1;
+    }
+    g.a_kcontig = g.sa_k == 1;
+    g.b_kcontig = g.sb_k == 1;
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0) return nullptr;
+    plan_tiles(g);
+    if (g.batch > 65535 || g.splits > 65535) return nullptr;
+    return p;
+}
+
+}  // namespace
+
+std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode) {
+    if (mode == PRESK_HIP_FAST) {
+        if (auto p = classify_gemm(k)) return p;
+    }
+    return nullptr;
+}
+
+}  // namespace presk

@@ -1,0 +1,304 @@
+// Device-side storage conversions and f32 transcendentals (gfx950).
+//
+// Included by the hand-written kernels and, as text, by every kernel the
+// generic printer builds with hiprtc, so it uses compiler builtins only.
+// Compile with -ffp-contract=off and correctly rounded f32 division/sqrt:
+// every function below must round each f32 operation where its reference
+// does, for equal bits.
+//
+// Conversions, from the reference's bit recipes:
+//   bf16   crates/presk-rt/src/lib.rs:228-241
+//   f16    crates/presk-rt/src/codes.rs:29-87 (IEEE round to nearest even,
+//          overflow to infinity, a NaN quiet with its top 9 payload bits)
+//   e8m15  crates/presk-rt/src/codes.rs:89-110 (the top 24 bits of the f32)
+//   guard  crates/presk-rt/src/codes.rs:112-136 (a finite value whose
+//          narrowing is an infinity)
+// Transcendentals: the kernel interpreter's (exec.rs:158-170), the `libm`
+// crate 0.2.16 = musl 1.1.22 = fdlibm's f32 method; same reductions,
+// coefficients and operation order as crates/presk-export-c/c/presk_libm.c
+// (expf :1605, logf :1811, expm1f :436, tanhf :1915, erff :2542).
+//
+// Each is checked over every f32 input on the GPU against the reference's
+// compiled C (tests/test_gpu_scalar.py, digests in tests/golden/digests.json).
+#pragma once
+
+#define PK_DEV __device__ __forceinline__
+
+PK_DEV unsigned pk_bits(float x) { return __builtin_bit_cast(unsigned, x); }
+PK_DEV float pk_float(unsigned b) { return __builtin_bit_cast(float, b); }
+
+// ---- bf16 ---------------------------------------------------------------------
+PK_DEV float pk_bf16_to_f32(unsigned short h) { return pk_float((unsigned)h << 16); }
+PK_DEV unsigned short pk_f32_to_bf16(float x) {
+    unsigned b = pk_bits(x);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((b >> 16) | 0x0040u);
+    return (unsigned short)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+// ---- binary16 -----------------------------------------------------------------
+PK_DEV float pk_f16_to_f32(unsigned short c) {
+    unsigned sign = (unsigned)(c & 0x8000u) << 16, field = (c >> 10) & 0x1fu, frac = c & 0x3ffu, mag;
+    if (field == 0x1fu) mag = frac == 0 ? 0x7f800000u : (0x7fc00000u | (frac << 13));
+    else if (field == 0) mag = pk_bits((float)frac * 5.9604644775390625e-8f);   // frac * 2^-24, exact
+    else mag = ((field + 112u) << 23) | (frac << 13);
+    return pk_float(sign | mag);
+}
+PK_DEV unsigned short pk_f32_to_f16(float x) {
+    unsigned b = pk_bits(x), sign = (b >> 16) & 0x8000u, a = b & 0x7fffffffu, code;
+    if (a > 0x7f800000u) code = 0x7e00u | ((a >> 13) & 0x1ffu);          // NaN, quiet
+    else if (a >= 0x477ff000u) code = 0x7c00u;                           // rounds past 65504: inf
+    else if (a >= 0x38800000u) {                                          // normal binary16
+        unsigned r = a - 0x38000000u;                                     // rebias 127 -> 15
+        code = (r + 0xfffu + ((r >> 13) & 1u)) >> 13;
+    } else {                                                              // subnormal or zero:
+        code = (unsigned)__builtin_rintf(pk_float(a) * 16777216.0f);      // |x| / 2^-24, to even
+    }
+    return (unsigned short)(sign | code);
+}
+PK_DEV bool pk_overflows_f16(float x) {
+    unsigned a = pk_bits(x) & 0x7fffffffu;
+    return a >= 0x477ff000u && a < 0x7f800000u;
+}
+
+// ---- e8m15: 3 bytes, little-endian, the f32's top 24 bits ---------------------
+PK_DEV float pk_e8m15_to_f32(unsigned c) { return pk_float(c << 8); }
+PK_DEV unsigned pk_f32_to_e8m15(float x) {
+    unsigned b = pk_bits(x);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 8) | 0x4000u;
+    return (b + 0x7fu + ((b >> 8) & 1u)) >> 8;
+}
+PK_DEV bool pk_overflows_e8m15(float x) {
+    unsigned a = pk_bits(x) & 0x7fffffffu;
+    return a >= 0x7f7fff80u && a < 0x7f800000u;
+}
+PK_DEV unsigned pk_ld24(const unsigned char* p, long long e) {
+    return (unsigned)p[3 * e] | ((unsigned)p[3 * e + 1] << 8) | ((unsigned)p[3 * e + 2] << 16);
+}
+PK_DEV void pk_st24(unsigned char* p, long long e, unsigned c) {
+    p[3 * e] = (unsigned char)c;
+    p[3 * e + 1] = (unsigned char)(c >> 8);
+    p[3 * e + 2] = (unsigned char)(c >> 16);
+}
+
+// Rust's `f as i64`: saturating, NaN to zero.
+PK_DEV long long pk_i64(double x) {
+    if (x != x) return 0;
+    if (x >= 9223372036854775807.0) return 9223372036854775807LL;
+    if (x <= -9223372036854775808.0) return (-9223372036854775807LL - 1);
+    return (long long)x;
+}
+
+// ---- f32 transcendentals ---------------------------------------------------------
+PK_DEV float pk_ldexpf(float y, int n) {
+    if (n > 127) {
+        y *= 0x1p127f;
+        n -= 127;
+        if (n > 127) {
+            y *= 0x1p127f;
+            n -= 127;
+            if (n > 127) n = 127;
+        }
+    } else if (n < -126) {
+        y *= 0x1p-102f;
+        n += 102;
+        if (n < -126) {
+            y *= 0x1p-102f;
+            n += 102;
+            if (n < -126) n = -126;
+        }
+    }
+    return y * pk_float((unsigned)(0x7f + n) << 23);
+}
+
+__device__ __noinline__ float pk_expf(float x) {
+    const float ln2_hi = 6.9314575195e-1f, ln2_lo = 1.4286067653e-6f, inv_ln2 = 1.4426950216e+0f;
+    const float p1 = 1.6666625440e-1f, p2 = -2.7667332906e-3f;
+    unsigned ax = pk_bits(x);
+    const int neg = (int)(ax >> 31);
+    ax &= 0x7fffffffu;
+    if (ax >= 0x42aeac50u) {
+        if (ax > 0x7f800000u) return x;
+        if (ax >= 0x42b17218u && !neg) return x * 0x1p127f;
+        if (neg && ax >= 0x42cff1b5u) return 0.0f;
+    }
+    float hi, lo;
+    int k;
+    if (ax > 0x3eb17218u) {
+        if (ax > 0x3f851592u) k = (int)(inv_ln2 * x + (neg ? -0.5f : 0.5f));
+        else k = 1 - neg - neg;
+        hi = x - (float)k * ln2_hi;
+        lo = (float)k * ln2_lo;
+        x = hi - lo;
+    } else if (ax > 0x39000000u) {
+        k = 0;
+        hi = x;
+        lo = 0.0f;
+    } else {
+        return 1.0f + x;
+    }
+    const float xx = x * x;
+    const float c = x - xx * (p1 + xx * p2);
+    const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+    return k == 0 ? y : pk_ldexpf(y, k);
+}
+
+__device__ __noinline__ float pk_logf(float x) {
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
+    const float lg1 = 0xaaaaaa.0p-24f, lg2 = 0xccce13.0p-25f, lg3 = 0x91e9ee.0p-25f, lg4 = 0xf89e26.0p-26f;
+    unsigned ix = pk_bits(x);
+    int k = 0;
+    if (ix < 0x00800000u || (ix >> 31)) {
+        if ((ix << 1) == 0) return -1.0f / (x * x);
+        if (ix >> 31) return (x - x) / 0.0f;
+        k -= 25;
+        x *= 0x1p25f;
+        ix = pk_bits(x);
+    } else if (ix >= 0x7f800000u) {
+        return x;
+    } else if (ix == 0x3f800000u) {
+        return 0.0f;
+    }
+    ix += 0x3f800000u - 0x3f3504f3u;
+    k += (int)(ix >> 23) - 0x7f;
+    ix = (ix & 0x007fffffu) + 0x3f3504f3u;
+    x = pk_float(ix);
+    const float f = x - 1.0f;
+    const float s = f / (2.0f + f);
+    const float z = s * s;
+    const float w = z * z;
+    const float t1 = w * (lg2 + w * lg4);
+    const float t2 = z * (lg1 + w * lg3);
+    const float r = t2 + t1;
+    const float hfsq = 0.5f * f * f;
+    const float dk = (float)k;
+    return s * (hfsq + r) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
+}
+
+__device__ __noinline__ float pk_expm1f(float x) {
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, inv_ln2 = 1.4426950216e+00f;
+    const float q1 = -3.3333212137e-2f, q2 = 1.5807170421e-3f;
+    const unsigned ux = pk_bits(x), ax = ux & 0x7fffffffu;
+    const int neg = (int)(ux >> 31);
+    float hi, lo, c = 0.0f, t;
+    int k;
+    if (ax >= 0x4195b844u) {
+        if (ax > 0x7f800000u) return x;
+        if (neg) return -1.0f;
+        if (ax > 0x42b17217u) return x * 0x1p127f;
+    }
+    if (ax > 0x3eb17218u) {
+        if (ax < 0x3f851592u) {
+            if (!neg) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+            else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+        } else {
+            k = (int)(inv_ln2 * x + (neg ? -0.5f : 0.5f));
+            t = (float)k;
+            hi = x - t * ln2_hi;
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (ax < 0x33000000u) {
+        return x;
+    } else {
+        k = 0;
+    }
+    const float hfx = 0.5f * x;
+    const float hxs = x * hfx;
+    const float r1 = 1.0f + hxs * (q1 + hxs * q2);
+    t = 3.0f - r1 * hfx;
+    float e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = x * (e - c) - c;
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return 1.0f + 2.0f * (x - e);
+    }
+    const float twopk = pk_float((unsigned)(0x7f + k) << 23);
+    float y;
+    if (k < 0 || k > 56) {
+        y = x - e + 1.0f;
+        if (k == 128) y = y * 2.0f * 0x1p127f;
+        else y = y * twopk;
+        return y - 1.0f;
+    }
+    const float twomk = pk_float((unsigned)(0x7f - k) << 23);
+    if (k < 23) y = (x - e + (1.0f - twomk)) * twopk;
+    else y = (x - (e + twomk) + 1.0f) * twopk;
+    return y;
+}
+
+__device__ __noinline__ float pk_tanhf(float x) {
+    const unsigned ux = pk_bits(x);
+    const int neg = (int)(ux >> 31);
+    const unsigned w = ux & 0x7fffffffu;
+    x = pk_float(w);
+    float t;
+    if (w > 0x3f0c9f54u) {
+        if (w > 0x41200000u) t = 1.0f + 0.0f / x;
+        else { t = pk_expm1f(2.0f * x); t = 1.0f - 2.0f / (t + 2.0f); }
+    } else if (w > 0x3e82c578u) {
+        t = pk_expm1f(2.0f * x);
+        t = t / (t + 2.0f);
+    } else if (w >= 0x00800000u) {
+        t = pk_expm1f(-2.0f * x);
+        t = -t / (t + 2.0f);
+    } else {
+        t = x;
+    }
+    return neg ? -t : t;
+}
+
+PK_DEV float pk_erf_mid(float x) {
+    const float erx = 8.4506291151e-01f;
+    const float a0 = -2.3621185683e-03f, a1 = 4.1485610604e-01f, a2 = -3.7220788002e-01f, a3 = 3.1834661961e-01f,
+                a4 = -1.1089469492e-01f, a5 = 3.5478305072e-02f, a6 = -2.1663755178e-03f;
+    const float b1 = 1.0642088205e-01f, b2 = 5.4039794207e-01f, b3 = 7.1828655899e-02f, b4 = 1.2617121637e-01f,
+                b5 = 1.3637083583e-02f, b6 = 1.1984500103e-02f;
+    const float s = __builtin_fabsf(x) - 1.0f;
+    const float p = a0 + s * (a1 + s * (a2 + s * (a3 + s * (a4 + s * (a5 + s * a6)))));
+    const float q = 1.0f + s * (b1 + s * (b2 + s * (b3 + s * (b4 + s * (b5 + s * b6)))));
+    return 1.0f - erx - p / q;
+}
+
+PK_DEV float pk_erfc_tail(unsigned ax, float x) {
+    if (ax < 0x3fa00000u) return pk_erf_mid(x);
+    x = __builtin_fabsf(x);
+    const float s = 1.0f / (x * x);
+    float r, q;
+    if (ax < 0x4036db6du) {
+        r = -9.8649440333e-03f + s * (-6.9385856390e-01f + s * (-1.0558626175e+01f + s * (-6.2375331879e+01f +
+            s * (-1.6239666748e+02f + s * (-1.8460508728e+02f + s * (-8.1287437439e+01f + s * -9.8143291473e+00f))))));
+        q = 1.0f + s * (1.9651271820e+01f + s * (1.3765776062e+02f + s * (4.3456588745e+02f + s * (6.4538726807e+02f +
+            s * (4.2900814819e+02f + s * (1.0863500214e+02f + s * (6.5702495575e+00f + s * -6.0424413532e-02f)))))));
+    } else {
+        r = -9.8649431020e-03f + s * (-7.9928326607e-01f + s * (-1.7757955551e+01f + s * (-1.6063638306e+02f +
+            s * (-6.3756646729e+02f + s * (-1.0250950928e+03f + s * -4.8351919556e+02f)))));
+        q = 1.0f + s * (3.0338060379e+01f + s * (3.2579251099e+02f + s * (1.5367296143e+03f + s * (3.1998581543e+03f +
+            s * (2.5530502930e+03f + s * (4.7452853394e+02f + s * -2.2440952301e+01f))))));
+    }
+    const float z = pk_float(pk_bits(x) & 0xffffe000u);
+    return pk_expf(-z * z - 0.5625f) * pk_expf((z - x) * (z + x) + r / q) / x;
+}
+
+__device__ __noinline__ float pk_erff(float x) {
+    const float efx8 = 1.0270333290e+00f;
+    unsigned ax = pk_bits(x);
+    const int neg = (int)(ax >> 31);
+    ax &= 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (float)(1 - 2 * neg) + 1.0f / x;
+    if (ax < 0x3f580000u) {
+        if (ax < 0x31800000u) return 0.125f * (8.0f * x + efx8 * x);
+        const float z = x * x;
+        const float r = 1.2837916613e-01f + z * (-3.2504209876e-01f + z * (-2.8481749818e-02f + z * (-5.7702702470e-03f + z * -2.3763017452e-05f)));
+        const float s = 1.0f + z * (3.9791721106e-01f + z * (6.5022252500e-02f + z * (5.0813062117e-03f + z * (1.3249473704e-04f + z * -3.9602282413e-06f))));
+        const float y = r / s;
+        return x + x * y;
+    }
+    float y;
+    if (ax < 0x40c00000u) y = 1.0f - pk_erfc_tail(ax, x);
+    else y = 1.0f - 0x1p-120f;
+    return neg ? -y : y;
+}

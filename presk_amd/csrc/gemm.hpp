@@ -1,0 +1,37 @@
+// The MFMA contraction kernel's launch description (gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace presk {
+
+enum Storage { kF32 = 0, kBF16 = 1, kF16 = 2 };
+
+struct GemmArgs {
+    const void* A;        // operand 0, element (b, m, k) at A + batch + m*sa_m + k*sa_k
+    const void* B;        // operand 1, element (b, k, n) at B + batch + k*sb_k + n*sb_n
+    const void* bias;     // the epilogue's operand or null
+    void* C;              // output, row-major [batch][M][N]
+    float* work;          // split-K partials [splits][M][N] (splits > 1)
+    unsigned* flag;       // overflow guard (f16 output) or null
+    long long M, N, K;
+    long long sa_m, sa_k, sb_k, sb_n;
+    int nbatch;                     // batch axes (outer axes of an `ein`), at most 3
+    long long bdim[3], sa_b[3], sb_b[3], sc_b[3];
+    long long batch;                // product of bdim
+    // bias element of (m, n): ((m / bias_div) % bias_mod) * sbias_m + n * sbias_n
+    long long bias_div, bias_mod, sbias_m, sbias_n;
+    int storage;                    // Storage
+    bool a_kcontig, b_kcontig;      // sa_k == 1 / sb_k == 1
+    bool a_vec, b_vec;              // 16-byte vector loads are aligned
+    int splits;
+    long long k_per_split;
+    int tiles_m, tiles_n;
+};
+
+hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream);
+int gemm_block_k(int storage);
+int gemm_tile_m();
+int gemm_tile_n();
+
+}  // namespace presk

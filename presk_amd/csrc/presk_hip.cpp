@@ -1,0 +1,357 @@
+// The C ABI of include/presk_hip.h: compile (text -> hand-written class or
+// generic printed kernel), run (one KernelFn call on a stream), device memory.
+#include "presk_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <mutex>
+#include <sstream>
+#include <unordered_map>
+
+#include "executor.hpp"
+
+namespace presk {
+
+namespace {
+
+thread_local std::string g_error;
+int g_device = -1;
+std::mutex g_mu;
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(PRESK_HIP_ERR, std::string("E10001: ") + what + ": " + hipGetErrorString(e));
+}
+
+const char kDevfmt[] =
+#include "_devfmt.inc"
+    ;
+
+uint64_t fnv1a(const std::string& s) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+std::string cache_dir() {
+    const char* env = std::getenv("PRESK_HIP_CACHE");
+    if (env && *env) return env;
+    const char* home = std::getenv("HOME");
+    std::string base = home && *home ? std::string(home) + "/.cache" : "/tmp";
+    return base + "/presk-hip";
+}
+
+}  // namespace
+
+bool build_code_object(const std::string& src, std::vector<char>* code, std::string* err) {
+    static std::unordered_map<uint64_t, std::vector<char>> memo;
+    static const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                                 "-fno-gpu-flush-denormals-to-zero", "-fhip-fp32-correctly-rounded-divide-sqrt",
+                                 "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+    const int nopts = sizeof(opts) / sizeof(opts[0]);
+    std::string key_text = src + kDevfmt;
+    for (int i = 0; i < nopts; ++i) key_text += opts[i];
+    const uint64_t key = fnv1a(key_text);
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        auto it = memo.find(key);
+        if (it != memo.end()) { *code = it->second; return true; }
+    }
+    char name[32];
+    std::snprintf(name, sizeof name, "%016llx.co", (unsigned long long)key);
+    const std::string dir = cache_dir(), path = dir + "/" + name;
+    {
+        std::ifstream f(path, std::ios::binary);
+        if (f) {
+            std::vector<char> data((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+            if (!data.empty()) {
+                std::lock_guard<std::mutex> lock(g_mu);
+                memo[key] = data;
+                *code = std::move(data);
+                return true;
+            }
+        }
+    }
+    hiprtcProgram prog;
+    const char* headers[] = {kDevfmt};
+    const char* names[] = {"devfmt.hpp"};
+    if (hiprtcCreateProgram(&prog, src.c_str(), "presk_kernel.hip", 1, headers, names) != HIPRTC_SUCCESS) {
+        *err = "E10001: hiprtcCreateProgram failed";
+        return false;
+    }
+    hiprtcResult r = hiprtcCompileProgram(prog, nopts, opts);
+    if (r != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n, '\0');
+        if (n) hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        *err = "E10001: hiprtc: " + log.substr(0, 2000);
+        return false;
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(prog, &n);
+    std::vector<char> data(n);
+    hiprtcGetCode(prog, data.data());
+    hiprtcDestroyProgram(&prog);
+    // best-effort disk cache, written atomically
+    ::mkdir(dir.c_str(), 0755);
+    std::string tmp = path + ".tmp" + std::to_string(::getpid());
+    {
+        std::ofstream f(tmp, std::ios::binary);
+        if (f) f.write(data.data(), (std::streamsize)data.size());
+    }
+    std::rename(tmp.c_str(), path.c_str());
+    std::lock_guard<std::mutex> lock(g_mu);
+    memo[key] = data;
+    *code = std::move(data);
+    return true;
+}
+
+double kernel_bytes(const Kernel& k) {
+    double q = 0;
+    for (size_t b = 0; b <= k.inputs.size(); ++b) {
+        const BufSpec& s = k.buf((int)b);
+        q += (double)s.numel() * ty_bytes(s.ty);
+    }
+    return q;
+}
+
+double kernel_flops(const Kernel& k) {
+    // 2 * numel(out) * K, K the summed length: 2*prod(outer)*I*J*K of a
+    // contraction nest (crates/presk-kernel/src/lower.rs:695-784)
+    const std::string& n = k.name;
+    double K = 0;
+    auto prod = [](const std::vector<int64_t>& d, size_t from, size_t to) {
+        double p = 1;
+        for (size_t i = from; i < to && i < d.size(); ++i) p *= (double)d[i];
+        return p;
+    };
+    if ((n == "dot" || n == "dot+add") && k.inputs.size() >= 2 && !k.inputs[0].dims.empty()) {
+        K = (double)k.inputs[0].dims.back();
+    } else if ((n == "dot_vjp_l" || n == "dot_vjp_l+add") && k.inputs.size() >= 2) {
+        K = prod(k.inputs[1].dims, 1, k.inputs[1].dims.size());
+    } else if ((n == "dot_vjp_r" || n == "dot_vjp_r+add") && k.inputs.size() >= 2 && !k.inputs[0].dims.empty()) {
+        K = prod(k.inputs[0].dims, 0, k.inputs[0].dims.size() - 1);
+    } else if (n.compare(0, 4, "ein[") == 0 && k.inputs.size() >= 2) {
+        K = 1;
+        for (size_t a = 0; a < k.inputs[0].dims.size(); ++a) {
+            const std::string& nm = k.inputs[0].names[a];
+            bool out_axis = false;
+            for (auto& o : k.output.names) out_axis |= (!nm.empty() && o == nm);
+            if (!out_axis) K *= (double)k.inputs[0].dims[a];
+        }
+    }
+    return 2.0 * (double)k.output.numel() * K;
+}
+
+}  // namespace presk
+
+using namespace presk;
+
+struct presk_hip_kernel {
+    std::unique_ptr<Kernel> k;
+    std::unique_ptr<ClassPlan> plan;
+    Generated gen;
+    std::vector<char> code;
+    mutable hipModule_t module = nullptr;
+    mutable std::vector<hipFunction_t> fns;
+    int mode = PRESK_HIP_EXACT;
+};
+
+extern "C" {
+
+const char* presk_hip_last_error(void) { return g_error.c_str(); }
+
+int presk_hip_init(int device) {
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    g_device = device;
+    return PRESK_HIP_OK;
+}
+
+int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, presk_hip_kernel** out) {
+    if (!text || !out) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    std::string err;
+    auto k = parse_kernel(text, dtype ? dtype : "", lanes, &err);
+    if (!k) {
+        bool refused = err.compare(0, 5, "E7005") == 0;
+        return fail(refused ? PRESK_HIP_REFUSED : PRESK_HIP_ERR, (refused ? "" : "E10001: ") + err);
+    }
+    if (!k->arith.empty())
+        return fail(PRESK_HIP_REFUSED, "E7005: the kernel `" + k->name + "` computes in " + k->arith +
+                                           ", which only the kernel interpreter emulates");
+    auto h = std::make_unique<presk_hip_kernel>();
+    h->mode = mode;
+    h->plan = classify(*k, mode);
+    if (!h->plan) {
+        if (!generate_hip(*k, &h->gen, &err)) return fail(err.compare(0, 5, "E7005") == 0 ? PRESK_HIP_REFUSED : PRESK_HIP_ERR, err);
+        if (!build_code_object(h->gen.src, &h->code, &err)) return fail(PRESK_HIP_ERR, err);
+    }
+    h->k = std::move(k);
+    *out = h.release();
+    return PRESK_HIP_OK;
+}
+
+int presk_hip_run(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int64_t hi, void* stream) {
+    if (!h || !bufs) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    hipStream_t s = (hipStream_t)stream;
+    if (h->plan) {
+        hipError_t e = h->plan->launch(bufs, lo, hi, s);
+        return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
+    }
+    if (!h->module) {
+        hipError_t e = hipModuleLoadData(&h->module, h->code.data());
+        if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
+        for (auto& ph : h->gen.phases) {
+            hipFunction_t f;
+            e = hipModuleGetFunction(&f, h->module, ph.fn.c_str());
+            if (e != hipSuccess) return hip_fail(e, "hipModuleGetFunction");
+            h->fns.push_back(f);
+        }
+    }
+    const Kernel& k = *h->k;
+    PhaseArgs args{};
+    const int nb = (int)k.inputs.size() + 1;
+    for (int i = 0; i < nb; ++i) args.buf[i] = bufs[i];
+    args.flag = k.guarded() ? (unsigned*)bufs[nb] : nullptr;
+    for (size_t p = 0; p < h->gen.phases.size(); ++p) {
+        const Phase& ph = h->gen.phases[p];
+        long long total = 1;
+        args.lo = 0;
+        args.hi = 0;
+        if (!ph.bounds.empty()) {
+            long long n0 = ph.bounds[0];
+            if (ph.split) {
+                if (lo < 0 || hi > n0 || lo > hi) return fail(PRESK_HIP_ERR, "E10001: split range outside the loop");
+                args.lo = lo;
+                args.hi = hi;
+                n0 = hi - lo;
+            }
+            total = n0;
+            for (size_t d = 1; d < ph.bounds.size(); ++d) total *= ph.bounds[d];
+        }
+        if (total == 0) continue;
+        const unsigned block = ph.bounds.empty() ? 1 : 256;
+        const long long grid = (total + block - 1) / block;
+        if (grid > 0x7fffffffLL) return fail(PRESK_HIP_ERR, "E10001: launch too large");
+        void* params[] = {&args};
+        hipError_t e = hipModuleLaunchKernel(h->fns[p], (unsigned)grid, 1, 1, block, 1, 1, 0, s, params, nullptr);
+        if (e != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel");
+    }
+    return PRESK_HIP_OK;
+}
+
+int presk_hip_kernel_info(const presk_hip_kernel* h, presk_hip_info* info) {
+    if (!h || !info) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    std::memset(info, 0, sizeof *info);
+    std::snprintf(info->kind, sizeof info->kind, "%s", h->plan ? h->plan->kind() : "generic");
+    std::snprintf(info->order, sizeof info->order, "%s", h->plan ? h->plan->order().c_str() : "sequential");
+    info->guarded = h->k->guarded();
+    info->n_inputs = (int32_t)h->k->inputs.size();
+    info->split_bound = parallel_outer(*h->k);
+    info->flops = kernel_flops(*h->k);
+    info->bytes = kernel_bytes(*h->k);
+    return PRESK_HIP_OK;
+}
+
+int64_t presk_hip_kernel_text(const presk_hip_kernel* h, char* buf, size_t cap) {
+    if (!h) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    std::string t = show_kernel(*h->k);
+    if (buf && cap) std::snprintf(buf, cap, "%s", t.c_str());
+    return (int64_t)t.size();
+}
+
+void presk_hip_release(presk_hip_kernel* h) {
+    if (!h) return;
+    if (h->module) hipModuleUnload(h->module);
+    delete h;
+}
+
+int presk_hip_alloc(size_t bytes, void** dev) {
+    hipError_t e = hipMalloc(dev, bytes ? bytes : 1);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipMalloc");
+}
+int presk_hip_free(void* dev) {
+    hipError_t e = hipFree(dev);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipFree");
+}
+int presk_hip_h2d(void* dev, const void* host, size_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipMemcpy h2d");
+}
+int presk_hip_d2h(void* host, const void* dev, size_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipMemcpy d2h");
+}
+int presk_hip_memset(void* dev, int value, size_t bytes, void* stream) {
+    hipError_t e = hipMemsetAsync(dev, value, bytes, (hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipMemsetAsync");
+}
+int presk_hip_sync(void* stream) {
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipStreamSynchronize");
+}
+int presk_hip_stream_create(void** stream) {
+    hipError_t e = hipStreamCreate((hipStream_t*)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipStreamCreate");
+}
+int presk_hip_stream_destroy(void* stream) {
+    hipError_t e = hipStreamDestroy((hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipStreamDestroy");
+}
+
+int presk_hip_time(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int64_t hi, void* stream, int warmup, int reps,
+                   double* ms_per_launch) {
+    if (reps <= 0 || !ms_per_launch) return fail(PRESK_HIP_ERR, "E10001: bad timing arguments");
+    for (int i = 0; i < warmup; ++i) {
+        int rc = presk_hip_run(h, bufs, lo, hi, stream);
+        if (rc) return rc;
+    }
+    hipEvent_t a, b;
+    hipEventCreate(&a);
+    hipEventCreate(&b);
+    hipEventRecord(a, (hipStream_t)stream);
+    for (int i = 0; i < reps; ++i) {
+        int rc = presk_hip_run(h, bufs, lo, hi, stream);
+        if (rc) {
+            hipEventDestroy(a);
+            hipEventDestroy(b);
+            return rc;
+        }
+    }
+    hipEventRecord(b, (hipStream_t)stream);
+    hipError_t e = hipEventSynchronize(b);
+    float ms = 0;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    if (e != hipSuccess) return hip_fail(e, "hipEvent timing");
+    *ms_per_launch = (double)ms / reps;
+    return PRESK_HIP_OK;
+}
+
+int presk_hip_scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
+    hipError_t e = scalar_digest(fn, lo, hi, digest);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "scalar digest");
+}
+
+}  // extern "C"

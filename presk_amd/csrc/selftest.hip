@@ -1,0 +1,116 @@
+// Device self-test of the scalar functions (presk_hip_scalar_digest): the
+// digest oracle/digest.c defines, computed with the executor's own device
+// conversions and transcendentals over a block of their domain.
+#include <hip/hip_runtime.h>
+
+#include "devfmt.hpp"
+#include "executor.hpp"
+
+namespace presk {
+
+namespace {
+
+__device__ __forceinline__ unsigned long long mix64(unsigned long long z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// the f64 sample of the narrowings from f64 (oracle/digest.c pd_sample_f64_bits)
+__device__ __forceinline__ unsigned long long sample_f64_bits(unsigned long long i) {
+    unsigned long long r = mix64(i * 0x9e3779b97f4a7c15ull + 0x632be59bd9b4e019ull);
+    if ((i & 3) == 3) return r;
+    unsigned long long e = 1023 - 40 + (r >> 52) % 65, frac = r & ((1ull << 52) - 1);
+    if ((i & 3) == 2) frac &= ~((1ull << 28) - 1) | (r >> 40 & 1);
+    return (r & (1ull << 63)) | (e << 52) | frac;
+}
+
+// A double's narrowing as a native kernel performs it: the value is an f32
+// when a kernel stores it, so these go through the f32 of the double only
+// when it is exact; otherwise the f64 path of codes.rs:29-56, written here
+// for the self-test alone.
+__device__ unsigned long long narrow64(unsigned long long b, unsigned t, unsigned w) {
+    const unsigned long long sign = (b >> 63) << (t + w), inf = ((1ull << w) - 1) << t, mag = b & ~(1ull << 63);
+    if (mag > (0x7ffull << 52)) return sign | inf | (1ull << (t - 1)) | ((mag >> (52 - t)) & ((1ull << (t - 1)) - 1));
+    const int field = (int)(mag >> 52);
+    if (field == 0) return sign;
+    const unsigned long long sig = (mag & ((1ull << 52) - 1)) | (1ull << 52);
+    const int e = field - 1023, bias = (1 << (w - 1)) - 1, emin = 1 - bias;
+    const int shift = 52 - (int)t + (emin - e > 0 ? emin - e : 0);
+    unsigned long long q = 0;
+    if (shift <= 63) {
+        const unsigned long long low = sig & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+        q = sig >> shift;
+        if (low > half || (low == half && (q & 1))) q += 1;
+    }
+    unsigned long long code = e >= emin ? ((unsigned long long)(e + bias - 1) << t) + q : q;
+    return sign | (code > inf ? inf : code);
+}
+
+__device__ unsigned eval1(int fn, unsigned long long i) {
+    const float x = pk_float((unsigned)i);
+    switch (fn) {
+        case 0: return pk_bits(pk_expf(x));
+        case 1: return pk_bits(pk_logf(x));
+        case 2: return pk_bits(pk_tanhf(x));
+        case 3: return pk_bits(pk_erff(x));
+        case 10: return pk_f32_to_bf16(x);
+        case 11: return pk_f32_to_f16(x);
+        case 12: return pk_f32_to_e8m15(x);
+        case 20: return pk_bits(pk_bf16_to_f32((unsigned short)i));
+        case 21: return pk_bits(pk_f16_to_f32((unsigned short)i));
+        case 22: return pk_bits(pk_e8m15_to_f32((unsigned)i));
+        case 30: return (unsigned)narrow64(sample_f64_bits(i), 10, 5);
+        case 31: return (unsigned)narrow64(sample_f64_bits(i), 15, 8);
+        case 32: return pk_overflows_f16(x) ? 1u : 0u;
+        case 33: return pk_overflows_e8m15(x) ? 1u : 0u;
+        default: return 0;
+    }
+}
+
+__global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long lo, unsigned long long n,
+                                                     unsigned long long per_thread, unsigned long long* out) {
+    const unsigned long long t = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
+    unsigned long long acc = 0;
+    const unsigned long long first = t * per_thread;
+    for (unsigned long long j = 0; j < per_thread; ++j) {
+        const unsigned long long k = first + j;
+        if (k >= n) break;
+        const unsigned long long i = lo + k;
+        acc += mix64((i << 32) | eval1(fn, i));
+    }
+    // wave then block sum (order-free: the digest is a sum mod 2^64)
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+    __shared__ unsigned long long part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(out, part[0] + part[1] + part[2] + part[3]);
+}
+
+}  // namespace
+
+hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
+    const int known[] = {0, 1, 2, 3, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
+    bool ok = false;
+    for (int f : known) ok |= f == fn;
+    if (!ok || hi < lo) return hipErrorInvalidValue;
+    const unsigned long long n = hi - lo;
+    unsigned long long* d = nullptr;
+    hipError_t e = hipMalloc(&d, sizeof *d);
+    if (e != hipSuccess) return e;
+    e = hipMemset(d, 0, sizeof *d);
+    const unsigned long long per_thread = 64, threads = (n + per_thread - 1) / per_thread;
+    const unsigned long long blocks = (threads + 255) / 256;
+    if (e == hipSuccess && n) {
+        digest_kernel<<<dim3((unsigned)blocks), dim3(256)>>>(fn, lo, n, per_thread, d);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    unsigned long long h = 0;
+    if (e == hipSuccess) e = hipMemcpy(&h, d, sizeof h, hipMemcpyDeviceToHost);
+    hipFree(d);
+    *digest = h;
+    return e;
+}
+
+}  // namespace presk

@@ -1,0 +1,130 @@
+"""A sequence of kernel launches over device-resident buffers: the host's
+`call_fn` walk (crates/presk-kernel/src/host.rs:887-1039) reduced to what a
+fixed entry needs once its nests are known -- each `let` one launch
+(`KernelBackend::launch`, host.rs:742-868), every buffer allocated once and
+kept in HBM, no copy between launches, the overflow flags read once at the
+end of the call.
+
+`Program` holds the launches; `Buffers` the named device allocations.  The
+measured configurations (presk_amd/configs.py) are built from it.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import hip
+from . import lower as L
+
+BYTES = {"f64": 8, "f32": 4, "bf16": 2, "f16": 2, "e8m15": 3, "i64": 8}
+
+
+def numel(axes) -> int:
+    n = 1
+    for a in axes:
+        n *= a.len
+    return n
+
+
+class Buffers:
+    """Named device buffers, each with its storage type and element count."""
+
+    def __init__(self):
+        self.dev: dict = {}
+        self.meta: dict = {}
+
+    def alloc(self, name: str, ty: str, count: int) -> hip.DeviceBuffer:
+        if name in self.dev:
+            ty0, c0 = self.meta[name]
+            if (ty0, c0) != (ty, count):
+                raise ValueError(f"buffer {name} redeclared as {ty}[{count}] (was {ty0}[{c0}])")
+            return self.dev[name]
+        b = hip.DeviceBuffer(max(count, 1) * BYTES[ty])
+        self.dev[name] = b
+        self.meta[name] = (ty, count)
+        return b
+
+    def upload(self, name: str, storage: np.ndarray):
+        self.dev[name].upload(storage)
+
+    def download(self, name: str) -> np.ndarray:
+        ty, count = self.meta[name]
+        if ty == "e8m15":
+            return self.dev[name].download(np.uint8, 3 * count)
+        dt = {"f64": np.float64, "f32": np.float32, "bf16": np.uint16, "f16": np.uint16, "i64": np.int64}[ty]
+        return self.dev[name].download(dt, count)
+
+
+class Launch:
+    def __init__(self, low: L.Lowered, ins: list, out: str):
+        self.low, self.ins, self.out = low, ins, out
+        self.compiled: hip.Compiled | None = None
+        self.table = None
+
+
+class Program:
+    """Launches in order on one stream; `run` enqueues them all."""
+
+    def __init__(self, name: str, mode: int = hip.FAST):
+        self.name = name
+        self.mode = mode
+        self.launches: list = []
+        self.bufs = Buffers()
+        self._flag = None
+
+    def add(self, low: L.Lowered, ins: list, out: str) -> str:
+        """Appends one launch of `low` reading buffers `ins`, writing `out`."""
+        self.launches.append(Launch(low, list(ins), out))
+        return out
+
+    def compile(self, cache: dict | None = None):
+        hip.init(0)
+        cache = {} if cache is None else cache
+        self._flag = hip.DeviceBuffer(4)
+        for ln in self.launches:
+            key = (ln.low.text, ln.low.dtype, ln.low.lanes, self.mode)
+            c = cache.get(key)
+            if c is None:
+                c = hip.Compiled(ln.low.text, ln.low.dtype, ln.low.lanes, self.mode)
+                cache[key] = c
+            ln.compiled = c
+        return self
+
+    def declare(self, name: str, ty: str, count: int):
+        return self.bufs.alloc(name, ty, count)
+
+    def prepare(self):
+        for ln in self.launches:
+            c = ln.compiled
+            ty = ln.low.dtype if ln.low.out_kind == "real" else "i64"
+            self.bufs.alloc(ln.out, ty, numel(ln.low.out_axes))
+            ptrs = [self.bufs.dev[n].ptr for n in ln.ins] + [self.bufs.dev[ln.out].ptr]
+            if c.guarded:
+                ptrs.append(self._flag.ptr)
+            ln.table = (ctypes.c_void_p * len(ptrs))(*ptrs)
+        self._flag.zero()
+        return self
+
+    def run(self, stream=None):
+        lib = hip.lib()
+        for ln in self.launches:
+            c = ln.compiled
+            rc = lib.presk_hip_run(c.handle, ln.table, 0, max(c.split_bound, 0), stream)
+            if rc:
+                hip.check(rc)
+
+    def check_overflow(self):
+        """E7007 when any narrowing store of the call overflowed."""
+        if int(self._flag.download(np.uint32, 1)[0]):
+            raise hip.HipError(hip.OVERFLOW, f"E7007: a store of `{self.name}` overflowed its storage type")
+
+    def kernel_times(self, reps: int = 10, stream=None) -> list:
+        """Mean ms of each launch alone (HIP events on the launch stream)."""
+        out = []
+        for ln in self.launches:
+            ms = ctypes.c_double()
+            c = ln.compiled
+            hip.check(hip.lib().presk_hip_time(c.handle, ln.table, 0, max(c.split_bound, 0), stream, 2, reps, ctypes.byref(ms)))
+            out.append((ln, ms.value))
+        return out

@@ -1,0 +1,88 @@
+"""The MFMA contraction class (FAST mode) against the oracle's sequential
+sums, within the band the reassociation allows.
+
+The executor's order is declared (its kernel info names it): MFMA tiles with
+f32 accumulation, k-blocks in increasing order, split-K partials added in
+split order.  Two f32 orders of one sum of K terms differ by at most
+2*gamma_K*sum|x_k w_k| (gamma_K = K u / (1 - K u), u = 2^-24); a narrow
+storage type adds at most one unit in its last place per store, of the sum
+(at most sum|x_k w_k|) and of the result.  Every element must be within that bound, and the bulk far inside it
+(median error below 1/64 of the bound), so a misplaced operand or a lost
+k-block cannot pass."""
+import numpy as np
+import pytest
+
+from oracle import cexec
+from presk_amd import hip
+from presk_amd import lower as L
+from tests import fmt
+
+pytestmark = pytest.mark.gpu
+A, O = L.ax, L.Operand
+
+ULP = {"f32": 2.0 ** -23, "bf16": 2.0 ** -7, "f16": 2.0 ** -10}
+
+
+def cases():
+    out = []
+    for dt in ("f32", "bf16", "f16"):
+        x = O(A(("batch", 3), ("seq", 200), 96))
+        w = O(A(96, 136))
+        d = L.dot([x, w], dt)
+        out.append((f"dot-{dt}", d, None))
+        out.append((f"dot+add-{dt}", L.dot([x, w, O(A(136))], dt, epilogue=(True, d.out_axes)), None))
+        out.append((f"dot_vjp_l-{dt}", L.dot_vjp_l([O(A(("batch", 2), ("seq", 130), 200)), O(A(72, 200))], dt), None))
+        out.append((f"dot_vjp_r-split-{dt}", L.dot_vjp_r([O(A(("batch", 4), ("seq", 600), 96)), O(A(("batch", 4), ("seq", 600), 80))], dt), None))
+        q = O(A(("batch", 2), ("heads", 3), ("seq", 40), ("hd", 64)))
+        kk = O(A(("batch", 2), ("heads", 3), ("seq2", 40), ("hd", 64)))
+        s = O(A(("batch", 2), ("heads", 3), ("seq", 40), ("seq2", 40)))
+        out.append((f"ein_qk-{dt}", L.ein([q, kk], [["batch", "heads", "seq", "hd"], ["batch", "heads", "seq2", "hd"]], ["batch", "heads", "seq", "seq2"], dt), None))
+        out.append((f"ein_av-{dt}", L.ein([s, kk], [["batch", "heads", "seq", "seq2"], ["batch", "heads", "seq2", "hd"]], ["batch", "heads", "seq", "hd"], dt), None))
+    # a K that is not a multiple of the k-block, M and N below one tile
+    out.append(("dot-odd-bf16", L.dot([O(A(("batch", 5), 77)), O(A(77, 24))], "bf16"), None))
+    return out
+
+
+def abs_products(low, vals):
+    """sum_k |x_k w_k| per output element, in f64, via the oracle on |x|, |w| in f64."""
+    text = low.text.replace(f": {low.dtype}[", ": f64[")
+    absv = [np.abs(v.astype(np.float64)) for v in vals]
+    if low.name.endswith("+add"):
+        absv[2] = np.zeros_like(absv[2])
+    out, _ = cexec.run(text, "f64", [a.ravel() for a in absv], lanes=low.lanes)
+    return out
+
+
+@pytest.fixture(scope="module")
+def ex():
+    return hip.HipExec(0, mode=hip.FAST)
+
+
+@pytest.mark.parametrize("case", cases(), ids=lambda c: c[0])
+def test_fast_contraction_within_band(ex, case):
+    name, low, _ = case
+    print(f"[gemm] {name}", flush=True)
+    from oracle import kernel_text as kt
+    k = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(3)
+    vals = [fmt.roundtrip(rng.standard_normal(b.dims).astype(np.float32), low.dtype) for b in k.inputs]
+    ins = [fmt.encode(v, low.dtype) for v in vals]
+    want, _ = cexec.run(low.text, low.dtype, ins, lanes=low.lanes)
+    nbytes = k.output.numel * hip.STORAGE_BYTES[low.dtype]
+    out = hip.DeviceBuffer(nbytes)
+    out.upload(np.full(nbytes, 0xFF, np.uint8))
+    c = ex.run(low.text, low.dtype, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+    assert c.kind == "gemm", c.kind
+    got = fmt.decode(out.download(want.dtype), low.dtype).astype(np.float64)
+    ref = fmt.decode(want, low.dtype).astype(np.float64)
+    K = c.flops / (2 * k.output.numel)
+    u = 2.0 ** -24
+    gamma = K * u / (1 - K * u)
+    S = abs_products(low, vals)
+    # a narrow store of the sum can differ by one unit of |sum| <= S, which a
+    # bias that cancels carries into a smaller result
+    bound = 2 * gamma * S + ULP[low.dtype] * (S + 2 * np.maximum(np.abs(ref), np.abs(got))) + 1e-30
+    err = np.abs(got - ref)
+    assert np.all(np.isfinite(got)), f"{name}: unwritten or non-finite outputs"
+    assert np.all(err <= bound), f"{name} [{c.order}]: {np.count_nonzero(err > bound)} elements outside the band"
+    assert np.median(err / bound) < 1 / 64, f"{name}: median error {np.median(err / bound):.3g} of the band"

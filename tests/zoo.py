@@ -1,0 +1,112 @@
+"""A zoo of the nests the configurations launch, at small shapes, with seeded
+inputs: the cases every parity test runs through the oracle and the device."""
+from __future__ import annotations
+
+import numpy as np
+
+from presk_amd import lower as L
+from tests import fmt
+
+A = L.ax
+O = L.Operand
+
+
+def _gpt_like(dt, B=2, T=8, D=16, H=2, V=11):
+    hd = D // H
+    x = O(A(("batch", B), ("seq", T), ("model", D)))
+    w = O(A(D, D))
+    w4 = O(A(D, 4 * D))
+    h4 = O(A(("batch", B), ("seq", T), 4 * D))
+    b = O(A(D))
+    q = O(A(("batch", B), ("heads", H), ("seq", T), ("hd", hd)))
+    k = O(A(("batch", B), ("heads", H), ("seq2", T), ("hd", hd)))
+    s = O(A(("batch", B), ("heads", H), ("seq", T), ("seq2", T)))
+    mask = O(A(("seq", T), ("seq2", T)), "idx")
+    ids = O(A(("batch", B), ("seq", T)), "idx")
+    tok = O(A(("vocab", V), ("model", D)))
+    logits = O(A(("batch", B), ("seq", T), ("vocab", V)))
+    rows = O(A(("batch", B), ("seq", T)))
+    d = L.dot([x, w], dt)
+    cases = {
+        "dot": d,
+        "dot+add": L.dot([x, w, b], dt, epilogue=(True, d.out_axes)),
+        "dot_vjp_l": L.dot_vjp_l([O(A(("batch", B), ("seq", T), 4 * D)), O(A(D, 4 * D))], dt),
+        "dot_vjp_r": L.dot_vjp_r([x, h4], dt),
+        "ein_scores": L.ein([q, k], [["batch", "heads", "seq", "hd"], ["batch", "heads", "seq2", "hd"]], ["batch", "heads", "seq", "seq2"], dt),
+        "ein_values": L.ein([s, O(A(("batch", B), ("heads", H), ("seq2", T), ("hd", hd)))],
+                            [["batch", "heads", "seq", "seq2"], ["batch", "heads", "seq2", "hd"]], ["batch", "heads", "seq", "hd"], dt),
+        "softmax": L.softmax("seq2", [s], dt),
+        "softmax2": L.softmax_two_pass("seq2", [s], dt),
+        "masked_softmax": L.masked_softmax("seq2", [s, mask], dt),
+        "masked_softmax2": L.masked_softmax("seq2", [s, mask], dt, two_passes=True),
+        "mean": L.reduce_axis("mean", "model", [x], dt),
+        "sum": L.reduce_axis("sum", "model", [x], dt),
+        "mean_all": L.reduce_all("mean_all", [rows], dt),
+        "sum_squares": L.sum_squares([w4], dt),
+        "gelu": L.unary("gelu", [h4], dt),
+        "gelu_deriv": L.unary("gelu_deriv", [h4], dt),
+        "tanh": L.unary("tanh", [x], dt),
+        "sub": L.elementwise_binary("sub", [x, O(A(("batch", B), ("seq", T)))], dt),
+        "max": L.elementwise_binary("max", [x, b], dt),
+        "layernorm_tail": L.fused([("sub", [("in", 0), ("in", 1)]), ("add", [("in", 2), ("in", 3)]), ("sqrt", [("step", 1)]),
+                                   ("div", [("step", 0), ("step", 2)]), ("mul", [("step", 3), ("in", 4)]), ("add", [("step", 4), ("in", 5)])],
+                                  [x, O(A(("batch", B), ("seq", T))), O(A(("batch", B), ("seq", T))), O([]), b, b], x.axes, dt),
+        "embed": L.embed([tok, ids], dt),
+        "embed_vjp": L.embed_vjp([tok, ids, x], dt),
+        "cross_entropy": L.cross_entropy([logits, ids], dt),
+        "cross_entropy_vjp": L.cross_entropy_vjp([logits, ids, rows], dt),
+        "sum_to": L.sum_to([x, b], dt),
+        "mean_vjp": L.mean_vjp("model", [rows, x], dt),
+        "split_heads": L.split_heads(H, hd, [x], dt),
+        "merge_heads": L.merge_heads(H, hd, [q], dt),
+        "causal_mask": L.causal_mask("seq", T, dt),
+        "positions": L.positions("seq", T, dt),
+    }
+    return cases
+
+
+def cases(dtypes=("f32", "bf16", "f16", "e8m15")):
+    """[(id, Lowered)] over the zoo and the storage types."""
+    out = []
+    for dt in dtypes:
+        for name, low in _gpt_like(dt).items():
+            if dt != "f32" and name in ("causal_mask", "positions"):
+                continue
+            out.append((f"{name}-{dt}", low))
+    # row-wise dot (J % 8 != 0 in f32) and the chunked order
+    x = O(A(("batch", 5), 7))
+    out.append(("dot_rowwise-f32", L.dot([x, O(A(7, 3))], "f32")))
+    out.append(("dot+add_rowwise-f32", L.dot([x, O(A(7, 3)), O(A(3))], "f32", epilogue=(True, A(("batch", 5), 3)))))
+    out.append(("dot_chunked4-f32", L.dot([O(A(("batch", 5), 10)), O(A(10, 8))], "f32", order=("chunked", 4))))
+    return out
+
+
+def inputs(low: L.Lowered, seed: int = 0, scale: float = 1.0):
+    """Seeded inputs for a kernel: storage arrays (host) in input order."""
+    from oracle import kernel_text as kt
+    k = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(seed)
+    arrs = []
+    for b in k.inputs:
+        if b.ty == "i64":
+            hi = 2
+            if "vocab" in (b.names or []):
+                hi = 2
+            # an index input: bounded by the axis it indexes in the kernel's use
+            hi = _index_bound(low, k, len(arrs))
+            arrs.append(rng.integers(0, hi, size=b.numel, dtype=np.int64))
+        else:
+            v = (rng.standard_normal(b.dims) * scale).astype(np.float32)
+            arrs.append(fmt.encode(v, b.ty))
+    return arrs
+
+
+def _index_bound(low, k, i):
+    name = low.name
+    if name in ("embed", "embed_vjp"):
+        return k.inputs[0].dims[0]
+    if name.startswith("cross_entropy"):
+        return k.inputs[0].dims[-1]
+    if name.startswith("softmax"):
+        return 2
+    return 2
