@@ -140,21 +140,23 @@ struct GemmPlan : ClassPlan {
                 a.C = (char*)a.C + m0 * a.N * esz;
                 a.M = (hi - lo) * rows_per_iter;
                 a.tiles_m = (int)((a.M + gemm_tile_m() - 1) / gemm_tile_m());
-                if (a.bias && a.sbias_m) a.bias = (const char*)a.bias + ((m0 / a.bias_div) % a.bias_mod) * a.sbias_m * esz;
+                if (a.bias && a.bias_kind == 2) a.bias = (const char*)a.bias + m0 * a.N * esz;
                 if (a.splits > 1) return hipErrorInvalidValue;  // a partial range of a split-K plan
             }
         }
-        // 16-byte loads need aligned rows
+        // the clamped 16-byte loads need whole aligned vectors along the
+        // loaded axis: k when it is contiguous, else the rows
         const int vec = storage == kF32 ? 4 : 8;
-        auto aligned = [&](const void* p, long long row_stride, const long long* bs) {
+        auto aligned = [&](const void* p, bool kcontig, long long rows, long long other_stride, const long long* bs) {
             if ((uintptr_t)p % 16) return false;
-            if (row_stride % vec) return false;
+            if (other_stride % vec) return false;
+            if ((kcontig ? a.K : rows) % vec) return false;
             for (int d = 0; d < a.nbatch; ++d)
                 if (bs[d] % vec) return false;
             return true;
         };
-        a.a_vec = aligned(a.A, a.a_kcontig ? a.sa_m : a.sa_k, a.sa_b);
-        a.b_vec = aligned(a.B, a.b_kcontig ? a.sb_n : a.sb_k, a.sb_b);
+        a.a_vec = aligned(a.A, a.a_kcontig, a.M, a.a_kcontig ? a.sa_m : a.sa_k, a.sa_b);
+        a.b_vec = aligned(a.B, a.b_kcontig, a.N, a.b_kcontig ? a.sb_n : a.sb_k, a.sb_b);
         if (a.splits > 1) {
             const size_t need = (size_t)a.splits * a.M * a.N;
             if (need > work_floats) {
@@ -223,8 +225,6 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     g.storage = st;
     g.batch = 1;
     g.nbatch = 0;
-    g.bias_div = 1;
-    g.bias_mod = 1;
     p->name = n;
     p->storage = st;
     p->epilogue = epi;
@@ -330,23 +330,26 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
         // supported broadcasts: the bias over the last axis (J), over every axis, or a scalar
         const size_t r = o.dims.size();
         if (m.empty()) {
-            g.sbias_m = 0; g.sbias_n = 0;
+            g.bias_kind = 3;
         } else if (m.size() == 1 && m[0] == (int)r - 1) {
-            g.sbias_m = 0; g.sbias_n = 1;
+            g.bias_kind = 1;
         } else if (m.size() == r) {
             for (size_t i = 0; i < r; ++i)
                 if (m[i] != (int)i) return nullptr;
-            g.sbias_m = g.N; g.sbias_n = 1; g.bias_mod = g.M;
+            g.bias_kind = 2;
         } else {
             return nullptr;
         }
-        if (g.bias_mod == 0) g.bias_mod = 1;
     }
     g.a_kcontig = g.sa_k == 1;
     g.b_kcontig = g.sb_k == 1;
     if (g.M <= 0 || g.N <= 0 || g.K <= 0) return nullptr;
     plan_tiles(g);
     if (g.batch > 65535 || g.splits > 65535) return nullptr;
+    // 32-bit element offsets inside one batch entry
+    const double lim = 2147483647.0;
+    if ((double)g.M * g.N > lim || (double)g.M * g.K > lim || (double)g.K * g.N > lim ||
+        (double)x.numel() > lim || (double)w.numel() > lim) return nullptr;
     return p;
 }
 

@@ -9,14 +9,16 @@
 //
 // Order (declared, not the interpreter's index order): each 16x16 output tile
 // accumulates on MFMA in f32 -- v_mfma_f32_16x16x32_{bf16,f16} for 16-bit
-// storage (the products of two 16-bit values are exact in f32), and
+// storage (the product of two 16-bit values is exact in f32), and
 // v_mfma_f32_16x16x4_f32 for f32 storage -- over k-blocks of 64 (32 for f32)
-// in increasing k, and, when K is split across workgroups, the split partial
-// sums are added in increasing split order by a second kernel (deterministic).
+// in increasing k; when K is split across workgroups, the partial sums are
+// added in increasing split order by a second kernel (deterministic).
 //
-// Tile: 128x128 per workgroup of 256 threads (4 waves of 64, each 64x64 =
-// 4x4 MFMA tiles), operands staged through LDS k-contiguous; an operand whose
-// contiguous axis is m or n is transposed on its way into LDS.
+// Workgroup: 256 threads (4 waves as 2x2), tile (2*WM*16) x (2*WN*16), each
+// wave WM x WN MFMA tiles of 16x16.  Operands are staged through LDS
+// k-contiguous, double-buffered (one barrier per k-block); an operand whose
+// contiguous axis is m or n is transposed in registers on its way into LDS
+// (8-byte LDS writes, consecutive lanes along k).
 #include <hip/hip_runtime.h>
 
 #include "devfmt.hpp"
@@ -32,26 +34,24 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, NT = 256;
+constexpr int NT = 256;
 
 // Storage traits: S = element in memory and LDS, BK = k-block, VEC = elements
-// per 16-byte global load.
+// per 16-byte global load, KSTEP = k per MFMA, KPL = k per lane per MFMA.
 template <int ST> struct St;
 template <> struct St<kF32> {
     typedef float S;
-    static constexpr int BK = 32, VEC = 4, PAD = 4;
-    static __device__ __forceinline__ float widen(float x) { return x; }
+    typedef f32x4 V;
+    typedef float Frag;
+    static constexpr int BK = 32, VEC = 4, PAD = 4, KSTEP = 4, KPL = 1;
 };
 template <> struct St<kBF16> {
     typedef unsigned short S;
-    static constexpr int BK = 64, VEC = 8, PAD = 8;
-    static __device__ __forceinline__ float widen(unsigned short x) { return pk_bf16_to_f32(x); }
+    typedef u16x8 V;
+    typedef u16x8 Frag;
+    static constexpr int BK = 64, VEC = 8, PAD = 8, KSTEP = 32, KPL = 8;
 };
-template <> struct St<kF16> {
-    typedef unsigned short S;
-    static constexpr int BK = 64, VEC = 8, PAD = 8;
-    static __device__ __forceinline__ float widen(unsigned short x) { return pk_f16_to_f32(x); }
-};
+template <> struct St<kF16> : St<kBF16> {};
 
 __device__ __forceinline__ long long batch_offset(const GemmArgs& g, long long b, const long long* strides) {
     long long off = 0;
@@ -63,65 +63,88 @@ __device__ __forceinline__ long long batch_offset(const GemmArgs& g, long long b
     return off;
 }
 
-// One operand's tile (rows x BK) staged into LDS as tile[row][k], k contiguous.
+// One operand's tile (ROWS x BK) staged into LDS as tile[row][k], k contiguous.
 // `rs`/`ks` are the operand's element strides along its row axis (m or n) and k.
-template <int ST, bool KCONTIG>
+template <int ST, bool KCONTIG, int ROWS>
 struct Loader {
     typedef typename St<ST>::S S;
+    typedef typename St<ST>::V V;
     static constexpr int BK = St<ST>::BK, VEC = St<ST>::VEC, LD = BK + St<ST>::PAD;
-    // registers: KCONTIG: 4 rounds of one 16-byte vector; else VEC rows x 4 k
-    static constexpr int REGS = KCONTIG ? 4 * VEC : 4 * VEC;
-    S r[REGS];
+    // KCONTIG: BK/VEC threads per row -> ROWS/(NT/(BK/VEC)) rounds of one vector.
+    // else: VEC rows x 4 k per thread block; (BK/4) k-quads x (ROWS/VEC) row
+    // blocks over NT threads -> rounds.
+    static constexpr int TPR = BK / VEC, RPR = NT / TPR, ROUNDS_K = ROWS / RPR;
+    static constexpr int KQ = BK / 4, RB = ROWS / VEC, ROUNDS_T = (KQ * RB) / NT;
+    static constexpr int NV = KCONTIG ? ROUNDS_K : 4 * ROUNDS_T;
+    V r[NV];
+    bool kin[NV];   // the vector's k lies below K; applied when it is stored, so
+                    // that no use of the loaded registers waits for the loads
+                    // before the MFMAs of the current k-block have been issued
 
-    __device__ __forceinline__ void load(const S* __restrict__ p, long long rows, long long K, long long rs, long long ks,
-                                         long long row0, long long k0, bool vec_ok) {
+    // Loads are unconditional 16-byte vectors from clamped addresses: a row
+    // past the operand repeats its last row (the results of such rows are
+    // never stored), a k past K reads k = K-1 and is zeroed by a select, so
+    // the hot loop has no branches.  Needs the vector axis (k, or the rows
+    // when the operand is transposed) to be a multiple of VEC and aligned;
+    // the launcher checks, and otherwise uses the element-wise variant.
+    __device__ __forceinline__ void load(const S* __restrict__ p, int rows, int K, int rs, int ks, int row0, int k0) {
         const int t = threadIdx.x;
         if (KCONTIG) {
-            // BK/VEC threads per row, NT/(BK/VEC) rows per round, 4 rounds
-            constexpr int TPR = BK / VEC, RPR = NT / TPR;
             const int kc = (t % TPR) * VEC;
+            const int k = k0 + kc;
+            const bool in = k < K;
+            const int kcl = in ? k : K - VEC;
 #pragma unroll
-            for (int round = 0; round < 4; ++round) {
-                const long long row = row0 + (t / TPR) + round * RPR;
-                const long long k = k0 + kc;
-                const S* src = p + row * rs + k;
-                if (row < rows && vec_ok && k + VEC <= K) {
-                    if (VEC == 8) {
-                        u16x8 v = *(const u16x8*)src;
-#pragma unroll
-                        for (int j = 0; j < VEC; ++j) r[round * VEC + j] = (S)v[j];
-                    } else {
-                        f32x4 v = *(const f32x4*)src;
-#pragma unroll
-                        for (int j = 0; j < VEC; ++j) r[round * VEC + j] = (S)v[j];
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < VEC; ++j) r[round * VEC + j] = (row < rows && k + j < K) ? src[j * ks] : (S)0;
-                }
+            for (int q = 0; q < ROUNDS_K; ++q) {
+                int row = row0 + (t / TPR) + q * RPR;
+                row = row < rows ? row : rows - 1;
+                r[q] = *(const V*)(p + (long long)row * rs + kcl);
+                kin[q] = in;
             }
         } else {
-            // the row axis contiguous: each thread a VEC(rows) x 4(k) block
-            constexpr int TPK = BM / VEC;   // threads along rows per k-quad
-            const long long row = row0 + (t % TPK) * VEC;
-            const long long kq = k0 + (t / TPK) * 4;
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const long long k = kq + kk;
-                const S* src = p + k * ks + row * rs;
-                if (k < K && vec_ok && row + VEC <= rows) {
-                    if (VEC == 8) {
-                        u16x8 v = *(const u16x8*)src;
+            for (int q = 0; q < ROUNDS_T; ++q) {
+                const int u = t + q * NT;
+                int row = row0 + (u / KQ) * VEC;
+                row = row + VEC <= rows ? row : rows - VEC;
+                const int kq = k0 + (u % KQ) * 4;
 #pragma unroll
-                        for (int j = 0; j < VEC; ++j) r[kk * VEC + j] = (S)v[j];
-                    } else {
-                        f32x4 v = *(const f32x4*)src;
+                for (int kk = 0; kk < 4; ++kk) {
+                    const int k = kq + kk;
+                    const bool in = k < K;
+                    r[q * 4 + kk] = *(const V*)(p + (long long)(in ? k : K - 1) * ks + row);
+                    kin[q * 4 + kk] = in;
+                }
+            }
+        }
+    }
+
+    // The element-wise variant for operands whose vector axis is ragged or
+    // unaligned: every element bounds-checked.
+    __device__ __forceinline__ void load_checked(const S* __restrict__ p, int rows, int K, int rs, int ks, int row0, int k0) {
+        const int t = threadIdx.x;
+        if (KCONTIG) {
+            const int kc = (t % TPR) * VEC;
 #pragma unroll
-                        for (int j = 0; j < VEC; ++j) r[kk * VEC + j] = (S)v[j];
+            for (int q = 0; q < ROUNDS_K; ++q) {
+                const int row = row0 + (t / TPR) + q * RPR;
+                for (int j = 0; j < VEC; ++j) {
+                    const int k = k0 + kc + j;
+                    r[q][j] = (row < rows && k < K) ? p[(long long)row * rs + (long long)k * ks] : (S)0;
+                }
+                kin[q] = true;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < ROUNDS_T; ++q) {
+                const int u = t + q * NT;
+                const int row = row0 + (u / KQ) * VEC, kq = k0 + (u % KQ) * 4;
+                for (int kk = 0; kk < 4; ++kk) {
+                    for (int j = 0; j < VEC; ++j) {
+                        const int k = kq + kk;
+                        r[q * 4 + kk][j] = (k < K && row + j < rows) ? p[(long long)k * ks + (long long)(row + j) * rs] : (S)0;
                     }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < VEC; ++j) r[kk * VEC + j] = (k < K && row + j < rows) ? src[j * rs] : (S)0;
+                    kin[q * 4 + kk] = true;
                 }
             }
         }
@@ -130,43 +153,53 @@ struct Loader {
     __device__ __forceinline__ void store(S* tile) const {
         const int t = threadIdx.x;
         if (KCONTIG) {
-            constexpr int TPR = BK / VEC, RPR = NT / TPR;
             const int kc = (t % TPR) * VEC;
 #pragma unroll
-            for (int round = 0; round < 4; ++round) {
-                S* dst = tile + ((t / TPR) + round * RPR) * LD + kc;
-#pragma unroll
-                for (int j = 0; j < VEC; ++j) dst[j] = r[round * VEC + j];
-            }
+            for (int q = 0; q < ROUNDS_K; ++q) *(V*)(tile + ((t / TPR) + q * RPR) * LD + kc) = kin[q] ? r[q] : V{};
         } else {
-            constexpr int TPK = BM / VEC;
-            const int row = (t % TPK) * VEC, kq = (t / TPK) * 4;
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                S* dst = tile + (row + j) * LD + kq;
+            for (int q = 0; q < ROUNDS_T; ++q) {
+                const int u = t + q * NT;
+                const int row = (u / KQ) * VEC, kq = (u % KQ) * 4;
+                V z[4];
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) dst[kk] = r[kk * VEC + j];
+                for (int kk = 0; kk < 4; ++kk) z[kk] = kin[q * 4 + kk] ? r[q * 4 + kk] : V{};
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    if (VEC == 8) {
+                        u16x4 w;
+                        w[0] = (unsigned short)z[0][j];
+                        w[1] = (unsigned short)z[1][j];
+                        w[2] = (unsigned short)z[2][j];
+                        w[3] = (unsigned short)z[3][j];
+                        *(u16x4*)(tile + (row + j) * LD + kq) = w;
+                    } else {
+                        f32x4 w;
+                        w[0] = (float)z[0][j];
+                        w[1] = (float)z[1][j];
+                        w[2] = (float)z[2][j];
+                        w[3] = (float)z[3][j];
+                        *(f32x4*)(tile + (row + j) * LD + kq) = w;
+                    }
+                }
             }
         }
     }
 };
 
 template <int ST>
-__device__ __forceinline__ f32x4 mfma_step(const typename St<ST>::S* a, const typename St<ST>::S* b, f32x4 acc);
-
+__device__ __forceinline__ f32x4 mfma(typename St<ST>::Frag a, typename St<ST>::Frag b, f32x4 acc);
 template <>
-__device__ __forceinline__ f32x4 mfma_step<kBF16>(const unsigned short* a, const unsigned short* b, f32x4 acc) {
-    u16x8 va = *(const u16x8*)a, vb = *(const u16x8*)b;
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, va), __builtin_bit_cast(bf16x8, vb), acc, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma<kBF16>(u16x8 a, u16x8 b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
 }
 template <>
-__device__ __forceinline__ f32x4 mfma_step<kF16>(const unsigned short* a, const unsigned short* b, f32x4 acc) {
-    u16x8 va = *(const u16x8*)a, vb = *(const u16x8*)b;
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, va), __builtin_bit_cast(f16x8, vb), acc, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma<kF16>(u16x8 a, u16x8 b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
 }
 template <>
-__device__ __forceinline__ f32x4 mfma_step<kF32>(const float* a, const float* b, f32x4 acc) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(*a, *b, acc, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma<kF32>(float a, float b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
 }
 
 // The storage-type store of an output element with the epilogue: f32 storage
@@ -195,22 +228,24 @@ __device__ __forceinline__ void store_out(void* C, long long off, float sum, boo
 template <int ST>
 __device__ __forceinline__ float load_bias(const void* p, long long off) {
     if (ST == kF32) return ((const float*)p)[off];
-    return St<ST>::widen(((const unsigned short*)p)[off]);
+    if (ST == kBF16) return pk_bf16_to_f32(((const unsigned short*)p)[off]);
+    return pk_f16_to_f32(((const unsigned short*)p)[off]);
 }
 
-template <int ST, bool AK, bool BK_>
+template <int ST, bool AK, bool BK_, int WM, int WN, bool SAFE>
 __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     typedef typename St<ST>::S S;
-    constexpr int BK = St<ST>::BK, LD = BK + St<ST>::PAD;
-    __shared__ __attribute__((aligned(16))) S As[BM * LD];
-    __shared__ __attribute__((aligned(16))) S Bs[BN * LD];
+    typedef typename St<ST>::Frag Frag;
+    constexpr int BK = St<ST>::BK, LD = BK + St<ST>::PAD, KSTEP = St<ST>::KSTEP, KPL = St<ST>::KPL;
+    constexpr int BM = 2 * WM * 16, BN = 2 * WN * 16;
+    __shared__ __attribute__((aligned(16))) S As[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) S Bs[2][BN * LD];
 
     // tile order: blocks of one XCD (block id mod 8) take consecutive tiles,
     // and tiles go row-group by row-group so that concurrent tiles share A rows
     const long long tiles = (long long)g.tiles_m * g.tiles_n;
     long long bid = blockIdx.x;
-    const long long per_xcd = (tiles + 7) / 8;
-    if (tiles >= 64 && tiles % 8 == 0) bid = (bid % 8) * per_xcd + bid / 8;
+    if (tiles >= 64 && tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
     constexpr long long GROUP = 8;
     const long long group_size = GROUP * g.tiles_n;
     const long long grp = bid / group_size;
@@ -224,83 +259,84 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
 
     const S* A = (const S*)g.A + batch_offset(g, batch, g.sa_b);
     const S* B = (const S*)g.B + batch_offset(g, batch, g.sb_b);
-    const long long kbeg = (long long)split * g.k_per_split;
-    long long kend = kbeg + g.k_per_split;
-    if (kend > g.K) kend = g.K;
+    const int kbeg = split * (int)g.k_per_split;
+    int kend = kbeg + (int)g.k_per_split;
+    if (kend > (int)g.K) kend = (int)g.K;
+    const int M = (int)g.M, N = (int)g.N;
+    const int sa_m = (int)g.sa_m, sa_k = (int)g.sa_k, sb_k = (int)g.sb_k, sb_n = (int)g.sb_n;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    f32x4 acc[4][4];
+    const int wm = (wave >> 1) * (WM * 16), wn = (wave & 1) * (WN * 16);
+    f32x4 acc[WM][WN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < WN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    Loader<ST, AK> la;
-    Loader<ST, BK_> lb;
-    const long long nk = (kend - kbeg + BK - 1) / BK;
+    Loader<ST, AK, BM> la;
+    Loader<ST, BK_, BN> lb;
+    const int nk = (kend - kbeg + BK - 1) / BK;
+    auto fetch = [&](int k0) {
+        if (SAFE) {
+            la.load_checked(A, M, kend, sa_m, sa_k, (int)m0, k0);
+            lb.load_checked(B, N, kend, sb_n, sb_k, (int)n0, k0);
+        } else {
+            la.load(A, M, kend, sa_m, sa_k, (int)m0, k0);
+            lb.load(B, N, kend, sb_n, sb_k, (int)n0, k0);
+        }
+    };
     if (nk > 0) {
-        la.load(A, g.M, kend, g.sa_m, g.sa_k, m0, kbeg, g.a_vec);
-        lb.load(B, g.N, kend, g.sb_n, g.sb_k, n0, kbeg, g.b_vec);
-        la.store(As);
-        lb.store(Bs);
+        fetch(kbeg);
+        la.store(As[0]);
+        lb.store(Bs[0]);
     }
     __syncthreads();
-    for (long long kt = 0; kt < nk; ++kt) {
-        const long long knext = kbeg + (kt + 1) * BK;
-        if (kt + 1 < nk) {
-            la.load(A, g.M, kend, g.sa_m, g.sa_k, m0, knext, g.a_vec);
-            lb.load(B, g.N, kend, g.sb_n, g.sb_k, n0, knext, g.b_vec);
+    const int frow = lane & 15, fk = (lane >> 4) * KPL;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) fetch(kbeg + (kt + 1) * BK);
+        const S* as = As[cur];
+        const S* bs = Bs[cur];
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += KSTEP) {
+            Frag a[WM], b[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) a[i] = *(const Frag*)&as[(wm + i * 16 + frow) * LD + kk + fk];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) b[j] = *(const Frag*)&bs[(wn + j * 16 + frow) * LD + kk + fk];
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
         }
-        if (ST == kF32) {
-#pragma unroll
-            for (int kk = 0; kk < BK; kk += 4) {
-                const int kl = kk + (lane >> 4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = mfma_step<ST>(&As[(wm + i * 16 + (lane & 15)) * LD + kl], &Bs[(wn + j * 16 + (lane & 15)) * LD + kl], acc[i][j]);
-            }
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < BK; kk += 32) {
-                const int kl = kk + (lane >> 4) * 8;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = mfma_step<ST>(&As[(wm + i * 16 + (lane & 15)) * LD + kl], &Bs[(wn + j * 16 + (lane & 15)) * LD + kl], acc[i][j]);
-            }
+        if (kt + 1 < nk) {
+            la.store(As[cur ^ 1]);
+            lb.store(Bs[cur ^ 1]);
         }
         __syncthreads();
-        if (kt + 1 < nk) {
-            la.store(As);
-            lb.store(Bs);
-            __syncthreads();
-        }
     }
 
     // the tile's outputs: lane holds column (lane & 15), rows 4*(lane >> 4) + r
     bool ovf = false;
     const long long cbase = batch_offset(g, batch, g.sc_b);
+    S* C = (S*)g.C + cbase;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < WM; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const long long n = n0 + wn + j * 16 + (lane & 15);
+        for (int j = 0; j < WN; ++j) {
+            const int n = (int)n0 + wn + j * 16 + (lane & 15);
+            if (n >= N) continue;
+            const float bn = g.bias && g.bias_kind == 1 ? load_bias<ST>(g.bias, n) : 0.f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const long long m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
-                if (m < g.M && n < g.N) {
-                    const float v = acc[i][j][r];
-                    if (g.splits > 1) {
-                        g.work[((long long)split * g.M + m) * g.N + n] = v;
-                    } else {
-                        float b = 0.f;
-                        if (g.bias) b = load_bias<ST>(g.bias, ((m / g.bias_div) % g.bias_mod) * g.sbias_m + n * g.sbias_n);
-                        store_out<ST>(g.C, cbase + m * g.N + n, v, g.bias != nullptr, b, ovf);
-                    }
+                const int m = (int)m0 + wm + i * 16 + (lane >> 4) * 4 + r;
+                if (m >= M) continue;
+                const float v = acc[i][j][r];
+                if (g.splits > 1) {
+                    g.work[((long long)split * M + m) * N + n] = v;
+                } else {
+                    const float b = g.bias_kind == 2 ? load_bias<ST>(g.bias, (long long)m * N + n) : g.bias_kind == 3 ? load_bias<ST>(g.bias, 0) : bn;
+                    store_out<ST>(C, (long long)m * N + n, v, g.bias != nullptr, b, ovf);
                 }
             }
         }
@@ -318,19 +354,30 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     for (int p = 1; p < g.splits; ++p) s = s + g.work[(long long)p * g.M * g.N + idx];
     bool ovf = false;
     float b = 0.f;
-    if (g.bias) b = load_bias<ST>(g.bias, ((m / g.bias_div) % g.bias_mod) * g.sbias_m + n * g.sbias_n);
+    if (g.bias_kind == 1) b = load_bias<ST>(g.bias, n);
+    else if (g.bias_kind == 2) b = load_bias<ST>(g.bias, idx);
+    else if (g.bias_kind == 3) b = load_bias<ST>(g.bias, 0);
+    (void)m;
     store_out<ST>(g.C, idx, s, g.bias != nullptr, b, ovf);
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
 
+template <int ST, int WM, int WN, bool SAFE>
+hipError_t launch_shape(const GemmArgs& g, hipStream_t stream) {
+    dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)g.batch, (unsigned)g.splits);
+    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
+    else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
+    else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
+    else gemm_kernel<ST, false, false, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
+    return hipGetLastError();
+}
+
 template <int ST>
 hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
-    dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)g.batch, (unsigned)g.splits);
-    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true><<<grid, NT, 0, stream>>>(g);
-    else if (g.a_kcontig) gemm_kernel<ST, true, false><<<grid, NT, 0, stream>>>(g);
-    else if (g.b_kcontig) gemm_kernel<ST, false, true><<<grid, NT, 0, stream>>>(g);
-    else gemm_kernel<ST, false, false><<<grid, NT, 0, stream>>>(g);
-    hipError_t e = hipGetLastError();
+    // the clamped vector loads need each operand's vector axis (k when it is
+    // contiguous, else the rows) to hold whole aligned vectors
+    const bool fast = g.a_vec && g.b_vec;
+    hipError_t e = fast ? launch_shape<ST, 4, 4, false>(g, stream) : launch_shape<ST, 4, 4, true>(g, stream);
     if (e != hipSuccess || g.splits <= 1) return e;
     const long long n = g.M * g.N;
     split_reduce_kernel<ST><<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(g);
@@ -340,8 +387,8 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
 }  // namespace
 
 int gemm_block_k(int storage) { return storage == kF32 ? St<kF32>::BK : St<kBF16>::BK; }
-int gemm_tile_m() { return BM; }
-int gemm_tile_n() { return BN; }
+int gemm_tile_m() { return 128; }
+int gemm_tile_n() { return 128; }
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream) {
     switch (g.storage) {

@@ -19,11 +19,11 @@ struct GemmArgs {
     int nbatch;                     // batch axes (outer axes of an `ein`), at most 3
     long long bdim[3], sa_b[3], sb_b[3], sc_b[3];
     long long batch;                // product of bdim
-    // bias element of (m, n): ((m / bias_div) % bias_mod) * sbias_m + n * sbias_n
-    long long bias_div, bias_mod, sbias_m, sbias_n;
+    // bias element of (m, n): kind 1 bias[n], 2 bias[m*N + n], 3 bias[0]
+    int bias_kind;
     int storage;                    // Storage
     bool a_kcontig, b_kcontig;      // sa_k == 1 / sb_k == 1
-    bool a_vec, b_vec;              // 16-byte vector loads are aligned
+    bool a_vec, b_vec;              // whole aligned 16-byte vectors along the loaded axis
     int splits;
     long long k_per_split;
     int tiles_m, tiles_n;
