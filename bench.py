@@ -23,37 +23,48 @@ PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}   # MI355X dense MFM
 HBM_GBS = 8000.0
 
 
-def cpu_baseline(workload: str, dtype: str, rows: int, threads: int):
+def workload(name: str, dtype: str, rows=None):
+    """(program, host inputs, tokens per step, contraction flops, config record)
+    of a workload; `rows` shrinks it for the CPU sample."""
+    from presk_amd import configs, gpt
+
+    if name == "mlp":
+        r = rows or 8192
+        p, host, _, flops = configs.mlp(rows=r, dtype=dtype)
+        cfg = {"workload": "config 2: MLP block LN -> Linear 768->3072 -> GELU -> Linear 3072->768 -> residual",
+               "rows": r, "d_model": 768, "hidden": 3072, "storage": dtype, "compute": "f32"}
+        return p, host, r, flops, cfg
+    if name == "linear":
+        r = rows or 4096
+        p, host, _, flops = configs.linear(batch=r, dtype=dtype)
+        cfg = {"workload": "config 1: Linear x.w+b", "batch": r, "in": 1024, "out": 1024, "storage": dtype, "compute": "f32"}
+        return p, host, r, flops, cfg
+    train = name == "gpt-step"
+    s = gpt.COURSE if rows is None else gpt.GptShape(B=max(rows // gpt.COURSE.T, 1))
+    p, b, names = gpt.build(s, dtype, train=train)
+    host = gpt.host_inputs(s)
+    cfg = {"workload": ("config 4: course GPT training step (loss value and gradient of every parameter)" if train
+                        else "config 3: course GPT forward and loss"),
+           "L": s.L, "d_model": s.D, "heads": s.H, "vocab": s.V, "batch": s.B, "seq": s.T,
+           "storage": dtype, "compute": "f32", "launches": len(p.launches), "dropout": 0.0}
+    return p, host, s.B * s.T, gpt.contraction_flops(s, train), cfg
+
+
+def cpu_baseline(name: str, dtype: str, rows: int, threads: int):
     """The oracle (the kernel interpreter's semantics in C, -O3 -march=native,
     the outermost parallel loop split over OpenMP threads as the native
     executor splits it) on a bounded sample of the workload's rows."""
-    import numpy as np
+    from tests import cpu_program
 
-    from oracle import cexec
-    from presk_amd import configs
-
-    if workload == "mlp":
-        p, host, out, _ = configs.mlp(rows=rows, dtype=dtype)
-    else:
-        p, host, out, _ = configs.linear(batch=rows, dtype=dtype)
-    vals = {}
-    for ln in p.launches:
-        for name, (ty, count) in zip(ln.ins, configs._input_specs(ln.low)):
-            if name in host and name not in vals:
-                vals[name] = configs.encode(host[name].reshape(-1)[:count], ty)
-    # compile outside the timed region
-    for ln in p.launches:
-        cexec.compile_kernel(ln.low.text, ln.low.dtype, ln.low.lanes, opt="-O3", native=True)
+    p, host, tokens, _, _ = workload(name, dtype, rows)
+    cpu_program.compile_all(p, native=True, workers=threads)
     best = None
-    for _ in range(2):
+    for _ in range(1 if name.startswith("gpt") else 2):
         t0 = time.perf_counter()
-        env = dict(vals)
-        for ln in p.launches:
-            env[ln.out], _ = cexec.run(ln.low.text, ln.low.dtype, [env[n] for n in ln.ins], lanes=ln.low.lanes,
-                                       threads=threads, native=True)
+        cpu_program.run(p, host, threads=threads, native=True)
         dt = time.perf_counter() - t0
         best = dt if best is None else min(best, dt)
-    return rows / best, best
+    return tokens / best, best, tokens
 
 
 def main():
@@ -61,7 +72,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="mlp", choices=["mlp", "linear"])
+    ap.add_argument("--workload", default="gpt-step", choices=["gpt-step", "gpt-forward", "mlp", "linear"])
     ap.add_argument("--dtype", default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=None)
@@ -71,19 +82,10 @@ def main():
               "multi-GPU sharding is a design (DESIGN.md), not a run.", file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
-
     from presk_amd import configs, hip
 
     dtype = args.dtype or ("bf16" if args.workload == "mlp" else "f32")
-    if args.workload == "mlp":
-        p, host, out, flops = configs.mlp(dtype=dtype)
-        tokens, cfg = 8192, {"workload": "config 2: MLP block LN -> Linear 768->3072 -> GELU -> Linear 3072->768 -> residual",
-                             "rows": 8192, "d_model": 768, "hidden": 3072, "storage": dtype, "compute": "f32"}
-    else:
-        p, host, out, flops = configs.linear(dtype=dtype)
-        tokens, cfg = 4096, {"workload": "config 1: Linear x.w+b", "batch": 4096, "in": 1024, "out": 1024,
-                             "storage": dtype, "compute": "f32"}
+    p, host, tokens, flops, cfg = workload(args.workload, dtype)
     p.compile()
     configs.load_inputs(p, host)
     p.prepare()
@@ -114,7 +116,15 @@ def main():
         roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_GBS, "unit": "GB/s", "frac": round(achieved / HBM_GBS, 4), "traffic": None,
                 "ms_per_launch": round(ms, 5), "algorithmic_bytes": c.bytes}
-    per_kernel = [{"kernel": l.low.name, "kind": l.compiled.kind, "ms": round(m, 5)} for l, m in times]
+    # per nest name: launches and total ms (the step's time by kind of nest)
+    agg = {}
+    for l, m in times:
+        e = agg.setdefault(l.low.name, {"kernel": l.low.name, "kind": l.compiled.kind, "launches": 0, "ms": 0.0})
+        e["launches"] += 1
+        e["ms"] += m
+    per_kernel = sorted(agg.values(), key=lambda e: -e["ms"])[:16]
+    for e in per_kernel:
+        e["ms"] = round(e["ms"], 4)
 
     rec = {"metric": METRIC, "value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
@@ -123,11 +133,12 @@ def main():
            "kernels": per_kernel}
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)
-        rows = args.cpu_rows or (4096 if args.workload == "mlp" else 1024)
-        v, secs = cpu_baseline(args.workload, dtype, rows, threads)
+        rows = args.cpu_rows or {"mlp": 4096, "linear": 1024, "gpt-step": 2048, "gpt-forward": 4096}[args.workload]
+        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads)
         rec["cpu_baseline"] = {"value": round(v, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-                               "sample": f"{rows} of {tokens} rows of the same workload, oracle C restatement "
-                                         f"(-O3 -march=native, OpenMP outer-loop split), best of 2: {secs:.2f} s"}
+                               "sample": f"{n} of {tokens} tokens (rows) of the same workload: the oracle's C restatement of "
+                                         f"the same default-layout nests (-O3 -march=native, -ffp-contract=off, sequential "
+                                         f"sums, the outermost parallel loop split over OpenMP threads): {secs:.2f} s"}
     print(json.dumps(rec), flush=True)
 
 

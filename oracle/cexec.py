@@ -348,12 +348,18 @@ def compile_kernel(text: str, dtype: str, lanes: int = 1, opt: str = "-O2", nati
     os.makedirs(_CACHE, exist_ok=True)
     so = os.path.join(_CACHE, f"k_{key}.so")
     if not os.path.exists(so):
-        c = os.path.join(_CACHE, f"k_{key}.c")
-        with open(c, "w") as f:
+        # unique temporaries: threads of one process may build the same key
+        fd, c = tempfile.mkstemp(suffix=".c", prefix=f"k_{key}_", dir=_CACHE)
+        with os.fdopen(fd, "w") as f:
             f.write(src)
-        tmp = so + f".tmp{os.getpid()}"
-        subprocess.run(["gcc", *flags, "-o", tmp, c, os.path.join(HERE, "libm.c"), "-lm"], check=True, capture_output=True)
-        os.replace(tmp, so)
+        tmp = c[:-2] + ".so.tmp"
+        try:
+            subprocess.run(["gcc", *flags, "-o", tmp, c, os.path.join(HERE, "libm.c"), "-lm"], check=True, capture_output=True)
+            os.replace(tmp, so)
+        finally:
+            for f in (c, tmp):
+                if os.path.exists(f):
+                    os.remove(f)
     lib = ctypes.CDLL(so)
     lib.kern.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int64, ctypes.c_int64]
     lib.run_split.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int64, ctypes.c_int]

@@ -89,22 +89,37 @@ def mlp(rows=8192, d=768, hidden=3072, dtype="bf16", seed=1):
     return p, host, "out", flops
 
 
-INPUT_TYPES = {"eps": None}
+def storage_inputs(p: Program, host: dict) -> dict:
+    """Host values -> each input's storage in its declared type (indices int64)."""
+    env = {}
+    for ln in p.launches:
+        for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
+            if name in host and name not in env:
+                v = host[name]
+                if ty == "i64":
+                    env[name] = np.ascontiguousarray(v, dtype=np.int64).ravel()
+                else:
+                    env[name] = encode(np.asarray(v, np.float32).reshape(-1)[:max(count, 1)], ty)
+    return env
 
 
 def load_inputs(p: Program, host: dict):
     """Declares and uploads every host input in the program's storage type."""
+    specs = {}
     for ln in p.launches:
         for name, spec in zip(ln.ins, _input_specs(ln.low)):
-            if name in host and name not in p.bufs.dev:
-                ty, count = spec
-                p.declare(name, ty, count)
-                p.bufs.upload(name, encode(host[name].reshape(-1)[:count] if count else host[name].reshape(-1)[:1], ty))
+            specs.setdefault(name, spec)
+    for name, arr in storage_inputs(p, host).items():
+        ty, count = specs[name]
+        p.declare(name, ty, max(count, 1))
+        p.bufs.upload(name, arr)
 
 
 def _input_specs(low: L.Lowered):
     """(storage type, element count) of each input, read off the kernel's header."""
     head = low.text.split("\n", 1)[0]
+    if " () -> %" in head:
+        return []
     inner = head[head.index(" (%") + 2: head.index(") -> %")]
     specs, depth, cur = [], 0, ""
     for ch in inner:

@@ -13,6 +13,8 @@
 #include "devfmt.hpp"
 #include "executor.hpp"
 #include "gemm.hpp"
+#include "reduce.hpp"
+#include "rows.hpp"
 #include "presk_hip.h"
 
 namespace presk {
@@ -77,6 +79,10 @@ bool product_pattern(const Kernel& k, std::vector<int>* vars0, std::vector<int>*
             if (x->kind == Expr::Sv && i > 0 && body[i - 1]->kind == Stmt::Set && body[i - 1]->var == x->id &&
                 body[i - 1]->value->kind == Expr::Load && body[i - 1]->value->id == 0)
                 x = body[i - 1]->value;
+            // the generic `ein` term (1 * x0) * x1 (lower.rs:625-630): 1*x0 is x0 exactly
+            if (x->kind == Expr::Bin && x->op == Op::Mul && x->kids[0]->kind == Expr::Num && x->kids[0]->integral &&
+                x->kids[0]->inum == 1)
+                x = x->kids[1];
             if (x->kind != Expr::Load || x->id != 0) continue;
             load0 = x;
             load1 = w;
@@ -106,6 +112,7 @@ struct GemmPlan : ClassPlan {
     bool guarded = false;
     int64_t split_bound = -1;  // the KernelFn split loop's bound
     bool split_on_batch = false;
+    bool swapped = false;          // operand 1 is A (an `ein` whose operand 1 carries I)
     long long rows_per_iter = 0;   // M rows (or batch entries) one outer iteration covers
     mutable float* work = nullptr;
     mutable size_t work_floats = 0;
@@ -119,8 +126,8 @@ struct GemmPlan : ClassPlan {
 
     hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, hipStream_t stream) const override {
         GemmArgs a = g;
-        a.A = bufs[0];
-        a.B = bufs[1];
+        a.A = bufs[swapped ? 1 : 0];
+        a.B = bufs[swapped ? 0 : 1];
         a.bias = epilogue ? bufs[2] : nullptr;
         a.C = bufs[n_in];
         a.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
@@ -285,20 +292,32 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
                 if (v[i] == var) { p = (int)i; ++c; }
             return c == 1 ? p : -1;
         };
-        const auto s0 = x.strides(), s1 = w.strides(), so = o.strides();
-        const int a_i = pos(v0, vi), a_k = pos(v0, vk), b_j = pos(v1, vj), b_k = pos(v1, vk);
-        if (a_i < 0 || a_k < 0 || b_j < 0 || b_k < 0 || pos(v0, vj) >= 0 || pos(v1, vi) >= 0) return nullptr;
-        if (v0.size() != nouter + 2 || v1.size() != nouter + 2) return nullptr;
-        g.M = x.dims[a_i];
-        g.K = x.dims[a_k];
-        g.N = w.dims[b_j];
-        if (w.dims[b_k] != g.K || o.dims[nouter] != g.M || o.dims[nouter + 1] != g.N) return nullptr;
+        // operand roles: A carries I, B carries J; the generic `ein` form may
+        // have them the other way round (the product commutes exactly)
+        const BufSpec* xa = &x;
+        const BufSpec* wb = &w;
+        std::vector<int> va = v0, vb = v1;
+        bool swapped = false;
+        if (pos(v0, vi) < 0 && pos(v1, vi) >= 0 && pos(v0, vj) >= 0) {
+            std::swap(va, vb);
+            std::swap(xa, wb);
+            swapped = true;
+        }
+        p->swapped = swapped;
+        const auto s0 = xa->strides(), s1 = wb->strides(), so = o.strides();
+        const int a_i = pos(va, vi), a_k = pos(va, vk), b_j = pos(vb, vj), b_k = pos(vb, vk);
+        if (a_i < 0 || a_k < 0 || b_j < 0 || b_k < 0 || pos(va, vj) >= 0 || pos(vb, vi) >= 0) return nullptr;
+        if (va.size() != nouter + 2 || vb.size() != nouter + 2) return nullptr;
+        g.M = xa->dims[a_i];
+        g.K = xa->dims[a_k];
+        g.N = wb->dims[b_j];
+        if (wb->dims[b_k] != g.K || o.dims[nouter] != g.M || o.dims[nouter + 1] != g.N) return nullptr;
         g.sa_m = s0[a_i]; g.sa_k = s0[a_k]; g.sb_k = s1[b_k]; g.sb_n = s1[b_j];
         // outer axes, collapsed where all three operands allow it
         std::vector<long long> bd, sa, sb, sc;
         for (size_t q = 0; q < nouter; ++q) {
-            const int pa = pos(v0, vo[q]), pb = pos(v1, vo[q]);
-            if (pa < 0 || pb < 0 || x.dims[pa] != o.dims[q] || w.dims[pb] != o.dims[q]) return nullptr;
+            const int pa = pos(va, vo[q]), pb = pos(vb, vo[q]);
+            if (pa < 0 || pb < 0 || xa->dims[pa] != o.dims[q] || wb->dims[pb] != o.dims[q]) return nullptr;
             if (bd.size() > 1 && sa.back() == s0[pa] * o.dims[q] && sb.back() == s1[pb] * o.dims[q] && sc.back() == so[q] * o.dims[q]) {
                 bd.back() *= o.dims[q];
                 sa.back() = s0[pa];
@@ -353,11 +372,131 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     return p;
 }
 
+// ---- sum_to onto trailing axes, chunked order (reduce.hip) ---------------------
+struct ColSumPlan : ClassPlan {
+    ColSumArgs a{};
+    bool guarded = false;
+    mutable float* work = nullptr;
+    const char* kind() const override { return "colsum"; }
+    std::string order() const override { return "chunked(" + std::to_string(a.chunk) + ")-f32"; }
+    hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
+        ColSumArgs x = a;
+        x.x = bufs[0];
+        x.out = bufs[2];
+        x.flag = guarded ? (unsigned*)bufs[3] : nullptr;
+        if (!work) {
+            hipError_t e = hipMalloc(&work, sizeof(float) * (size_t)(a.nchunks * a.cols));
+            if (e != hipSuccess) return e;
+        }
+        x.work = work;
+        return colsum_launch(x, stream);
+    }
+    ~ColSumPlan() override {
+        if (work) hipFree(work);
+    }
+};
+
+std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
+    if (k.name != "sum_to" || k.inputs.size() != 2) return nullptr;
+    const int st = k.dtype == Ty::F32 ? 0 : k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : -1;
+    if (st < 0 || k.inputs[0].ty != k.dtype || k.output.ty != k.dtype) return nullptr;
+    const BufSpec &x = k.inputs[0], &o = k.output;
+    std::vector<int> m;
+    if (!align(o, x, &m)) return nullptr;
+    // the output is x's trailing axes: out[c] = sum_r x[r][c]
+    const size_t off = x.dims.size() - o.dims.size();
+    for (size_t i = 0; i < m.size(); ++i)
+        if (m[i] != (int)(off + i)) return nullptr;
+    auto p = std::make_unique<ColSumPlan>();
+    p->a.cols = o.numel();
+    p->a.rows = o.numel() ? x.numel() / o.numel() : 0;
+    if (p->a.rows < 256 || p->a.cols == 0) return nullptr;   // short sums: the interpreter's order is fast enough
+    p->a.chunk = 64;
+    p->a.nchunks = (p->a.rows + p->a.chunk - 1) / p->a.chunk;
+    p->a.storage = st;
+    p->guarded = k.guarded();
+    return p;
+}
+
+// ---- row nests in the interpreter's order (rows.hip) ---------------------------
+struct RowPlan : ClassPlan {
+    RowArgs a{};
+    int n_in = 1;
+    bool guarded = false;
+    const char* kind() const override { return "rows"; }
+    std::string order() const override { return "sequential"; }
+    hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
+        RowArgs x = a;
+        x.x = bufs[0];
+        if (a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2) x.mask = bufs[1];
+        if (a.op == kCrossEntropy || a.op == kCrossEntropyVjp) x.y = bufs[1];
+        if (a.op == kCrossEntropyVjp) x.ct = bufs[2];
+        x.out = bufs[n_in];
+        x.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
+        return rows_launch(x, stream);
+    }
+};
+
+std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
+    const int st = k.dtype == Ty::F32 ? 0 : k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : -1;
+    if (st < 0 || k.inputs.empty() || k.inputs[0].ty != k.dtype || k.inputs[0].dims.empty()) return nullptr;
+    const BufSpec& x = k.inputs[0];
+    const std::string& n = k.name;
+    auto p = std::make_unique<RowPlan>();
+    p->a.storage = st;
+    p->n_in = (int)k.inputs.size();
+    p->guarded = k.guarded();
+    p->a.n = x.dims.back();
+    p->a.rows = p->a.n ? x.numel() / p->a.n : 0;
+    p->a.n_real = (float)(double)p->a.n;
+    // the reduced or normalized axis must be the last, by name
+    auto last_axis = [&](const std::string& prefix, std::string* rest) {
+        if (n.compare(0, prefix.size(), prefix) != 0) return false;
+        // "<axis>", "<axis> where", "<axis>, two passes", "<axis> where, two passes"
+        const std::string ax = n.substr(prefix.size());
+        const size_t c = ax.find_first_of(" ,");
+        const std::string name = c == std::string::npos ? ax : ax.substr(0, c);
+        *rest = ax.substr(name.size());
+        return !x.names.back().empty() && x.names.back() == name;
+    };
+    std::string rest;
+    if (last_axis("mean axis ", &rest) && rest.empty() && k.inputs.size() == 1) {
+        p->a.op = kRowMean;
+    } else if (last_axis("sum axis ", &rest) && rest.empty() && k.inputs.size() == 1) {
+        p->a.op = kRowSum;
+    } else if (last_axis("softmax axis ", &rest)) {
+        if (rest.empty() && k.inputs.size() == 1) p->a.op = kSoftmax3;
+        else if (rest == ", two passes" && k.inputs.size() == 1) p->a.op = kSoftmax2;
+        else if ((rest == " where" || rest == " where, two passes") && k.inputs.size() == 2) {
+            p->a.op = rest == " where" ? kMaskedSoftmax3 : kMaskedSoftmax2;
+            const BufSpec& m = k.inputs[1];
+            std::vector<int> map;
+            const int r = (int)x.dims.size();
+            if (m.ty != Ty::I64 || m.dims.size() != 2 || r < 2 || !align(m, x, &map) || map[0] != r - 2 || map[1] != r - 1) return nullptr;
+            p->a.mask_rows = m.dims[0];
+        } else {
+            return nullptr;
+        }
+    } else if ((n == "cross_entropy" && k.inputs.size() == 2) || (n == "cross_entropy_vjp" && k.inputs.size() == 3)) {
+        const BufSpec& y = k.inputs[1];
+        if (y.ty != Ty::I64 || y.numel() != p->a.rows) return nullptr;
+        if (n == "cross_entropy_vjp" && (k.inputs[2].ty != k.dtype || k.inputs[2].numel() != p->a.rows)) return nullptr;
+        p->a.op = n == "cross_entropy" ? kCrossEntropy : kCrossEntropyVjp;
+    } else {
+        return nullptr;
+    }
+    if (k.output.ty != k.dtype) return nullptr;
+    return p;
+}
+
 }  // namespace
 
 std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode) {
+    // exact in every mode: the interpreter's order, row by row
+    if (auto p = classify_rows(k)) return p;
     if (mode == PRESK_HIP_FAST) {
         if (auto p = classify_gemm(k)) return p;
+        if (auto p = classify_sum_to(k)) return p;
     }
     return nullptr;
 }

@@ -110,7 +110,7 @@ PK_DEV float pk_ldexpf(float y, int n) {
     return y * pk_float((unsigned)(0x7f + n) << 23);
 }
 
-__device__ __noinline__ float pk_expf(float x) {
+PK_DEV float pk_expf(float x) {
     const float ln2_hi = 6.9314575195e-1f, ln2_lo = 1.4286067653e-6f, inv_ln2 = 1.4426950216e+0f;
     const float p1 = 1.6666625440e-1f, p2 = -2.7667332906e-3f;
     unsigned ax = pk_bits(x);
@@ -142,7 +142,7 @@ __device__ __noinline__ float pk_expf(float x) {
     return k == 0 ? y : pk_ldexpf(y, k);
 }
 
-__device__ __noinline__ float pk_logf(float x) {
+PK_DEV float pk_logf(float x) {
     const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
     const float lg1 = 0xaaaaaa.0p-24f, lg2 = 0xccce13.0p-25f, lg3 = 0x91e9ee.0p-25f, lg4 = 0xf89e26.0p-26f;
     unsigned ix = pk_bits(x);
@@ -174,7 +174,7 @@ __device__ __noinline__ float pk_logf(float x) {
     return s * (hfsq + r) + dk * ln2_lo - hfsq + f + dk * ln2_hi;
 }
 
-__device__ __noinline__ float pk_expm1f(float x) {
+PK_DEV float pk_expm1f(float x) {
     const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f, inv_ln2 = 1.4426950216e+00f;
     const float q1 = -3.3333212137e-2f, q2 = 1.5807170421e-3f;
     const unsigned ux = pk_bits(x), ax = ux & 0x7fffffffu;
@@ -230,7 +230,7 @@ __device__ __noinline__ float pk_expm1f(float x) {
     return y;
 }
 
-__device__ __noinline__ float pk_tanhf(float x) {
+PK_DEV float pk_tanhf(float x) {
     const unsigned ux = pk_bits(x);
     const int neg = (int)(ux >> 31);
     const unsigned w = ux & 0x7fffffffu;
@@ -283,7 +283,7 @@ PK_DEV float pk_erfc_tail(unsigned ax, float x) {
     return pk_expf(-z * z - 0.5625f) * pk_expf((z - x) * (z + x) + r / q) / x;
 }
 
-__device__ __noinline__ float pk_erff(float x) {
+PK_DEV float pk_erff(float x) {
     const float efx8 = 1.0270333290e+00f;
     unsigned ax = pk_bits(x);
     const int neg = (int)(ax >> 31);

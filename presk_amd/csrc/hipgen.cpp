@@ -1,9 +1,12 @@
 // The generic HIP printer (see hipgen.hpp).
 #include "hipgen.hpp"
 
+#include <cctype>
 #include <cmath>
 #include <cstdio>
+#include <algorithm>
 #include <functional>
+#include <map>
 #include <set>
 #include <sstream>
 
@@ -19,11 +22,22 @@ std::string hexlit(double x) {
     return buf;
 }
 
+// The text of an index list, to compare accesses.
+std::string index_key(const std::vector<const Expr*>& ix) {
+    std::string s;
+    for (auto e : ix) s += show_expr(*e) + ";";
+    return s;
+}
+
 struct Printer {
     const Kernel& k;
     std::string A;              // arithmetic type
     std::vector<std::vector<int64_t>> strides;
     std::string err;
+    // The output element a thread owns across its sequential loops, held in
+    // the register `cell` (its value as stored, i.e. rounded to the storage
+    // type) instead of memory: `cell_key` is its index list's text.
+    std::string cell_key;
 
     explicit Printer(const Kernel& k) : k(k) {
         A = k.dtype == Ty::F64 ? "double" : "float";
@@ -66,6 +80,7 @@ struct Printer {
         switch (e->kind) {
             case Expr::Num: return "((" + A + ")" + hexlit(e->num) + ")";
             case Expr::Load: {
+                if (!cell_key.empty() && e->id == k.out_buf() && index_key(e->kids) == cell_key) return "cell";
                 std::string off = offset(e->id, e->kids);
                 if (k.buf(e->id).ty == Ty::I64) return "((" + A + ")(double)" + ptr(e->id) + "[" + off + "])";
                 return "((" + A + ")" + load_stored(e->id, off) + ")";
@@ -161,6 +176,19 @@ struct Printer {
         return "";
     }
 
+    // `cell = t` as a store of t would leave it: rounded to the storage type,
+    // under the overflow guard
+    std::string cell_round(const std::string& t) const {
+        switch (k.output.ty) {
+            case Ty::F64: case Ty::F32: return "cell = " + t + ";";
+            case Ty::BF16: return "cell = pk_bf16_to_f32(pk_f32_to_bf16(" + t + "));";
+            case Ty::F16: return "ovf |= pk_overflows_f16(" + t + "); cell = pk_f16_to_f32(pk_f32_to_f16(" + t + "));";
+            case Ty::E8M15: return "ovf |= pk_overflows_e8m15(" + t + "); cell = pk_e8m15_to_f32(pk_f32_to_e8m15(" + t + "));";
+            case Ty::I64: break;
+        }
+        return "";
+    }
+
     void stmts(const std::vector<const Stmt*>& body, int depth, std::string& out) {
         std::string pad(4 * depth, ' ');
         for (auto s : body) {
@@ -189,6 +217,10 @@ struct Printer {
                     break;
                 }
                 case Stmt::Store: {
+                    if (!cell_key.empty() && s->buf == k.out_buf() && index_key(s->index) == cell_key) {
+                        out += pad + "{ " + A + " t_ = " + real(s->value) + "; " + cell_round("t_") + " stored = true; }\n";
+                        break;
+                    }
                     std::string off = offset(s->buf, s->index);
                     bool idx = k.buf(s->buf).ty == Ty::I64;
                     out += pad + store(s->buf, off, idx ? intx(s->value) : real(s->value)) + "\n";
@@ -271,6 +303,124 @@ std::set<std::string> writes(const std::vector<const Stmt*>& body) {
     return w;
 }
 
+// An index expression as sum_v c_v * i_v + c over loop variables, if it is one.
+struct Affine {
+    std::map<int, int64_t> coef;
+    int64_t c = 0;
+    bool ok = true;
+};
+
+Affine affine_of(const Expr* e) {
+    Affine a;
+    switch (e->kind) {
+        case Expr::Num:
+            if (e->integral) a.c = e->inum;
+            else a.ok = false;
+            return a;
+        case Expr::Iv: a.coef[e->id] = 1; return a;
+        case Expr::Bin: {
+            Affine x = affine_of(e->kids[0]), y = affine_of(e->kids[1]);
+            if (!x.ok || !y.ok) { a.ok = false; return a; }
+            if (e->op == Op::Add) {
+                a = x;
+                for (auto& kv : y.coef) a.coef[kv.first] += kv.second;
+                a.c += y.c;
+                return a;
+            }
+            if (e->op == Op::Mul) {
+                const Affine* v = nullptr;
+                int64_t f = 0;
+                if (x.coef.empty()) { f = x.c; v = &y; }
+                else if (y.coef.empty()) { f = y.c; v = &x; }
+                else { a.ok = false; return a; }
+                a = *v;
+                for (auto& kv : a.coef) kv.second *= f;
+                a.c *= f;
+                return a;
+            }
+            a.ok = false;
+            return a;
+        }
+        default: a.ok = false; return a;
+    }
+}
+
+// Every access to the output in `body`: (index list, is a vector access).
+void output_accesses(const Kernel& k, const std::vector<const Stmt*>& body,
+                     std::vector<std::pair<const std::vector<const Expr*>*, bool>>& acc) {
+    std::function<void(const Expr*)> ex = [&](const Expr* e) {
+        if ((e->kind == Expr::Load || e->kind == Expr::VLoad) && e->id == k.out_buf()) acc.push_back({&e->kids, e->kind == Expr::VLoad});
+        for (auto c : e->kids) ex(c);
+    };
+    for (auto s : body) {
+        if ((s->kind == Stmt::Store || s->kind == Stmt::VStore) && s->buf == k.out_buf())
+            acc.push_back({&s->index, s->kind == Stmt::VStore});
+        for (auto e : s->index) ex(e);
+        if (s->value) ex(s->value);
+        output_accesses(k, s->body, acc);
+    }
+}
+
+// The loops of `chain` that one output index, shared by every access to the
+// output, maps injectively: each index position that is an affine function
+// of chain loops alone, whose coefficients form a mixed radix over the loops'
+// bounds (c_1 = 1 >= ..., each c_j > sum of the smaller c_i (n_i - 1)), makes
+// its loops distinguishable.  Two iterations that differ in such a loop then
+// touch different elements -- a sufficient condition for running them on
+// different threads, wider than `writes_disjoint`'s c*v + t form (it takes
+// `hh*hd + d` of merge_heads).
+std::set<int> injective_loops(const Kernel& k, const std::vector<const Stmt*>& chain, const std::vector<const Stmt*>& body) {
+    std::set<int> out;
+    std::vector<std::pair<const std::vector<const Expr*>*, bool>> acc;
+    output_accesses(k, body, acc);
+    if (acc.empty()) return out;
+    const std::string key = index_key(*acc[0].first);
+    for (auto& a : acc)
+        if (a.second || index_key(*a.first) != key) return out;
+    std::map<int, int64_t> bound;
+    for (auto l : chain) bound[l->var] = l->bound;
+    for (auto e : *acc[0].first) {
+        Affine a = affine_of(e);
+        if (!a.ok || a.coef.empty()) continue;
+        std::vector<std::pair<int64_t, int>> terms;
+        bool mine = true;
+        for (auto& kv : a.coef) {
+            if (!bound.count(kv.first) || kv.second <= 0) mine = false;
+            terms.push_back({kv.second, kv.first});
+        }
+        if (!mine) continue;
+        std::sort(terms.begin(), terms.end());
+        int64_t reach = 0;   // the largest value the smaller terms add
+        bool radix = true;
+        for (auto& t : terms) {
+            if (t.first <= reach) radix = false;
+            reach += t.first * (bound[t.second] - 1);
+        }
+        if (!radix) continue;
+        for (auto& t : terms) out.insert(t.second);
+    }
+    return out;
+}
+
+// Whether every access to the output in `body` is the scalar element at one
+// index built from the loops `grid` alone: that element is the thread's own,
+// and it may live in a register across the thread's sequential loops.
+bool owns_one_element(const Kernel& k, const std::vector<const Stmt*>& body, const std::set<int>& grid, std::string* key) {
+    std::vector<std::pair<const std::vector<const Expr*>*, bool>> acc;
+    output_accesses(k, body, acc);
+    if (acc.empty() || k.output.ty == Ty::I64) return false;
+    *key = index_key(*acc[0].first);
+    for (auto& a : acc)
+        if (a.second || index_key(*a.first) != *key) return false;
+    for (auto e : *acc[0].first) {
+        Affine a = affine_of(e);
+        if (!a.ok) return false;
+        for (auto& kv : a.coef)
+            if (!grid.count(kv.first)) return false;
+    }
+    return true;
+}
+
 }  // namespace
 
 bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
@@ -310,21 +460,52 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
     int index = 0;
     for (auto& g : groups) {
         Phase ph;
-        ph.fn = "pk_phase" + std::to_string(index++);
-        // the perfect nest of parallel loops at the top of the group
-        std::vector<const Stmt*> loops;
+        // named after the nest, for profiles: pk_<name>_p<phase>
+        std::string tag;
+        for (char c : k.name) tag += std::isalnum((unsigned char)c) ? c : '_';
+        if (tag.size() > 40) tag.resize(40);
+        ph.fn = "pk_" + tag + "_p" + std::to_string(index++);
+        // The grid: the loops of the perfect nest at the top of the group whose
+        // iterations write disjoint output elements (ir.rs:375-492).  When the
+        // nest's innermost body carries no scalar from one iteration to the
+        // next, every such loop goes to the grid wherever it sits in the nest,
+        // and the others run in their order inside each thread (`sum_to`'s
+        // and `embed_vjp`'s column loops are promoted past their token
+        // loops): each output element is still updated by the same statements
+        // in the same order.  Otherwise only the disjoint prefix goes to the
+        // grid.
+        std::vector<const Stmt*> chain;
         const std::vector<const Stmt*>* level = &g;
         while (level->size() == 1 && (*level)[0]->kind == Stmt::For) {
-            const Stmt* f = (*level)[0];
-            if (!writes_disjoint(k, f->var, f->body)) break;
-            // no scalar may flow from one iteration to the next
+            chain.push_back((*level)[0]);
+            level = &(*level)[0]->body;
+        }
+        std::vector<const Stmt*> loops, serial;
+        bool whole = !chain.empty();
+        {
             std::set<std::string> def, exp;
-            for (auto l : loops) def.insert("i" + std::to_string(l->var));
-            def.insert("i" + std::to_string(f->var));
-            exposed(f->body, def, exp);
-            if (!exp.empty()) break;
-            loops.push_back(f);
-            level = &f->body;
+            for (auto l : chain) def.insert("i" + std::to_string(l->var));
+            exposed(*level, def, exp);
+            whole = whole && exp.empty();
+        }
+        if (whole) {
+            const std::set<int> inj = injective_loops(k, chain, *level);
+            for (auto f : chain) (writes_disjoint(k, f->var, f->body) || inj.count(f->var) ? loops : serial).push_back(f);
+        } else {
+            loops.clear();
+            const std::vector<const Stmt*>* lv = &g;
+            while (lv->size() == 1 && (*lv)[0]->kind == Stmt::For) {
+                const Stmt* f = (*lv)[0];
+                if (!writes_disjoint(k, f->var, f->body)) break;
+                std::set<std::string> def, exp;
+                for (auto l : loops) def.insert("i" + std::to_string(l->var));
+                def.insert("i" + std::to_string(f->var));
+                exposed(f->body, def, exp);
+                if (!exp.empty()) break;
+                loops.push_back(f);
+                lv = &f->body;
+            }
+            level = lv;
         }
         for (auto l : loops) ph.bounds.push_back(l->bound);
         ph.split = !loops.empty() && groups.size() == 1 && split_bound >= 0 && loops[0] == k.body[0];
@@ -348,7 +529,45 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
                 body += "    i" + std::to_string(loops[d]->var) + " = t % " + b + "; t /= " + b + ";\n";
             }
             body += "    i" + std::to_string(loops[0]->var) + " = t" + (ph.split ? " + a.lo" : "") + ";\n";
-            P.stmts(*level, 1, body);
+            // the loops left in the thread, in their order around the body;
+            // the thread's own output element in a register across them
+            std::set<int> grid;
+            for (auto l : loops) grid.insert(l->var);
+            std::string key;
+            const bool cell = !serial.empty() && owns_one_element(k, *level, grid, &key);
+            std::vector<const Expr*> cell_ix;
+            if (cell) {
+                std::vector<std::pair<const std::vector<const Expr*>*, bool>> acc;
+                output_accesses(k, *level, acc);
+                cell_ix = *acc[0].first;
+                body += "    " + P.A + " cell = ((" + P.A + ")" + P.load_stored(k.out_buf(), P.offset(k.out_buf(), cell_ix)) + ");\n";
+                body += "    bool stored = false;\n";
+                P.cell_key = key;
+            }
+            std::string close;
+            int depth = 1;
+            for (auto f : serial) {
+                std::string pad(4 * depth, ' '), v = "i" + std::to_string(f->var);
+                body += pad + "for (" + v + " = 0; " + v + " < " + std::to_string(f->bound) + "LL; ++" + v + ") {\n";
+                close = pad + "}\n" + close;
+                ++depth;
+            }
+            P.stmts(*level, depth, body);
+            body += close;
+            if (cell) {
+                P.cell_key.clear();
+                // the value is already the stored one: converting it back is exact
+                std::string off = P.offset(k.out_buf(), cell_ix), val;
+                switch (k.output.ty) {
+                    case Ty::BF16: val = "pk_f32_to_bf16(cell)"; break;
+                    case Ty::F16: val = "pk_f32_to_f16(cell)"; break;
+                    default: val = "cell"; break;
+                }
+                if (k.output.ty == Ty::E8M15)
+                    body += "    if (stored) pk_st24(" + P.ptr(k.out_buf()) + ", " + off + ", pk_f32_to_e8m15(cell));\n";
+                else
+                    body += "    if (stored) " + P.ptr(k.out_buf()) + "[" + off + "] = " + val + ";\n";
+            }
         } else {
             body += "    if (blockIdx.x != 0 || threadIdx.x != 0) return;\n";
             P.stmts(g, 1, body);

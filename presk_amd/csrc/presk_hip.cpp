@@ -202,6 +202,12 @@ int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, 
     h->plan = classify(*k, mode);
     if (!h->plan) {
         if (!generate_hip(*k, &h->gen, &err)) return fail(err.compare(0, 5, "E7005") == 0 ? PRESK_HIP_REFUSED : PRESK_HIP_ERR, err);
+        // PRESK_HIP_DUMP=<dir>: keep each printed source, for inspection
+        if (const char* dump = std::getenv("PRESK_HIP_DUMP")) {
+            char name[40];
+            std::snprintf(name, sizeof name, "/%016llx.hip", (unsigned long long)fnv1a(h->gen.src));
+            std::ofstream(std::string(dump) + name) << "// " << k->name << "\n" << h->gen.src;
+        }
         if (!build_code_object(h->gen.src, &h->code, &err)) return fail(PRESK_HIP_ERR, err);
     }
     h->k = std::move(k);

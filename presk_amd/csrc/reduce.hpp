@@ -1,0 +1,19 @@
+// Launch descriptions of the reduction classes (reduce.hip, rows.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace presk {
+
+struct ColSumArgs {
+    const void* x;        // [rows][cols] in the storage type
+    void* out;            // [cols]
+    float* work;          // [nchunks][cols] chunk sums
+    unsigned* flag;       // overflow guard (f16) or null
+    long long rows, cols, chunk, nchunks;
+    int storage;          // 0 f32, 1 bf16, 2 f16
+};
+
+hipError_t colsum_launch(const ColSumArgs& a, hipStream_t stream);
+
+}  // namespace presk

@@ -1,0 +1,26 @@
+// Launch description of the row-nest class (rows.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace presk {
+
+enum RowOp {
+    kRowMean = 0, kRowSum, kSoftmax3, kSoftmax2, kMaskedSoftmax3, kMaskedSoftmax2, kCrossEntropy, kCrossEntropyVjp
+};
+
+struct RowArgs {
+    const void* x;        // [rows][n]
+    const void* mask;     // i64 [mask_rows][n] (masked softmax)
+    const void* y;        // i64 [rows] (cross entropy)
+    const void* ct;       // [rows] (cross_entropy_vjp)
+    void* out;
+    unsigned* flag;
+    long long rows, n, mask_rows;
+    float n_real;         // n as the nest's f32 constant (mean)
+    int op, storage;      // RowOp; 0 f32, 1 bf16, 2 f16
+};
+
+hipError_t rows_launch(const RowArgs& a, hipStream_t stream);
+
+}  // namespace presk

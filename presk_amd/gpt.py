@@ -1,0 +1,369 @@
+"""The course GPT (examples/corpus/nlp/05_gpt.psk) as programs of the
+reference's nests: config 3 (forward and loss) and config 4 (one training
+step: the loss's value and its gradient in every parameter, `value_vjp`).
+
+The forward is the program's `GPT.apply` and `loss`: token and position
+embeddings, L pre-LayerNorm blocks of causal self-attention (split_heads,
+`ein` scores, the 1/sqrt(HD) scale, the masked softmax, `ein` values,
+merge_heads) and a GELU MLP, a final LayerNorm, the head `dot`, and
+`mean(cross_entropy(...))`.  Dropout is at p = 0 (the configs' reading).
+
+The gradient restates the reference's reverse mode: each primitive's
+vector-Jacobian product as crates/presk-core/src/ad/rules.rs:16-217 emits it
+(`dot` -> `dot_vjp_l` + `dot_vjp_r`; `ein` -> one `ein` per operand;
+broadcast adds -> `sum_to`; `mean` -> `mean_vjp`; `softmax` ->
+`y * (ct - broadcast(sum(ct * y)))`; `gelu` -> `gelu_deriv * ct`; `embed` ->
+`embed_vjp`; `cross_entropy` -> `cross_entropy_vjp`; split/merge_heads ->
+each other), cotangents of a value used twice added.  Elementwise chains are
+grouped as the fusion plan groups them (crates/presk-core/src/fusion.rs:
+138): a chain of one result type whose interior values have one consumer is
+one `fused` nest.  The reference's exact grouping of the gradient entry and
+its layout plan can only be read off `presk dump`, which needs the Rust
+reference; this restatement is pinned by its mathematics instead (the
+gradient against torch autograd, tests/test_gpt_program.py).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import lower as L
+from .program import Program
+
+A, O = L.ax, L.Operand
+
+
+@dataclass
+class GptShape:
+    V: int = 65
+    D: int = 384
+    H: int = 6
+    L: int = 6
+    B: int = 64
+    T: int = 256
+
+    @property
+    def HD(self):
+        return self.D // self.H
+
+
+TINY = GptShape(V=64, D=16, H=2, L=2, B=2, T=8)
+COURSE = GptShape()
+
+
+class Builder:
+    """Buffers by name with their axes and kind; each primitive one launch."""
+
+    def __init__(self, prog: Program, dtype: str):
+        self.p, self.dt = prog, dtype
+        self.axes: dict = {}
+        self.kind: dict = {}
+        self.n = 0
+
+    def input(self, name, axes, kind="real"):
+        self.axes[name], self.kind[name] = list(axes), kind
+        return name
+
+    def op(self, name):
+        return O(self.axes[name], self.kind[name])
+
+    def _out(self, low, ins, name=None):
+        if name is None:
+            self.n += 1
+            name = f"t{self.n}"
+        self.p.add(low, ins, name)
+        self.axes[name], self.kind[name] = list(low.out_axes), low.out_kind
+        return name
+
+    # --- primitives -----------------------------------------------------------
+    def binary(self, op, a, b, name=None):
+        return self._out(L.elementwise_binary(op, [self.op(a), self.op(b)], self.dt), [a, b], name)
+
+    def unary(self, op, a, name=None):
+        return self._out(L.unary(op, [self.op(a)], self.dt), [a], name)
+
+    def fused(self, steps, ins, out_like, name=None):
+        return self._out(L.fused(steps, [self.op(i) for i in ins], self.axes[out_like], self.dt), ins, name)
+
+    def dot(self, x, w, b=None, name=None):
+        d = L.dot([self.op(x), self.op(w)], self.dt)
+        if b is None:
+            return self._out(d, [x, w], name)
+        return self._out(L.dot([self.op(x), self.op(w), self.op(b)], self.dt, epilogue=(True, d.out_axes)), [x, w, b], name)
+
+    def dot_vjp_l(self, ct, b, name=None):
+        return self._out(L.dot_vjp_l([self.op(ct), self.op(b)], self.dt), [ct, b], name)
+
+    def dot_vjp_r(self, a, ct, name=None):
+        return self._out(L.dot_vjp_r([self.op(a), self.op(ct)], self.dt), [a, ct], name)
+
+    def ein(self, a, b, la, lb, out, name=None, like=None):
+        """`like`: the value whose type the result has -- an operand's, for the
+        `ein` of its cotangent (rules.rs:151-169 gives it `tys[j]`)."""
+        r = self._out(L.ein([self.op(a), self.op(b)], [la, lb], out, self.dt), [a, b], name)
+        if like is not None:
+            self.axes[r] = list(self.axes[like])
+        return r
+
+    def mean(self, x, axis, name=None):
+        return self._out(L.reduce_axis("mean", axis, [self.op(x)], self.dt), [x], name)
+
+    def sum(self, x, axis, name=None):
+        return self._out(L.reduce_axis("sum", axis, [self.op(x)], self.dt), [x], name)
+
+    def mean_all(self, x, name=None):
+        return self._out(L.reduce_all("mean_all", [self.op(x)], self.dt), [x], name)
+
+    def mean_vjp(self, ct, like, axis, name=None):
+        return self._out(L.mean_vjp(axis, [self.op(ct), self.op(like)], self.dt), [ct, like], name)
+
+    def sum_to(self, x, like, name=None):
+        return self._out(L.sum_to([self.op(x), self.op(like)], self.dt), [x, like], name)
+
+    def broadcast_like(self, x, like, name=None):
+        return self._out(L.broadcast_like([self.op(x), self.op(like)], self.dt), [x, like], name)
+
+    def masked_softmax(self, x, mask, axis, name=None):
+        return self._out(L.masked_softmax(axis, [self.op(x), self.op(mask)], self.dt), [x, mask], name)
+
+    def embed(self, table, ids, name=None):
+        out = self._out(L.embed([self.op(table), self.op(ids)], self.dt), [table, ids], name)
+        # the result's last axis is the table's (its type names it)
+        last = self.axes[table][-1]
+        self.axes[out][-1] = L.Axis(last.name, last.len)
+        return out
+
+    def embed_vjp(self, table, ids, ct, name=None):
+        return self._out(L.embed_vjp([self.op(table), self.op(ids), self.op(ct)], self.dt), [table, ids, ct], name)
+
+    def split_heads(self, x, h, hd, name=None):
+        return self._out(L.split_heads(h, hd, [self.op(x)], self.dt), [x], name)
+
+    def merge_heads(self, x, h, hd, name=None):
+        return self._out(L.merge_heads(h, hd, [self.op(x)], self.dt), [x], name)
+
+    def cross_entropy(self, logits, y, name=None):
+        return self._out(L.cross_entropy([self.op(logits), self.op(y)], self.dt), [logits, y], name)
+
+    def cross_entropy_vjp(self, logits, y, ct, name=None):
+        return self._out(L.cross_entropy_vjp([self.op(logits), self.op(y), self.op(ct)], self.dt), [logits, y, ct], name)
+
+    def causal_mask(self, T, name):
+        return self._out(L.causal_mask("seq", T, self.dt), [], name)
+
+    def positions(self, T, name):
+        return self._out(L.positions("seq", T, self.dt), [], name)
+
+
+def param_shapes(s: GptShape) -> dict:
+    """name -> axes of every parameter (05_gpt.psk's modules)."""
+    ps = {"tok": A(("vocab", s.V), ("model", s.D)), "pos": A(s.T, s.D)}
+    for l in range(s.L):
+        p = f"b{l}."
+        for ln in ("ln1", "ln2"):
+            ps[p + ln + ".g"] = A(("model", s.D))
+            ps[p + ln + ".b"] = A(("model", s.D))
+        for w in ("wq", "wk", "wv", "wo"):
+            ps[p + w] = A(s.D, s.D)
+            ps[p + w + ".b"] = A(s.D)
+        ps[p + "up"] = A(s.D, 4 * s.D)
+        ps[p + "up.b"] = A(4 * s.D)
+        ps[p + "down"] = A(4 * s.D, s.D)
+        ps[p + "down.b"] = A(s.D)
+    ps["lnf.g"] = A(("model", s.D))
+    ps["lnf.b"] = A(("model", s.D))
+    ps["head"] = A(s.D, s.V)
+    return ps
+
+
+def init_params(s: GptShape, seed: int = 2) -> dict:
+    """Config 3's weights: N(0, 0.02) for every weight matrix and embedding,
+    LayerNorm gains one and biases zero, linear biases N(0, 0.02) (the
+    program's zeros would make the bias gradients' checks vacuous)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, axes in param_shapes(s).items():
+        shape = [a.len for a in axes]
+        if name.endswith(".g"):
+            out[name] = np.ones(shape, np.float32)
+        elif name.endswith(".b") and (".ln" in name or name.startswith("lnf")):
+            out[name] = np.zeros(shape, np.float32)
+        else:
+            out[name] = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    return out
+
+
+def _layernorm(b: Builder, x, g, bias, keep: bool, tag: str):
+    """examples/corpus/nlp/05_gpt.psk LayerNorm: (x - mu) / sqrt(var + eps) * g + b.
+    `keep`: the training entry keeps the values the gradient reads
+    (x - mu, sqrt(var + eps), the normalized x), so they reach memory."""
+    mu = b.mean(x, "model", name=f"{tag}.mu")
+    if not keep:
+        sq = b.fused([("sub", [("in", 0), ("in", 1)]), ("pow2", [("step", 0)])], [x, mu], x)
+        var = b.mean(sq, "model")
+        return b.fused([("sub", [("in", 0), ("in", 1)]), ("add", [("in", 2), ("in", 3)]), ("sqrt", [("step", 1)]),
+                        ("div", [("step", 0), ("step", 2)]), ("mul", [("step", 3), ("in", 4)]), ("add", [("step", 4), ("in", 5)])],
+                       [x, mu, var, "eps", g, bias], x), {}
+    xm = b.binary("sub", x, mu, name=f"{tag}.xm")
+    sq = b.unary("pow2", xm, name=f"{tag}.sq")
+    var = b.mean(sq, "model", name=f"{tag}.var")
+    sd = b.fused([("add", [("in", 0), ("in", 1)]), ("sqrt", [("step", 0)])], [var, "eps"], var, name=f"{tag}.sd")
+    xh = b.binary("div", xm, sd, name=f"{tag}.xh")
+    y = b.fused([("mul", [("in", 0), ("in", 1)]), ("add", [("step", 0), ("in", 2)])], [xh, g, bias], xh, name=f"{tag}.y")
+    return y, {"x": x, "xm": xm, "sq": sq, "sd": sd, "xh": xh, "g": g, "b": bias}
+
+
+def _layernorm_vjp(b: Builder, saved, dy, tag):
+    """The LayerNorm's reverse mode (rules.rs: add, mul, div, sqrt, pow(2),
+    mean, sub), cotangents added where a value has two consumers.  Returns dx,
+    dg, dbias."""
+    xm, sd, xh, g = saved["xm"], saved["sd"], saved["xh"], saved["g"]
+    db = b.sum_to(dy, saved["b"], name=f"{tag}.dbias")                      # add: sum_to to b's axes
+    dg = b.sum_to(b.binary("mul", dy, xh), g, name=f"{tag}.dg")            # mul by g: ct * xh, to g's axes
+    dxh = b.binary("mul", dy, g)                                            # ct * g
+    # div xh = xm / sd: d xm = ct / sd;  d sd = sum_to(-(ct * xh) / sd)
+    dsd = b.sum_to(b.fused([("mul", [("in", 0), ("in", 1)]), ("div", [("step", 0), ("in", 2)]), ("neg", [("step", 1)])],
+                           [dxh, xh, sd], dxh), sd)
+    # sqrt: d(var + eps) = dsd / (2 * sd)
+    dvar = b.fused([("mul", [("in", 0), ("in", 1)]), ("div", [("in", 2), ("step", 0)])], ["two", sd, dsd], sd)
+    # mean: d sq = mean_vjp(dvar);  pow(2): d xm += d sq * (2 * xm); plus dxh / sd
+    dsq = b.mean_vjp(dvar, saved["sq"], "model")
+    dxm = b.fused([("div", [("in", 0), ("in", 1)]), ("pow1", [("in", 3)]), ("mul", [("in", 2), ("step", 1)]),
+                   ("mul", [("in", 4), ("step", 2)]), ("add", [("step", 0), ("step", 3)])],
+                  [dxh, sd, "two", xm, dsq], xm)
+    # sub xm = x - mu: d x = dxm;  d mu = sum_to(-dxm);  mean: d x += mean_vjp(d mu)
+    dmu = b.sum_to(b.unary("neg", dxm), f"{tag}.mu")
+    dx2 = b.mean_vjp(dmu, saved["x"], "model")
+    dx = b.binary("add", dxm, dx2)
+    return dx, dg, db
+
+
+def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None) -> tuple:
+    """The program of config 3 (`train=False`: loss only) or config 4.
+    Returns (program, builder, names) with names["loss"] and, for training,
+    names["grads"][param] = buffer of its gradient."""
+    from . import hip
+    p = Program(f"gpt-{'step' if train else 'forward'}-{dtype}", mode=hip.FAST if mode is None else mode)
+    b = Builder(p, dtype)
+    for name, axes in param_shapes(s).items():
+        b.input(name, axes)
+    b.input("ids", A(("batch", s.B), ("seq", s.T)), "idx")
+    b.input("y", A(("batch", s.B), ("seq", s.T)), "idx")
+    b.input("eps", A())
+    b.input("scale", A())       # sqrt(HD : R), the attention scores' divisor
+    b.input("two", A())         # real(2) of pow(2)'s and sqrt's adjoints
+    b.input("one", A())         # the loss's cotangent
+    mask = b.causal_mask(s.T, "mask")
+    pos_ids = b.positions(s.T, "pos_ids")
+    te = b.embed("tok", "ids", name="te")
+    pe = b.embed("pos", pos_ids, name="pe")
+    x = b.binary("add", te, pe, name="h0")
+    saved = []
+    H, HD = s.H, s.HD
+    lbl_q = ["batch", "heads", "seq", "hd"]
+    lbl_k = ["batch", "heads", "seq2", "hd"]
+    lbl_s = ["batch", "heads", "seq", "seq2"]
+    for l in range(s.L):
+        pr = f"b{l}."
+        xn1, ln1 = _layernorm(b, x, pr + "ln1.g", pr + "ln1.b", train, f"b{l}.ln1")
+        q = b.dot(xn1, pr + "wq", pr + "wq.b")
+        k = b.dot(xn1, pr + "wk", pr + "wk.b")
+        v = b.dot(xn1, pr + "wv", pr + "wv.b")
+        qh, kh, vh = b.split_heads(q, H, HD), b.split_heads(k, H, HD), b.split_heads(v, H, HD)
+        sc = b.ein(qh, kh, lbl_q, lbl_k, lbl_s)
+        sc2 = b.binary("div", sc, "scale")
+        a = b.masked_softmax(sc2, mask, "seq2")
+        o = b.ein(a, vh, lbl_s, lbl_k, lbl_q)
+        om = b.merge_heads(o, H, HD)
+        ao = b.dot(om, pr + "wo", pr + "wo.b")
+        h = b.binary("add", x, ao)
+        xn2, ln2 = _layernorm(b, h, pr + "ln2.g", pr + "ln2.b", train, f"b{l}.ln2")
+        u = b.dot(xn2, pr + "up", pr + "up.b")
+        g = b.unary("gelu", u)
+        dn = b.dot(g, pr + "down", pr + "down.b")
+        xo = b.binary("add", h, dn)
+        saved.append(dict(x=x, xn1=xn1, ln1=ln1, qh=qh, kh=kh, vh=vh, a=a, om=om, h=h, xn2=xn2, ln2=ln2, u=u, g=g))
+        x = xo
+    xf, lnf = _layernorm(b, x, "lnf.g", "lnf.b", train, "lnf")
+    logits = b.dot(xf, "head", name="logits")
+    ce = b.cross_entropy(logits, "y", name="ce")
+    loss = b.mean_all(ce, name="loss")
+    names = {"loss": loss, "grads": {}}
+    if not train:
+        return p, b, names
+    G = names["grads"]
+    # ---- reverse mode -------------------------------------------------------
+    dce = b.mean_vjp("one", ce, None)
+    dlogits = b.cross_entropy_vjp(logits, "y", dce)
+    dxf = b.dot_vjp_l(dlogits, "head")
+    G["head"] = b.dot_vjp_r(xf, dlogits, name="d.head")
+    dx, G["lnf.g"], G["lnf.b"] = _layernorm_vjp(b, lnf, dxf, "lnf")
+    for l in reversed(range(s.L)):
+        pr, sv = f"b{l}.", saved[l]
+        # xo = h + dn
+        ddn = dx
+        dg_ = b.dot_vjp_l(ddn, pr + "down")
+        G[pr + "down"] = b.dot_vjp_r(sv["g"], ddn, name="d." + pr + "down")
+        G[pr + "down.b"] = b.sum_to(ddn, pr + "down.b", name="d." + pr + "down.b")
+        du = b.fused([("gelu_deriv", [("in", 1)]), ("mul", [("in", 0), ("step", 0)])], [dg_, sv["u"]], sv["u"])
+        dxn2 = b.dot_vjp_l(du, pr + "up")
+        G[pr + "up"] = b.dot_vjp_r(sv["xn2"], du, name="d." + pr + "up")
+        G[pr + "up.b"] = b.sum_to(du, pr + "up.b", name="d." + pr + "up.b")
+        dh_ln, G[pr + "ln2.g"], G[pr + "ln2.b"] = _layernorm_vjp(b, sv["ln2"], dxn2, f"b{l}.ln2")
+        dh = b.binary("add", dx, dh_ln)
+        # h = x + ao
+        dao = dh
+        dom = b.dot_vjp_l(dao, pr + "wo")
+        G[pr + "wo"] = b.dot_vjp_r(sv["om"], dao, name="d." + pr + "wo")
+        G[pr + "wo.b"] = b.sum_to(dao, pr + "wo.b", name="d." + pr + "wo.b")
+        do = b.split_heads(dom, H, HD)
+        da = b.ein(do, sv["vh"], lbl_q, lbl_k, lbl_s, like=sv["a"])
+        dvh = b.ein(do, sv["a"], lbl_q, lbl_s, lbl_k, like=sv["vh"])
+        # softmax: a * (da - broadcast(sum(da * a)))
+        t = b.binary("mul", da, sv["a"])
+        ssum = b.sum(t, "seq2")
+        sb = b.broadcast_like(ssum, da)
+        dsc2 = b.fused([("sub", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("step", 0)])], [da, sb, sv["a"]], da)
+        dsc = b.binary("div", dsc2, "scale")
+        dqh = b.ein(dsc, sv["kh"], lbl_s, lbl_k, lbl_q, like=sv["qh"])
+        dkh = b.ein(dsc, sv["qh"], lbl_s, lbl_q, lbl_k, like=sv["kh"])
+        dq, dk, dv = b.merge_heads(dqh, H, HD), b.merge_heads(dkh, H, HD), b.merge_heads(dvh, H, HD)
+        dxq = b.dot_vjp_l(dq, pr + "wq")
+        dxk = b.dot_vjp_l(dk, pr + "wk")
+        dxv = b.dot_vjp_l(dv, pr + "wv")
+        for w, dw in (("wq", dq), ("wk", dk), ("wv", dv)):
+            G[pr + w] = b.dot_vjp_r(sv["xn1"], dw, name="d." + pr + w)
+            G[pr + w + ".b"] = b.sum_to(dw, pr + w + ".b", name="d." + pr + w + ".b")
+        dxn1 = b.fused([("add", [("in", 0), ("in", 1)]), ("add", [("step", 0), ("in", 2)])], [dxq, dxk, dxv], dxq)
+        dx_ln, G[pr + "ln1.g"], G[pr + "ln1.b"] = _layernorm_vjp(b, sv["ln1"], dxn1, f"b{l}.ln1")
+        dx = b.binary("add", dh, dx_ln)
+    # h0 = te + pe: te's cotangent dx; pe's sum_to over the batch
+    G["tok"] = b.embed_vjp("tok", "ids", dx, name="d.tok")
+    dpe = b.sum_to(dx, pe)
+    G["pos"] = b.embed_vjp("pos", pos_ids, dpe, name="d.pos")
+    return p, b, names
+
+
+def host_inputs(s: GptShape, seed: int = 2) -> dict:
+    """The seeded synthetic inputs: parameters, token ids and targets uniform
+    over the vocabulary, and the scalar constants."""
+    host = init_params(s, seed)
+    rng = np.random.default_rng(seed + 100)
+    host["ids"] = rng.integers(0, s.V, size=(s.B, s.T), dtype=np.int64)
+    host["y"] = rng.integers(0, s.V, size=(s.B, s.T), dtype=np.int64)
+    host["eps"] = np.array([1e-5], np.float32)
+    host["scale"] = np.array([math.sqrt(float(s.HD))], np.float32)
+    host["two"] = np.array([2.0], np.float32)
+    host["one"] = np.array([1.0], np.float32)
+    return host
+
+
+def contraction_flops(s: GptShape, train: bool) -> float:
+    """Algorithmic contraction flops of one call: 2*prod(outer)*I*J*K summed
+    over the nests (the forward's, and the gradient's two per contraction)."""
+    N = s.B * s.T
+    per_layer = 2 * N * s.D * s.D * 4 + 2 * N * s.D * 4 * s.D * 2 + 2 * s.B * s.H * s.T * s.T * s.HD * 2
+    fwd = s.L * per_layer + 2 * N * s.D * s.V
+    return fwd * 3 if train else fwd

@@ -596,10 +596,33 @@ def dot_vjp_r(ins, dtype, order=None) -> Lowered:
 
 
 def ein(ins, operands, output, dtype) -> Lowered:
+    """`ein` (lower.rs:586-636): a contraction nest where the operands' roles
+    fit one (`Contraction::of`), else the generic many-operand form: one
+    accumulator per output element over the summed axes, its term
+    `(1 * x0) * x1 ...`."""
     c = contraction_of("ein", ins, operands, output)
-    if c is None:
-        raise ValueError("ein: not a contraction nest")
-    return emit_contraction(c, dtype, ins)
+    if c is not None:
+        return emit_contraction(c, dtype, ins)
+    names = []
+    for t, ns in zip(ins, operands):
+        for a, n in zip(t.axes, ns):
+            if not any(m == n for m, _ in names):
+                names.append((n, a.len))
+    contracted = [(n, l) for n, l in names if n not in output]
+    out = [Axis(o, next(l for n, l in names if n == o)) for o in output]
+    allv = list(output) + [n for n, _ in contracted]
+    bd = B()
+    ov = bd.loops(dims(out))
+    cv = bd.loops([l for _, l in contracted])
+    all_v = ov + cv
+    acc = bd.sv()
+    prod = num(1)
+    for i, ns in enumerate(operands):
+        ix = [iv(all_v[allv.index(n)]) for n in ns]
+        prod = bin_("*", prod, load(i, ix))
+    inner = nest(cv, [l for _, l in contracted], [Set(acc, bin_("+", sv(acc), prod))])
+    body = [Set(acc, num(0))] + inner + [Store(len(ins), ivs(ov), sv(acc))]
+    return kernel(f"ein[{', '.join(output)}]", dtype, ins, out, "real", bd, nest(ov, dims(out), body))
 
 
 # ----- reductions (lower.rs:1221-1419, 1670-1703) ------------------------------------------

@@ -1,0 +1,70 @@
+"""The course-GPT training step (presk_amd/gpt.py) end to end on the device,
+at the reference's TINY constants: in EXACT mode every buffer of the step
+(loss, gradients, every intermediate) equals the oracle's byte for byte; in
+FAST mode the loss and gradients stay within the reassociation band of the
+MFMA contractions."""
+import numpy as np
+import pytest
+
+from presk_amd import configs, gpt, hip
+from tests import cpu_program, fmt
+
+pytestmark = pytest.mark.gpu
+
+
+def device_run(p, host):
+    p.compile()
+    configs.load_inputs(p, host)
+    p.prepare()
+    p.run()
+    hip.sync()
+    p.check_overflow()
+    return p
+
+
+@pytest.fixture(scope="module")
+def oracle_tiny():
+    s = gpt.TINY
+    out = {}
+    for dt in ("f32", "bf16"):
+        p, b, names = gpt.build(s, dt, train=True, mode=hip.EXACT)
+        host = gpt.host_inputs(s)
+        out[dt] = (cpu_program.run(p, host), names)
+    return out
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_tiny_gpt_step_exact_bits(oracle_tiny, dt):
+    s = gpt.TINY
+    p, b, names = gpt.build(s, dt, train=True, mode=hip.EXACT)
+    host = gpt.host_inputs(s)
+    device_run(p, host)
+    env, _ = oracle_tiny[dt]
+    bad = []
+    for ln in p.launches:
+        got = p.bufs.download(ln.out)
+        if got.tobytes() != env[ln.out].tobytes():
+            bad.append((ln.out, ln.low.name))
+    assert not bad, f"{len(bad)} buffers differ, first: {bad[:5]}"
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_tiny_gpt_step_fast_band(oracle_tiny, dt):
+    s = gpt.TINY
+    p, b, names = gpt.build(s, dt, train=True, mode=hip.FAST)
+    host = gpt.host_inputs(s)
+    device_run(p, host)
+    env, _ = oracle_tiny[dt]
+    kinds = {ln.compiled.kind for ln in p.launches}
+    assert "gemm" in kinds
+    loss = float(fmt.decode(p.bufs.download(names["loss"]), dt)[0])
+    want = float(fmt.decode(env[names["loss"]], dt)[0])
+    tol = 1e-5 if dt == "f32" else 2e-2
+    assert abs(loss - want) <= tol * abs(want), (loss, want)
+    floor = 1e-3 * max(np.max(np.abs(fmt.decode(env[buf], dt))) for buf in names["grads"].values())
+    for name, buf in names["grads"].items():
+        got = fmt.decode(p.bufs.download(buf), dt).astype(np.float64)
+        ref = fmt.decode(env[buf], dt).astype(np.float64)
+        scale = max(np.max(np.abs(ref)), floor)
+        err = np.max(np.abs(got - ref)) / scale
+        assert err < (1e-4 if dt == "f32" else 6e-2), (name, err)

@@ -1,0 +1,85 @@
+"""The FAST-mode column sum (`sum_to` onto trailing axes) in its declared
+order: the reference's `ReductionOrder::Chunked { size: 64 }` semantics
+(crates/presk-kernel/src/lower.rs:427-464: chunks of 64 consecutive rows each
+summed from zero in order, the chunk sums added in order from zero) with f32
+accumulation.  The same order is written here as a PSK-Kernel nest and run by
+the oracle; the device must give its bits exactly.  Also the row-nest class
+at sizes beyond the zoo's, bit-exact against the oracle."""
+import numpy as np
+import pytest
+
+from oracle import cexec
+from presk_amd import hip
+from presk_amd import lower as L
+from tests import fmt, zoo
+
+pytestmark = pytest.mark.gpu
+A, O = L.ax, L.Operand
+
+
+def chunked_colsum_text(rows, cols, dtype, chunk=64):
+    """out[c] = chunked sum over r of x[r, c] (x viewed [rows, cols])."""
+    full, rem = divmod(rows, chunk)
+    lines = [f"kernel colsum (%0 : {dtype}[{rows}, {cols}]) -> %1 : {dtype}[{cols}] {{",
+             f"  for i0 in 0..{cols} {{", "    s0 = 0"]
+    if full:
+        lines += [f"    for i1 in 0..{full} {{", "      s1 = 0", f"      for i2 in 0..{chunk} {{",
+                  f"        s1 = (s1 + %0[((i1 * {chunk}) + i2), i0])", "      }", "      s0 = (s0 + s1)", "    }"]
+    if rem:
+        lines += ["    s1 = 0", f"    for i2 in 0..{rem} {{", f"      s1 = (s1 + %0[(i2 + {full * chunk}), i0])", "    }",
+                  "    s0 = (s0 + s1)"]
+    lines += ["    %1[i0] = s0", "  }", "}"]
+    return "\n".join(lines) + "\n"
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", [(4, 300, 40), (64, 256, 384)])
+def test_fast_sum_to_is_chunked_order(dt, shape):
+    B, T, D = shape
+    x = O(A(("batch", B), ("seq", T), ("model", D)))
+    low = L.sum_to([x, O(A(("model", D)))], dt)
+    ex = hip.HipExec(0, mode=hip.FAST)
+    c = ex.compiled(low.text, dt, low.lanes)
+    assert c.kind == "colsum", c.kind
+    rng = np.random.default_rng(5)
+    xs = fmt.encode(rng.standard_normal((B, T, D)).astype(np.float32), dt)
+    want, _ = cexec.run(chunked_colsum_text(B * T, D, dt), dt, [xs, ], lanes=1)
+    out = hip.DeviceBuffer(D * hip.STORAGE_BYTES[dt])
+    ex.run(low.text, dt, [hip.DeviceBuffer.of(xs), hip.DeviceBuffer.of(np.zeros(D * hip.STORAGE_BYTES[dt], np.uint8))], out)
+    assert out.download(want.dtype).tobytes() == want.tobytes()
+
+
+def _big_rows(dt):
+    B, H, T, V = 2, 3, 40, 65
+    s = O(A(("batch", B), ("heads", H), ("seq", T), ("seq2", T)))
+    mask = O(A(("seq", T), ("seq2", T)), "idx")
+    logits = O(A(("batch", 5), ("seq", 60), ("vocab", V)))
+    ids = O(A(("batch", 5), ("seq", 60)), "idx")
+    rows = O(A(("batch", 5), ("seq", 60)))
+    return [
+        ("masked_softmax", L.masked_softmax("seq2", [s, mask], dt)),
+        ("masked_softmax2", L.masked_softmax("seq2", [s, mask], dt, two_passes=True)),
+        ("softmax", L.softmax("seq2", [s], dt)),
+        ("mean", L.reduce_axis("mean", "vocab", [logits], dt)),
+        ("cross_entropy", L.cross_entropy([logits, ids], dt)),
+        ("cross_entropy_vjp", L.cross_entropy_vjp([logits, ids, rows], dt)),
+    ]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_rows_class_exact_at_size(dt):
+    ex = hip.HipExec(0, mode=hip.FAST)
+    for name, low in _big_rows(dt):
+        ins = zoo.inputs(low, seed=11, scale=3.0)
+        if name == "masked_softmax" or name == "masked_softmax2":
+            T = 40
+            ins[1] = np.tril(np.ones((T, T), np.int64)).ravel()
+        want, wf = cexec.run(low.text, dt, ins, lanes=low.lanes)
+        from oracle import kernel_text as kt
+        k = kt.parse_kernel(low.text)
+        nbytes = k.output.numel * hip.STORAGE_BYTES[dt]
+        out = hip.DeviceBuffer(nbytes)
+        out.upload(np.full(nbytes, 0xFF, np.uint8))
+        c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+        assert c.kind == "rows", (name, c.kind)
+        assert out.download(np.uint8, nbytes).tobytes() == want.view(np.uint8).tobytes(), name
