@@ -15,6 +15,7 @@
 #include "gemm.hpp"
 #include "reduce.hpp"
 #include "rows.hpp"
+#include "scatter.hpp"
 #include "presk_hip.h"
 
 namespace presk {
@@ -477,6 +478,16 @@ std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
         } else {
             return nullptr;
         }
+    } else if (n == "sum_to" && k.inputs.size() == 2) {
+        // onto x's leading axes: each output element the ordered sum of a row
+        std::vector<int> m;
+        const BufSpec& o = k.output;
+        if (!align(o, x, &m) || o.dims.empty() || o.dims.size() >= x.dims.size()) return nullptr;
+        for (size_t i = 0; i < m.size(); ++i)
+            if (m[i] != (int)i) return nullptr;
+        p->a.rows = o.numel();
+        p->a.n = p->a.rows ? x.numel() / p->a.rows : 0;
+        p->a.op = kSumToRows;
     } else if ((n == "cross_entropy" && k.inputs.size() == 2) || (n == "cross_entropy_vjp" && k.inputs.size() == 3)) {
         const BufSpec& y = k.inputs[1];
         if (y.ty != Ty::I64 || y.numel() != p->a.rows) return nullptr;
@@ -491,9 +502,47 @@ std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// embed_vjp: the tokens' cotangent rows added into the table rows they name,
+// in token order (exact in every mode)
+
+struct ScatterPlan : ClassPlan {
+    ScatterArgs a{};
+    bool guarded = false;
+    const char* kind() const override { return "scatter"; }
+    std::string order() const override { return "sequential"; }
+    hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
+        ScatterArgs x = a;
+        x.idx = (const long long*)bufs[1];
+        x.ct = bufs[2];
+        x.out = bufs[3];
+        x.flag = guarded ? (unsigned*)bufs[4] : nullptr;
+        return embed_vjp_launch(x, stream);
+    }
+};
+
+std::unique_ptr<ClassPlan> classify_scatter(const Kernel& k) {
+    const int st = k.dtype == Ty::F32 ? 0 : k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : -1;
+    if (st < 0 || k.name != "embed_vjp" || k.inputs.size() != 3) return nullptr;
+    const BufSpec &table = k.inputs[0], &idx = k.inputs[1], &ct = k.inputs[2], &o = k.output;
+    if (table.dims.size() != 2 || o.dims != table.dims || idx.ty != Ty::I64 || ct.ty != k.dtype) return nullptr;
+    if (ct.dims.size() != idx.dims.size() + 1 || ct.dims.back() != table.dims[1]) return nullptr;
+    for (size_t i = 0; i < idx.dims.size(); ++i)
+        if (ct.dims[i] != idx.dims[i]) return nullptr;
+    auto p = std::make_unique<ScatterPlan>();
+    p->a.tokens = idx.numel();
+    p->a.vocab = table.dims[0];
+    p->a.d = table.dims[1];
+    p->a.storage = st;
+    p->guarded = k.guarded();
+    if (p->a.tokens > (1ll << 30) || p->a.vocab > 0x7fffffffll) return nullptr;
+    return p;
+}
+
 std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode) {
     // exact in every mode: the interpreter's order, row by row
     if (auto p = classify_rows(k)) return p;
+    if (auto p = classify_scatter(k)) return p;
     if (mode == PRESK_HIP_FAST) {
         if (auto p = classify_gemm(k)) return p;
         if (auto p = classify_sum_to(k)) return p;

@@ -6,7 +6,8 @@
 namespace presk {
 
 enum RowOp {
-    kRowMean = 0, kRowSum, kSoftmax3, kSoftmax2, kMaskedSoftmax3, kMaskedSoftmax2, kCrossEntropy, kCrossEntropyVjp
+    kRowMean = 0, kRowSum, kSoftmax3, kSoftmax2, kMaskedSoftmax3, kMaskedSoftmax2, kCrossEntropy, kCrossEntropyVjp,
+    kSumToRows
 };
 
 struct RowArgs {

@@ -4,7 +4,8 @@ order: the reference's `ReductionOrder::Chunked { size: 64 }` semantics
 summed from zero in order, the chunk sums added in order from zero) with f32
 accumulation.  The same order is written here as a PSK-Kernel nest and run by
 the oracle; the device must give its bits exactly.  Also the row-nest class
-at sizes beyond the zoo's, bit-exact against the oracle."""
+at sizes beyond the zoo's, and the token scatter of `embed_vjp` over several
+scan rounds, bit-exact against the oracle."""
 import numpy as np
 import pytest
 
@@ -63,6 +64,7 @@ def _big_rows(dt):
         ("mean", L.reduce_axis("mean", "vocab", [logits], dt)),
         ("cross_entropy", L.cross_entropy([logits, ids], dt)),
         ("cross_entropy_vjp", L.cross_entropy_vjp([logits, ids, rows], dt)),
+        ("sum_to_rows", L.sum_to([logits, rows], dt)),
     ]
 
 
@@ -83,3 +85,27 @@ def test_rows_class_exact_at_size(dt):
         c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
         assert c.kind == "rows", (name, c.kind)
         assert out.download(np.uint8, nbytes).tobytes() == want.view(np.uint8).tobytes(), name
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("ids", ["spread", "one_row"])
+def test_scatter_class_exact_at_size(dt, ids):
+    """embed_vjp over 4500 tokens (three scan rounds of 2048) into a 7 x 300
+    table (a partial column block); with every token naming one row, a round's
+    whole list is that row's."""
+    B, T, V, D = 3, 1500, 7, 300
+    tok = O(A(("vocab", V), ("model", D)))
+    idx = O(A(("batch", B), ("seq", T)), "idx")
+    ct = O(A(("batch", B), ("seq", T), ("model", D)))
+    low = L.embed_vjp([tok, idx, ct], dt)
+    ins = zoo.inputs(low, seed=23)
+    if ids == "one_row":
+        ins[1] = np.full(B * T, 3, np.int64)
+    want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes)
+    ex = hip.HipExec(0, mode=hip.EXACT)
+    nbytes = V * D * hip.STORAGE_BYTES[dt]
+    out = hip.DeviceBuffer(nbytes)
+    out.upload(np.full(nbytes, 0xFF, np.uint8))
+    c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+    assert c.kind == "scatter", c.kind
+    assert out.download(np.uint8, nbytes).tobytes() == want.view(np.uint8).tobytes()

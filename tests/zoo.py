@@ -56,6 +56,7 @@ def _gpt_like(dt, B=2, T=8, D=16, H=2, V=11):
         "cross_entropy": L.cross_entropy([logits, ids], dt),
         "cross_entropy_vjp": L.cross_entropy_vjp([logits, ids, rows], dt),
         "sum_to": L.sum_to([x, b], dt),
+        "sum_to_rows": L.sum_to([x, rows], dt),
         "mean_vjp": L.mean_vjp("model", [rows, x], dt),
         "split_heads": L.split_heads(H, hd, [x], dt),
         "merge_heads": L.merge_heads(H, hd, [q], dt),
