@@ -129,7 +129,8 @@ def main():
     rec = {"metric": METRIC, "value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,1) inputs, xavier weights)",
-           "config": cfg, "matmul_tflops": round(flops / (ms_step * 1e-3) / 1e12, 2), "roofline": roof,
+           "config": cfg, "matmul_tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
+           "matmul_frac_of_peak": round(flops / (ms_step * 1e-3) / 1e12 / PEAK_TFLOPS[dtype], 4), "roofline": roof,
            "kernels": per_kernel}
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)

@@ -414,6 +414,7 @@ std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
     if (p->a.rows < 256 || p->a.cols == 0) return nullptr;   // short sums: the interpreter's order is fast enough
     p->a.chunk = 64;
     p->a.nchunks = (p->a.rows + p->a.chunk - 1) / p->a.chunk;
+    if (p->a.nchunks > 65535) return nullptr;  // one grid row per chunk
     p->a.storage = st;
     p->guarded = k.guarded();
     return p;

@@ -19,46 +19,63 @@ namespace presk {
 
 namespace {
 
-template <typename S>
-__device__ __forceinline__ float widen(const S* p, long long i);
-template <>
-__device__ __forceinline__ float widen<float>(const float* p, long long i) { return p[i]; }
-template <>
-__device__ __forceinline__ float widen<unsigned short>(const unsigned short* p, long long i) { return pk_bf16_to_f32(p[i]); }
-
-// one thread per (chunk, column): the chunk's rows summed in order
 template <int ST>
-__global__ void __launch_bounds__(256) colsum_chunks(ColSumArgs a) {
-    const long long col = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ float ld(const void* p, long long i) {
+    if (ST == 0) return ((const float*)p)[i];
+    if (ST == 1) return pk_bf16_to_f32(((const unsigned short*)p)[i]);
+    return pk_f16_to_f32(((const unsigned short*)p)[i]);
+}
+
+// one lane per (chunk, column): the chunk's rows summed in order, all of a
+// full chunk's loads in flight before the first add
+template <int ST>
+__global__ void __launch_bounds__(64) colsum_chunks(ColSumArgs a) {
+    const long long col = (long long)blockIdx.x * 64 + threadIdx.x;
     const long long ch = blockIdx.y;
     if (col >= a.cols) return;
     const long long r0 = ch * a.chunk;
-    long long r1 = r0 + a.chunk;
-    if (r1 > a.rows) r1 = a.rows;
     float part = 0.f;
-    if (ST == 0) {
-        const float* x = (const float*)a.x;
-#pragma unroll 8
-        for (long long r = r0; r < r1; ++r) part = part + x[r * a.cols + col];
-    } else if (ST == 1) {
-        const unsigned short* x = (const unsigned short*)a.x;
-#pragma unroll 8
-        for (long long r = r0; r < r1; ++r) part = part + pk_bf16_to_f32(x[r * a.cols + col]);
+    if (a.chunk == 64 && r0 + 64 <= a.rows) {
+        float v[64];
+#pragma unroll
+        for (int i = 0; i < 64; ++i) v[i] = ld<ST>(a.x, (r0 + i) * a.cols + col);
+#pragma unroll
+        for (int i = 0; i < 64; ++i) part = part + v[i];
     } else {
-        const unsigned short* x = (const unsigned short*)a.x;
-#pragma unroll 8
-        for (long long r = r0; r < r1; ++r) part = part + pk_f16_to_f32(x[r * a.cols + col]);
+        long long r1 = r0 + a.chunk;
+        if (r1 > a.rows) r1 = a.rows;
+        for (long long r = r0; r < r1; ++r) part = part + ld<ST>(a.x, r * a.cols + col);
     }
     a.work[ch * a.cols + col] = part;
 }
 
-// the chunk sums added in chunk order from zero, then one store
+// the chunk sums added in chunk order from zero, then one store: four waves
+// stage SEG chunk sums of 64 columns in LDS, lane c of wave 0 adds them in order
+constexpr int SEG = 128;
+
 template <int ST>
 __global__ void __launch_bounds__(256) colsum_total(ColSumArgs a) {
-    const long long col = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (col >= a.cols) return;
+    __shared__ float part[SEG][65];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long col = (long long)blockIdx.x * 64 + lane;
+    const bool live = col < a.cols;
     float acc = 0.f;
-    for (long long ch = 0; ch < a.nchunks; ++ch) acc = acc + a.work[ch * a.cols + col];
+    for (long long c0 = 0; c0 < a.nchunks; c0 += SEG) {
+        const int n = (int)(a.nchunks - c0 < SEG ? a.nchunks - c0 : SEG);
+        float v[SEG / 4];
+#pragma unroll
+        for (int i = 0; i < SEG / 4; ++i) {
+            const int c = i * 4 + w;
+            v[i] = live && c < n ? a.work[(c0 + c) * a.cols + col] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < SEG / 4; ++i) part[i * 4 + w][lane] = v[i];
+        __syncthreads();
+        if (w == 0)
+            for (int c = 0; c < n; ++c) acc = acc + part[c][lane];
+        __syncthreads();
+    }
+    if (w != 0 || !live) return;
     if (ST == 0) {
         ((float*)a.out)[col] = acc;
     } else if (ST == 1) {
@@ -72,12 +89,14 @@ __global__ void __launch_bounds__(256) colsum_total(ColSumArgs a) {
 }  // namespace
 
 hipError_t colsum_launch(const ColSumArgs& a, hipStream_t stream) {
-    const unsigned bx = (unsigned)((a.cols + 255) / 256);
+    if (a.cols == 0) return hipSuccess;
+    if (a.nchunks > 65535) return hipErrorInvalidValue;
+    const unsigned bx = (unsigned)((a.cols + 63) / 64);
     dim3 g1(bx, (unsigned)a.nchunks);
     switch (a.storage) {
-        case 0: colsum_chunks<0><<<g1, 256, 0, stream>>>(a); break;
-        case 1: colsum_chunks<1><<<g1, 256, 0, stream>>>(a); break;
-        case 2: colsum_chunks<2><<<g1, 256, 0, stream>>>(a); break;
+        case 0: colsum_chunks<0><<<g1, 64, 0, stream>>>(a); break;
+        case 1: colsum_chunks<1><<<g1, 64, 0, stream>>>(a); break;
+        case 2: colsum_chunks<2><<<g1, 64, 0, stream>>>(a); break;
         default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();

@@ -12,8 +12,10 @@
 // parks the chunk in LDS, where lane i walks row i in index order -- the
 // interpreter's sequential sum, bit for bit.  Passes that only write (the
 // last pass of a softmax, the vjp) stay in the coalesced layout throughout,
-// with the row's max and sum read from the walking lane.  Each pass of the
-// nest over its row reads the row again, as the nest does.
+// with the row's max and sum read from the walking lane.  A row of at most
+// four chunks is loaded once and kept in registers for all the nest's passes
+// (the nest reads the same values each pass); a longer row is read again at
+// each pass, as the nest does.
 #include <hip/hip_runtime.h>
 
 #include "devfmt.hpp"
@@ -23,8 +25,8 @@ namespace presk {
 
 namespace {
 
-constexpr int R = 16;   // rows per wave (one wave per workgroup)
-constexpr int CW = 64;  // columns per chunk, one per lane
+constexpr int CW = 64;     // columns per chunk, one per lane
+constexpr int NRES = 4;    // rows of at most NRES chunks stay in registers for every pass
 
 template <int ST>
 __device__ __forceinline__ float ld(const void* p, long long i) {
@@ -59,17 +61,19 @@ __device__ __forceinline__ float from_lane(float v, int i) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
 }
 
-template <int OP, int ST>
+// R rows per wave (one wave per workgroup); RES: the row fits in NRES chunks,
+// loaded once and kept in registers across the nest's passes
+template <int OP, int ST, int R, bool RES>
 __global__ void __launch_bounds__(64) rows_kernel(RowArgs a) {
     constexpr bool MASKED = OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2;
     __shared__ float tile[R][CW + 1];
-    __shared__ unsigned char mtile[MASKED ? R : 1][MASKED ? CW + 4 : 1];
     const int lane = threadIdx.x;
     const long long row0 = (long long)blockIdx.x * R;
     const long long n = a.n;
     const int nr = (int)(a.rows - row0 < R ? a.rows - row0 : R);  // live rows here
     const bool walker = lane < nr;
     const long long r = row0 + lane;  // the walking lane's row
+    const float qnan = __int_as_float(0x7fc00000);
     bool ovf = false;
 
     // the mask row of each of the R rows (the mask repeats over leading axes)
@@ -83,90 +87,147 @@ __global__ void __launch_bounds__(64) rows_kernel(RowArgs a) {
         }
     }
 
-    // x[row0 + i][c0 + lane] for every row, and whether the mask allows it
-    auto load = [&](long long c0, int cw, float (&v)[R], bool (&al)[R]) {
-        const bool col = lane < cw;
+    // x[row0 + i][c0 + lane] for every row, and the mask's verdicts as bits
+    // (bit i: row i).  Addresses are clamped into the rows and the chunk, so
+    // every load is issued unconditionally and all are in flight together;
+    // a clamped lane's values are never used.
+    auto load = [&](long long c0, int cw, float (&v)[R], unsigned& mb) {
+        const long long col = c0 + (lane < cw ? lane : cw - 1);
 #pragma unroll
-        for (int i = 0; i < R; ++i) v[i] = col && i < nr ? ld<ST>(a.x, (row0 + i) * n + c0 + lane) : 0.f;
+        for (int i = 0; i < R; ++i) v[i] = ld<ST>(a.x, (row0 + (i < nr ? i : nr - 1)) * n + col);
         if (MASKED) {
             const long long* mask = (const long long*)a.mask;
+            long long mv[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) mv[i] = mask[moff[i] + col];
+            unsigned b = 0;
 #pragma unroll
             for (int i = 0; i < R; ++i)
                 // allowed: real(mask) > 0.5 in the nest's f32
-                al[i] = col && i < nr ? (float)(double)mask[moff[i] + c0 + lane] > 0.5f : false;
+                b |= ((float)(double)mv[i] > 0.5f ? 1u : 0u) << i;
+            mb = lane < cw ? b & ((1u << nr) - 1u) : 0u;
         }
     };
     // lane i walks tile row i over columns [0, cw) in order
     auto walk = [&](int cw, auto&& f) {
         __syncthreads();
-        if (walker)
-            for (int j = 0; j < cw; ++j) f(tile[lane][j], MASKED ? mtile[lane][j] != 0 : true);
+        if (walker) {
+#pragma unroll 8
+            for (int j = 0; j < cw; ++j) f(tile[lane][j]);
+        }
         __syncthreads();
     };
-    // a reduction pass: the chunk transformed elementwise, then walked
-    auto reduce_pass = [&](auto&& elem, auto&& f) {
-        for (long long c0 = 0; c0 < n; c0 += CW) {
-            const int cw = (int)(n - c0 < CW ? n - c0 : CW);
-            float v[R];
-            bool al[R];
-            load(c0, cw, v, al);
+    // the row's chunks: resident ones loaded once here, others at each pass
+    constexpr int NV = RES ? NRES : 1;
+    float v[NV][R];
+    unsigned mb[NV];
+    auto for_chunks = [&](auto&& body) {
+        if constexpr (RES) {
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                tile[i][lane] = elem(i, v[i], al[i]);
-                if (MASKED) mtile[i][lane] = al[i] ? 1 : 0;
+            for (int ch = 0; ch < NRES; ++ch)
+                if (ch * CW < n) body(ch, (long long)ch * CW, (int)(n - ch * CW < CW ? n - ch * CW : CW));
+        } else {
+            for (long long c0 = 0; c0 < n; c0 += CW) {
+                const int cw = (int)(n - c0 < CW ? n - c0 : CW);
+                load(c0, cw, v[0], mb[0]);
+                body(0, c0, cw);
             }
-            walk(cw, f);
         }
+    };
+    if constexpr (RES) {
+#pragma unroll
+        for (int ch = 0; ch < NRES; ++ch)
+            if (ch * CW < n) load(ch * CW, (int)(n - ch * CW < CW ? n - ch * CW : CW), v[ch], mb[ch]);
+    }
+    auto allowed = [&](int ch, int i) { return MASKED ? ((mb[ch] >> i) & 1u) != 0 : true; };
+    // a reduction pass: each element transformed in the coalesced layout
+    // (elem may rewrite a resident value), then the chunk walked in order
+    auto reduce_pass = [&](auto&& elem, auto&& f) {
+        for_chunks([&](int ch, long long, int cw) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) tile[i][lane] = elem(i, v[ch][i], allowed(ch, i));
+            walk(cw, f);
+        });
     };
     // a write pass: out[row0 + i][k] = g(i, k, value, allowed), coalesced
     auto write_pass = [&](auto&& g) {
-        for (long long c0 = 0; c0 < n; c0 += CW) {
-            const int cw = (int)(n - c0 < CW ? n - c0 : CW);
-            float v[R];
-            bool al[R];
-            load(c0, cw, v, al);
+        for_chunks([&](int ch, long long c0, int cw) {
             if (lane < cw) {
 #pragma unroll
                 for (int i = 0; i < R; ++i)
-                    if (i < nr) st<ST>(a.out, (row0 + i) * n + c0 + lane, g(i, c0 + lane, v[i], al[i]), ovf);
+                    if (i < nr) st<ST>(a.out, (row0 + i) * n + c0 + lane, g(i, c0 + lane, v[ch][i], allowed(ch, i)), ovf);
             }
-        }
+        });
     };
-    auto same = [](int, float v, bool) { return v; };
+    auto same = [](int, float& v, bool) { return v; };
 
     if (OP == kRowMean || OP == kRowSum) {
         float acc = 0.f;
-        reduce_pass(same, [&](float v, bool) { acc = acc + v; });
+        reduce_pass(same, [&](float x) { acc = acc + x; });
         if (walker) st<ST>(a.out, r, OP == kRowMean ? acc / a.n_real : acc, ovf);
     } else if (OP == kSumToRows) {
         // the running sum lives in the output: every step stored (rounded)
         float acc = 0.f;
-        reduce_pass(same, [&](float v, bool) {
-            const float s = acc + v;
+        reduce_pass(same, [&](float x) {
+            const float s = acc + x;
             if (ST == 2) ovf |= pk_overflows_f16(s);
             acc = stored<ST>(s);
         });
         if (walker) st<ST>(a.out, r, acc, ovf);
-    } else if (OP == kSoftmax3 || OP == kSoftmax2 || OP == kCrossEntropy || OP == kCrossEntropyVjp) {
+    } else {
         if (n == 0) return;
-        float m = walker ? ld<ST>(a.x, r * n) : 0.f;
-        reduce_pass(same, [&](float v, bool) { if (v > m) m = v; });
+        float m;
+        if (!MASKED) {
+            // m = x[0]; then m = x[k] wherever x[k] > m
+            m = walker ? ld<ST>(a.x, r * n) : 0.f;
+            reduce_pass(same, [&](float x) { m = x > m ? x : m; });
+        } else {
+            // The nest's masked max: the first allowed element, then any
+            // later allowed one greater than the running max.  Walked as the
+            // plain max from -inf over the allowed elements (a disallowed one
+            // walks as NaN, which is never greater), which agrees except when
+            // the first allowed element is NaN (the nest's max is then NaN)
+            // or none is allowed (the nest's max stays 0): both found here by
+            // ballots over the chunks in order.
+            unsigned found = 0, nanfirst = 0;  // bit i: row i
+            m = -__builtin_inff();
+            reduce_pass([&](int i, float& x, bool al) {
+                const unsigned long long A = __ballot(al), N = __ballot(al && x != x);
+                if (!((found >> i) & 1u) && A) {
+                    found |= 1u << i;
+                    if (N & (A & (~A + 1ull))) nanfirst |= 1u << i;
+                }
+                return al ? x : qnan;
+            }, [&](float x) { m = x > m ? x : m; });
+            m = ((nanfirst >> lane) & 1u) ? qnan : ((found >> lane) & 1u) ? m : 0.f;
+        }
         float mi[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) mi[i] = from_lane(m, i);
+        // the exponentials: a resident row keeps them for the write pass (the
+        // nest computes the same exp(x - m) there)
         float z = 0.f;
-        reduce_pass([&](int i, float v, bool) { return pk_expf(v - mi[i]); }, [&](float e, bool) { z = z + e; });
+        reduce_pass([&](int i, float& x, bool al) {
+            const float e = al ? pk_expf(x - mi[i]) : 0.f;
+            if (RES) x = e;
+            return e;
+        }, [&](float e) { z = z + e; });
+        auto expo = [&](int i, float x, bool al) -> float {
+            if (RES) return x;
+            return al ? pk_expf(x - mi[i]) : 0.f;
+        };
         float zi[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) zi[i] = from_lane(z, i);
-        if (OP == kSoftmax3) {
-            write_pass([&](int i, long long, float v, bool) { return pk_expf(v - mi[i]) / zi[i]; });
-        } else if (OP == kSoftmax2) {
-            // the stored exponential over z (the first pass's stores are overwritten)
-            write_pass([&](int i, long long, float v, bool) {
-                const float e = pk_expf(v - mi[i]);
+        if (OP == kSoftmax3 || OP == kMaskedSoftmax3) {
+            write_pass([&](int i, long long, float x, bool al) { return al ? expo(i, x, al) / zi[i] : 0.f; });
+        } else if (OP == kSoftmax2 || OP == kMaskedSoftmax2) {
+            // the stored exponential over z (the first pass's stores of e,
+            // guarded, are overwritten)
+            write_pass([&](int i, long long, float x, bool al) {
+                const float e = expo(i, x, al);
                 if (ST == 2) ovf |= pk_overflows_f16(e);
-                return stored<ST>(e) / zi[i];
+                return al ? stored<ST>(e) / zi[i] : 0.f;
             });
         } else if (OP == kCrossEntropy) {
             if (walker) {
@@ -182,53 +243,40 @@ __global__ void __launch_bounds__(64) rows_kernel(RowArgs a) {
                 cti[i] = from_lane(ct, i);
                 fyi[i] = from_lane(fy, i);
             }
-            write_pass([&](int i, long long k, float v, bool) {
-                const float sm = pk_expf(v - mi[i]) / zi[i];
+            write_pass([&](int i, long long k, float x, bool al) {
+                const float sm = expo(i, x, al) / zi[i];
                 const float onehot = (float)(double)k == fyi[i] ? 1.f : 0.f;
                 return (sm - onehot) * cti[i];
-            });
-        }
-    } else if (MASKED) {
-        if (n == 0) return;
-        float first = 1.f, mx = 0.f;
-        reduce_pass(same, [&](float v, bool al) {
-            mx = al ? (first > 0.5f ? v : (v > mx ? v : mx)) : mx;
-            first = al ? 0.f : first;
-        });
-        float mi[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) mi[i] = from_lane(mx, i);
-        float z = 0.f;
-        reduce_pass([&](int i, float v, bool al) { return al ? pk_expf(v - mi[i]) : 0.f; },
-                    [&](float e, bool) { z = z + e; });
-        float zi[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) zi[i] = from_lane(z, i);
-        if (OP == kMaskedSoftmax3) {
-            write_pass([&](int i, long long, float v, bool al) { return al ? pk_expf(v - mi[i]) / zi[i] : 0.f; });
-        } else {
-            write_pass([&](int i, long long, float v, bool al) {
-                const float e = al ? pk_expf(v - mi[i]) : 0.f;
-                if (ST == 2) ovf |= pk_overflows_f16(e);
-                return al ? stored<ST>(e) / zi[i] : 0.f;
             });
         }
     }
     if (ovf && a.flag) atomicOr(a.flag, 1u);
 }
 
+template <int OP, int R, bool RES>
+hipError_t launch_r(const RowArgs& a, hipStream_t stream) {
+    const unsigned grid = (unsigned)((a.rows + R - 1) / R);
+    switch (a.storage) {
+        case 0: rows_kernel<OP, 0, R, RES><<<grid, 64, 0, stream>>>(a); break;
+        case 1: rows_kernel<OP, 1, R, RES><<<grid, 64, 0, stream>>>(a); break;
+        case 2: rows_kernel<OP, 2, R, RES><<<grid, 64, 0, stream>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Rows per wave: a walk costs the same issue slots however many of its
+// lanes are live, so 16 rows a wave -- unless that leaves fewer waves than
+// SIMDs (under 8192 rows), when 4 rows a wave spreads the walks wider.
 template <int OP>
 hipError_t launch_op(const RowArgs& a, hipStream_t stream) {
     if (a.rows == 0) return hipSuccess;
     if ((OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2) && a.mask_rows <= 0) return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)((a.rows + R - 1) / R);
-    switch (a.storage) {
-        case 0: rows_kernel<OP, 0><<<grid, 64, 0, stream>>>(a); break;
-        case 1: rows_kernel<OP, 1><<<grid, 64, 0, stream>>>(a); break;
-        case 2: rows_kernel<OP, 2><<<grid, 64, 0, stream>>>(a); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if ((a.rows + 3) / 4 > 0x7fffffffll) return hipErrorInvalidValue;
+    const bool res = a.n <= NRES * CW;
+    if (a.rows >= 8192)
+        return res ? launch_r<OP, 16, true>(a, stream) : launch_r<OP, 16, false>(a, stream);
+    return res ? launch_r<OP, 4, true>(a, stream) : launch_r<OP, 4, false>(a, stream);
 }
 
 }  // namespace

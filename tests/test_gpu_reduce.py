@@ -68,6 +68,42 @@ def _big_rows(dt):
     ]
 
 
+def _long_rows(dt):
+    """rows longer than the four register-resident chunks (300 columns), and
+    enough rows for sixteen rows a wave (65536)"""
+    wide = O(A(("batch", 7), ("seq", 30), ("vocab", 300)))
+    wide_rows = O(A(("batch", 7), ("seq", 30)))
+    T = 256
+    tall = O(A(("batch", 16), ("heads", 16), ("seq", T), ("seq2", T)))
+    mask = O(A(("seq", T), ("seq2", T)), "idx")
+    tall_wide = O(A(("batch", 1024), ("seq", 64), ("vocab", 300)))
+    return [
+        ("softmax", L.softmax("vocab", [wide], dt)),
+        ("mean", L.reduce_axis("mean", "vocab", [wide], dt)),
+        ("sum_to_rows", L.sum_to([wide, wide_rows], dt)),
+        ("masked_softmax", L.masked_softmax("seq2", [tall, mask], dt)),
+        ("softmax2", L.softmax_two_pass("vocab", [tall_wide], dt)),
+    ]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_rows_class_exact_long_and_many(dt):
+    ex = hip.HipExec(0, mode=hip.EXACT)
+    from oracle import kernel_text as kt
+    for name, low in _long_rows(dt):
+        ins = zoo.inputs(low, seed=13, scale=2.0)
+        if name == "masked_softmax":
+            ins[1] = np.tril(np.ones((256, 256), np.int64)).ravel()
+        want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes, threads=8)
+        k = kt.parse_kernel(low.text)
+        nbytes = k.output.numel * hip.STORAGE_BYTES[dt]
+        out = hip.DeviceBuffer(nbytes)
+        out.upload(np.full(nbytes, 0xFF, np.uint8))
+        c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+        assert c.kind == "rows", (name, c.kind)
+        assert out.download(np.uint8, nbytes).tobytes() == want.view(np.uint8).tobytes(), name
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 def test_rows_class_exact_at_size(dt):
     ex = hip.HipExec(0, mode=hip.FAST)
@@ -109,3 +145,46 @@ def test_scatter_class_exact_at_size(dt, ids):
     c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
     assert c.kind == "scatter", c.kind
     assert out.download(np.uint8, nbytes).tobytes() == want.view(np.uint8).tobytes()
+
+
+def _same_bits_nan_as_nan(got, want, dt):
+    """bit-identical, except that any NaN matches any NaN (payloads of NaN
+    arithmetic are not fixed by IEEE 754)"""
+    g, w = fmt.decode(got, dt), fmt.decode(want, dt)
+    gn, wn = np.isnan(g), np.isnan(w)
+    assert (gn == wn).all(), np.argwhere(gn != wn)[:5]
+    assert got.view(np.uint8).reshape(got.shape[0], -1)[~gn].tobytes() == want.view(np.uint8).reshape(want.shape[0], -1)[~wn].tobytes()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_rows_class_nan_and_empty_rows(dt):
+    """the masked max's corner cases: a NaN first allowed element (the max is
+    NaN), a NaN later allowed element and a NaN disallowed one (both passed
+    over), -inf first, and a row the mask allows nowhere (all zeros)"""
+    B, H, T = 2, 3, 40
+    s = O(A(("batch", B), ("heads", H), ("seq", T), ("seq2", T)))
+    mask = O(A(("seq", T), ("seq2", T)), "idx")
+    ex = hip.HipExec(0, mode=hip.EXACT)
+    from oracle import kernel_text as kt
+    for low in (L.masked_softmax("seq2", [s, mask], dt), L.masked_softmax("seq2", [s, mask], dt, two_passes=True),
+                L.softmax("seq2", [s], dt)):
+        ins = zoo.inputs(low, seed=3)
+        x = fmt.decode(ins[0], dt).reshape(B, H, T, T).copy()
+        x[0, 0, 7, 0] = np.nan
+        x[0, 1, 9, 4] = np.nan
+        x[1, 2, 3, 20] = np.nan
+        x[1, 0, 10, 0] = -np.inf
+        x[1, 1, 12, 0] = np.nan if len(ins) == 1 else x[1, 1, 12, 0]
+        ins[0] = fmt.encode(x.astype(np.float32), dt)
+        if len(ins) == 2:
+            m = np.tril(np.ones((T, T), np.int64))
+            m[5, :] = 0
+            ins[1] = m.ravel()
+        want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes)
+        k = kt.parse_kernel(low.text)
+        nbytes = k.output.numel * hip.STORAGE_BYTES[dt]
+        out = hip.DeviceBuffer(nbytes)
+        c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+        assert c.kind == "rows", c.kind
+        got = out.download(want.dtype, want.size).reshape(want.shape)
+        _same_bits_nan_as_nan(got, want, dt)
