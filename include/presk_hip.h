@@ -124,6 +124,25 @@ int presk_hip_stream_destroy(void *stream);
 int presk_hip_time(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi, void *stream, int warmup,
                    int reps, double *ms_per_launch);
 
+/* A recorded launch sequence: a function body's kernels in the order the
+ * host's call loop issues them (crates/presk-kernel/src/host.rs:887-1030 runs
+ * each `let` of the body as one or more launches through `KernelExec::run`).
+ * No counterpart in the reference's interface: a host that calls the same
+ * body again and again (a training loop, a serving loop) records it once and
+ * replays it.  `presk_hip_batch_add` copies the kernel's pointer table (its
+ * inputs, output and, for a guarded kernel, the flag); the kernels and
+ * buffers must outlive the batch.  `presk_hip_batch_graph` makes every later
+ * `presk_hip_batch_run` one HIP graph launch of the whole sequence (lazy
+ * module loads and workspaces are done first, outside the capture, and
+ * nothing the sequence launches is a memset); without it each run issues the
+ * launches one by one.  Adding a launch discards the graph. */
+typedef struct presk_hip_batch presk_hip_batch;
+int presk_hip_batch_create(presk_hip_batch **out);
+int presk_hip_batch_add(presk_hip_batch *b, const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi);
+int presk_hip_batch_graph(presk_hip_batch *b);
+int presk_hip_batch_run(presk_hip_batch *b, void *stream);
+void presk_hip_batch_release(presk_hip_batch *b);
+
 /* Self-test of the device's scalar functions over a domain block: the digest
  * (sum of splitmix64 finalizers of (i << 32 | out_i)) of function `fn` over
  * inputs [lo, hi), as tests/golden/digests.json holds the reference's.  No

@@ -179,6 +179,18 @@ struct GemmPlan : ClassPlan {
         return gemm_launch(a, stream);
     }
 
+    hipError_t prepare() const override {
+        if (g.splits <= 1) return hipSuccess;
+        const size_t need = (size_t)g.splits * g.M * g.N;
+        if (need <= work_floats) return hipSuccess;
+        if (work) hipFree(work);
+        work = nullptr;
+        work_floats = 0;
+        hipError_t e = hipMalloc(&work, need * sizeof(float));
+        if (e == hipSuccess) work_floats = need;
+        return e;
+    }
+
     ~GemmPlan() override {
         if (work) hipFree(work);
     }
@@ -385,12 +397,14 @@ struct ColSumPlan : ClassPlan {
         x.x = bufs[0];
         x.out = bufs[2];
         x.flag = guarded ? (unsigned*)bufs[3] : nullptr;
-        if (!work) {
-            hipError_t e = hipMalloc(&work, sizeof(float) * (size_t)(a.nchunks * a.cols));
-            if (e != hipSuccess) return e;
-        }
+        hipError_t e = prepare();
+        if (e != hipSuccess) return e;
         x.work = work;
         return colsum_launch(x, stream);
+    }
+    hipError_t prepare() const override {
+        if (work) return hipSuccess;
+        return hipMalloc(&work, sizeof(float) * (size_t)(a.nchunks * a.cols));
     }
     ~ColSumPlan() override {
         if (work) hipFree(work);

@@ -19,6 +19,9 @@ struct ClassPlan {
     virtual const char* kind() const = 0;
     virtual std::string order() const = 0;
     virtual hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, hipStream_t stream) const = 0;
+    // allocate what a full-range launch would allocate on first use (its
+    // workspace), so that a recorded sequence can be captured into a graph
+    virtual hipError_t prepare() const { return hipSuccess; }
 };
 
 // The hand-written kernel for `k` under `mode` (PRESK_HIP_EXACT/FAST), or

@@ -215,6 +215,41 @@ int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, 
     return PRESK_HIP_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// What a kernel's first launch would set up: the generic kernel's module, a
+// class kernel's workspace.
+int prepare_kernel(const presk_hip_kernel* h) {
+    if (h->plan) {
+        hipError_t e = h->plan->prepare();
+        return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
+    }
+    if (!h->module) {
+        hipModule_t m = nullptr;
+        hipError_t e = hipModuleLoadData(&m, h->code.data());
+        if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
+        std::vector<hipFunction_t> fns;
+        for (auto& ph : h->gen.phases) {
+            hipFunction_t f;
+            e = hipModuleGetFunction(&f, m, ph.fn.c_str());
+            if (e != hipSuccess) {
+                hipModuleUnload(m);
+                return hip_fail(e, "hipModuleGetFunction");
+            }
+            fns.push_back(f);
+        }
+        h->module = m;
+        h->fns = std::move(fns);
+    }
+    return PRESK_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int presk_hip_run(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int64_t hi, void* stream) {
     if (!h || !bufs) return fail(PRESK_HIP_ERR, "E10001: null argument");
     hipStream_t s = (hipStream_t)stream;
@@ -222,16 +257,7 @@ int presk_hip_run(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int6
         hipError_t e = h->plan->launch(bufs, lo, hi, s);
         return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
     }
-    if (!h->module) {
-        hipError_t e = hipModuleLoadData(&h->module, h->code.data());
-        if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
-        for (auto& ph : h->gen.phases) {
-            hipFunction_t f;
-            e = hipModuleGetFunction(&f, h->module, ph.fn.c_str());
-            if (e != hipSuccess) return hip_fail(e, "hipModuleGetFunction");
-            h->fns.push_back(f);
-        }
-    }
+    if (int rc = prepare_kernel(h)) return rc;
     const Kernel& k = *h->k;
     PhaseArgs args{};
     const int nb = (int)k.inputs.size() + 1;
@@ -354,6 +380,92 @@ int presk_hip_time(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int
     *ms_per_launch = (double)ms / reps;
     return PRESK_HIP_OK;
 }
+
+}  // extern "C"
+
+struct presk_hip_batch {
+    struct Item {
+        const presk_hip_kernel* k;
+        std::vector<void*> bufs;
+        int64_t lo, hi;
+    };
+    std::vector<Item> items;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    void drop_graph() {
+        if (exec) hipGraphExecDestroy(exec);
+        if (graph) hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+    }
+    int run_each(hipStream_t s) const {
+        for (const Item& it : items)
+            if (int rc = presk_hip_run(it.k, it.bufs.data(), it.lo, it.hi, s)) return rc;
+        return PRESK_HIP_OK;
+    }
+    ~presk_hip_batch() { drop_graph(); }
+};
+
+extern "C" {
+
+int presk_hip_batch_create(presk_hip_batch** out) {
+    if (!out) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    *out = new presk_hip_batch();
+    return PRESK_HIP_OK;
+}
+
+int presk_hip_batch_add(presk_hip_batch* b, const presk_hip_kernel* k, void* const* bufs, int64_t lo, int64_t hi) {
+    if (!b || !k || !bufs) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    const size_t n = k->k->inputs.size() + 1 + (k->k->guarded() ? 1 : 0);
+    b->drop_graph();
+    b->items.push_back({k, std::vector<void*>(bufs, bufs + n), lo, hi});
+    return PRESK_HIP_OK;
+}
+
+int presk_hip_batch_graph(presk_hip_batch* b) {
+    if (!b) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    b->drop_graph();
+    for (const auto& it : b->items)
+        if (int rc = prepare_kernel(it.k)) return rc;
+    hipStream_t cs = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
+    e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        hipStreamDestroy(cs);
+        return hip_fail(e, "hipStreamBeginCapture");
+    }
+    const int rc = b->run_each(cs);
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(cs, &g);  // ended whatever the launches returned
+    hipStreamDestroy(cs);
+    if (rc) {
+        if (g) hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(g);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    b->graph = g;
+    b->exec = x;
+    return PRESK_HIP_OK;
+}
+
+int presk_hip_batch_run(presk_hip_batch* b, void* stream) {
+    if (!b) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    if (b->exec) {
+        hipError_t e = hipGraphLaunch(b->exec, (hipStream_t)stream);
+        return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "hipGraphLaunch");
+    }
+    return b->run_each((hipStream_t)stream);
+}
+
+void presk_hip_batch_release(presk_hip_batch* b) { delete b; }
 
 int presk_hip_scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
     hipError_t e = scalar_digest(fn, lo, hi, digest);

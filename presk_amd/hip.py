@@ -24,7 +24,8 @@ STORAGE_BYTES = {"f64": 8, "f32": 4, "bf16": 2, "f16": 2, "e8m15": 3, "i64": 8}
 SYMBOLS = ["presk_hip_init", "presk_hip_last_error", "presk_hip_compile", "presk_hip_run", "presk_hip_kernel_info",
            "presk_hip_release", "presk_hip_kernel_text", "presk_hip_alloc", "presk_hip_free", "presk_hip_h2d", "presk_hip_d2h", "presk_hip_memset",
            "presk_hip_sync", "presk_hip_stream_create", "presk_hip_stream_destroy", "presk_hip_time",
-           "presk_hip_scalar_digest"]
+           "presk_hip_scalar_digest", "presk_hip_batch_create", "presk_hip_batch_add", "presk_hip_batch_graph",
+           "presk_hip_batch_run", "presk_hip_batch_release"]
 
 
 class HipError(RuntimeError):
@@ -73,6 +74,12 @@ def lib():
         L.presk_hip_stream_destroy.argtypes = [vp]
         L.presk_hip_time.argtypes = [vp, ctypes.POINTER(vp), i64, i64, vp, i32, i32, ctypes.POINTER(ctypes.c_double)]
         L.presk_hip_scalar_digest.argtypes = [i32, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
+        L.presk_hip_batch_create.argtypes = [ctypes.POINTER(vp)]
+        L.presk_hip_batch_add.argtypes = [vp, vp, ctypes.POINTER(vp), i64, i64]
+        L.presk_hip_batch_graph.argtypes = [vp]
+        L.presk_hip_batch_run.argtypes = [vp, vp]
+        L.presk_hip_batch_release.argtypes = [vp]
+        L.presk_hip_batch_release.restype = None
         _lib = L
     return _lib
 

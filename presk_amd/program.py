@@ -72,6 +72,7 @@ class Program:
         self.launches: list = []
         self.bufs = Buffers()
         self._flag = None
+        self._batch = None
 
     def add(self, low: L.Lowered, ins: list, out: str) -> str:
         """Appends one launch of `low` reading buffers `ins`, writing `out`."""
@@ -106,8 +107,37 @@ class Program:
         self._flag.zero()
         return self
 
+    def record(self, graph: bool = True):
+        """Hands the prepared launch sequence to the executor: `run` then
+        issues it from one C call, and with `graph` as one HIP graph launch."""
+        lib = hip.lib()
+        self.release_batch()
+        b = ctypes.c_void_p()
+        hip.check(lib.presk_hip_batch_create(ctypes.byref(b)))
+        self._batch = b
+        for ln in self.launches:
+            c = ln.compiled
+            hip.check(lib.presk_hip_batch_add(b, c.handle, ln.table, 0, max(c.split_bound, 0)))
+        if graph:
+            hip.check(lib.presk_hip_batch_graph(b))
+        return self
+
+    def release_batch(self):
+        if self._batch is not None:
+            hip.lib().presk_hip_batch_release(self._batch)
+            self._batch = None
+
+    def __del__(self):
+        try:
+            self.release_batch()
+        except Exception:
+            pass
+
     def run(self, stream=None):
         lib = hip.lib()
+        if self._batch is not None:
+            hip.check(lib.presk_hip_batch_run(self._batch, stream))
+            return
         for ln in self.launches:
             c = ln.compiled
             rc = lib.presk_hip_run(c.handle, ln.table, 0, max(c.split_bound, 0), stream)
