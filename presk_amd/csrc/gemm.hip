@@ -225,6 +225,27 @@ __device__ __forceinline__ void store_out(void* C, long long off, float sum, boo
     }
 }
 
+// The stored value of an output element (as store_out computes it).
+template <int ST>
+__device__ __forceinline__ typename St<ST>::S round_out(float sum, bool has_bias, float bias, bool& ovf) {
+    if constexpr (ST == kF32) {
+        return has_bias ? sum + bias : sum;
+    } else if constexpr (ST == kBF16) {
+        unsigned short h = pk_f32_to_bf16(sum);
+        if (has_bias) h = pk_f32_to_bf16(pk_bf16_to_f32(h) + bias);
+        return h;
+    } else {
+        ovf |= pk_overflows_f16(sum);
+        unsigned short h = pk_f32_to_f16(sum);
+        if (has_bias) {
+            const float v = pk_f16_to_f32(h) + bias;
+            ovf |= pk_overflows_f16(v);
+            h = pk_f32_to_f16(v);
+        }
+        return h;
+    }
+}
+
 template <int ST>
 __device__ __forceinline__ float load_bias(const void* p, long long off) {
     if (ST == kF32) return ((const float*)p)[off];
@@ -238,8 +259,13 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     typedef typename St<ST>::Frag Frag;
     constexpr int BK = St<ST>::BK, LD = BK + St<ST>::PAD, KSTEP = St<ST>::KSTEP, KPL = St<ST>::KPL;
     constexpr int BM = 2 * WM * 16, BN = 2 * WN * 16;
-    __shared__ __attribute__((aligned(16))) S As[2][BM * LD];
-    __shared__ __attribute__((aligned(16))) S Bs[2][BN * LD];
+    // LDS: the double-buffered operand tiles, reused by the epilogue for the
+    // tile's f32 sums
+    constexpr int CLD = BN + 4;
+    constexpr int OPER = 2 * (BM + BN) * LD * (int)sizeof(S), CTILE = BM * CLD * 4;
+    __shared__ __attribute__((aligned(16))) char smem[OPER > CTILE ? OPER : CTILE];
+    S* const As0 = (S*)smem;
+    S* const Bs0 = As0 + 2 * BM * LD;
 
     // tile order: blocks of one XCD (block id mod 8) take consecutive tiles,
     // and tiles go row-group by row-group so that concurrent tiles share A rows
@@ -273,6 +299,8 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < WN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // One k-block ahead: block kt+1 is loaded into registers while block kt
+    // is multiplied out of one LDS buffer, then stored to the other.
     Loader<ST, AK, BM> la;
     Loader<ST, BK_, BN> lb;
     const int nk = (kend - kbeg + BK - 1) / BK;
@@ -287,16 +315,16 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     };
     if (nk > 0) {
         fetch(kbeg);
-        la.store(As[0]);
-        lb.store(Bs[0]);
+        la.store(As0);
+        lb.store(Bs0);
     }
     __syncthreads();
     const int frow = lane & 15, fk = (lane >> 4) * KPL;
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < nk) fetch(kbeg + (kt + 1) * BK);
-        const S* as = As[cur];
-        const S* bs = Bs[cur];
+        const S* as = As0 + cur * BM * LD;
+        const S* bs = Bs0 + cur * BN * LD;
 #pragma unroll
         for (int kk = 0; kk < BK; kk += KSTEP) {
             Frag a[WM], b[WN];
@@ -310,35 +338,77 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
                 for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
         }
         if (kt + 1 < nk) {
-            la.store(As[cur ^ 1]);
-            lb.store(Bs[cur ^ 1]);
+            la.store(As0 + (cur ^ 1) * BM * LD);
+            lb.store(Bs0 + (cur ^ 1) * BN * LD);
         }
         __syncthreads();
     }
 
-    // the tile's outputs: lane holds column (lane & 15), rows 4*(lane >> 4) + r
+    // The tile's sums go through LDS (lane holds column lane & 15, rows
+    // 4*(lane >> 4) + r of each 16x16 tile) so that each thread then stores
+    // 16 contiguous bytes of one output row.
+    __syncthreads();
+    float* const cs = (float*)smem;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cs[(wm + i * 16 + (lane >> 4) * 4 + r) * CLD + wn + j * 16 + (lane & 15)] = acc[i][j][r];
+    __syncthreads();
+
+    constexpr int OV = 16 / (int)sizeof(S);  // output elements per 16-byte store
+    constexpr int TPR = BN / OV, RPR = NT / TPR;
     bool ovf = false;
     const long long cbase = batch_offset(g, batch, g.sc_b);
     S* C = (S*)g.C + cbase;
+    const int nl = (threadIdx.x % TPR) * OV;
+    const int n = (int)n0 + nl;
+    const bool cvec = N % OV == 0 && (uintptr_t)C % 16 == 0;
+    const bool wvec = N % 4 == 0;
+    // a per-column bias is the same for every row this thread stores
+    float bcol[OV];
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
+    for (int e = 0; e < OV; ++e)
+        bcol[e] = g.bias && g.bias_kind == 1 && g.splits <= 1 && n + e < N ? load_bias<ST>(g.bias, n + e) : 0.f;
+    const float bscalar = g.bias && g.bias_kind == 3 && g.splits <= 1 ? load_bias<ST>(g.bias, 0) : 0.f;
+    for (int rr = threadIdx.x / TPR; rr < BM; rr += RPR) {
+        const int m = (int)m0 + rr;
+        if (m >= M || n >= N) continue;
+        float v[OV];
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const int n = (int)n0 + wn + j * 16 + (lane & 15);
-            if (n >= N) continue;
-            const float bn = g.bias && g.bias_kind == 1 ? load_bias<ST>(g.bias, n) : 0.f;
+        for (int e = 0; e < OV; e += 4) {
+            const f32x4 q = *(const f32x4*)&cs[rr * CLD + nl + e];
+            v[e] = q[0];
+            v[e + 1] = q[1];
+            v[e + 2] = q[2];
+            v[e + 3] = q[3];
+        }
+        const bool full = n + OV <= N;
+        if (g.splits > 1) {
+            float* w = g.work + ((long long)split * M + m) * N + n;
+            if (full && wvec) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = (int)m0 + wm + i * 16 + (lane >> 4) * 4 + r;
-                if (m >= M) continue;
-                const float v = acc[i][j][r];
-                if (g.splits > 1) {
-                    g.work[((long long)split * M + m) * N + n] = v;
-                } else {
-                    const float b = g.bias_kind == 2 ? load_bias<ST>(g.bias, (long long)m * N + n) : g.bias_kind == 3 ? load_bias<ST>(g.bias, 0) : bn;
-                    store_out<ST>(C, (long long)m * N + n, v, g.bias != nullptr, b, ovf);
-                }
+                for (int e = 0; e < OV; e += 4) *(f32x4*)(w + e) = f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]};
+            } else {
+                for (int e = 0; e < OV && n + e < N; ++e) w[e] = v[e];
             }
+            continue;
+        }
+        S out[OV];
+#pragma unroll
+        for (int e = 0; e < OV; ++e) {
+            float b = g.bias_kind == 1 ? bcol[e] : bscalar;
+            if (g.bias && g.bias_kind == 2 && n + e < N) b = load_bias<ST>(g.bias, (long long)m * N + n + e);
+            out[e] = round_out<ST>(v[e], g.bias != nullptr, b, ovf);
+        }
+        S* c = C + (long long)m * N + n;
+        if (full && cvec) {
+            typename St<ST>::V w;
+            __builtin_memcpy(&w, out, 16);
+            *(typename St<ST>::V*)c = w;
+        } else {
+            for (int e = 0; e < OV && n + e < N; ++e) c[e] = out[e];
         }
     }
     if (ovf && g.flag) atomicOr(g.flag, 1u);
@@ -350,8 +420,18 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= g.M * g.N) return;
     const long long m = idx / g.N, n = idx % g.N;
+    // the partials in increasing split order, eight loads in flight
+    const long long mn = g.M * g.N;
     float s = g.work[idx];
-    for (int p = 1; p < g.splits; ++p) s = s + g.work[(long long)p * g.M * g.N + idx];
+    int p = 1;
+    for (; p + 8 <= g.splits; p += 8) {
+        float w[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) w[q] = g.work[(long long)(p + q) * mn + idx];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s = s + w[q];
+    }
+    for (; p < g.splits; ++p) s = s + g.work[(long long)p * mn + idx];
     bool ovf = false;
     float b = 0.f;
     if (g.bias_kind == 1) b = load_bias<ST>(g.bias, n);
