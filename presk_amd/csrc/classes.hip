@@ -207,22 +207,29 @@ int storage_of(Ty t) {
 
 void plan_tiles(GemmArgs& g) {
     g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
-    g.tiles_n = (int)((g.N + gemm_tile_n() - 1) / gemm_tile_n());
+    // tile columns: 128, or 96 when that fills the 512 workgroup slots (two
+    // per CU) in fewer, fuller rounds (N = 384: 4 column tiles, not 3)
+    auto fill = [&](long long bn) {
+        const long long t = (long long)g.tiles_m * ((g.N + bn - 1) / bn) * g.batch;
+        return (double)t / (double)(((t + 511) / 512) * 512);
+    };
+    g.bn = fill(96) > fill(128) + 0.05 ? 96 : 128;
+    g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
     g.splits = 1;
     g.k_per_split = g.K;
     const long long tiles = (long long)g.tiles_m * g.tiles_n * g.batch;
     const int bk = gemm_block_k(g.storage);
     // fewer tiles than compute units and a long K: split K across workgroups
+    // (as many splits as fill one round of two workgroups per CU, each split
+    // at least 4 k-blocks; split s takes k-blocks [s*nkb/S, (s+1)*nkb/S))
     if (g.batch == 1 && tiles < 256 && g.K >= 8 * bk) {
-        long long s = (512 + tiles - 1) / tiles;
-        long long maxs = g.K / (4 * bk);
-        if (s > maxs) s = maxs;
+        const long long nkb = (g.K + bk - 1) / bk;
+        long long s = 512 / tiles;
+        if (s > nkb / 4) s = nkb / 4;
         if (s > 64) s = 64;
         if (s > 1) {
-            long long per = (g.K + s - 1) / s;
-            per = (per + bk - 1) / bk * bk;
-            g.splits = (int)((g.K + per - 1) / per);
-            g.k_per_split = per;
+            g.splits = (int)s;
+            g.k_per_split = (nkb + s - 1) / s * bk;  // the longest split
         }
     }
 }

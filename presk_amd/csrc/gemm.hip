@@ -74,7 +74,8 @@ struct Loader {
     // else: VEC rows x 4 k per thread block; (BK/4) k-quads x (ROWS/VEC) row
     // blocks over NT threads -> rounds.
     static constexpr int TPR = BK / VEC, RPR = NT / TPR, ROUNDS_K = ROWS / RPR;
-    static constexpr int KQ = BK / 4, RB = ROWS / VEC, ROUNDS_T = (KQ * RB) / NT;
+    static constexpr int KQ = BK / 4, RB = ROWS / VEC, ROUNDS_T = (KQ * RB + NT - 1) / NT;
+    static constexpr bool PARTIAL_T = (KQ * RB) % NT != 0;  // the last round leaves threads idle
     static constexpr int NV = KCONTIG ? ROUNDS_K : 4 * ROUNDS_T;
     V r[NV];
     bool kin[NV];   // the vector's k lies below K; applied when it is stored, so
@@ -104,7 +105,7 @@ struct Loader {
         } else {
 #pragma unroll
             for (int q = 0; q < ROUNDS_T; ++q) {
-                const int u = t + q * NT;
+                const int u = PARTIAL_T && t + q * NT >= KQ * RB ? KQ * RB - 1 : t + q * NT;
                 int row = row0 + (u / KQ) * VEC;
                 row = row + VEC <= rows ? row : rows - VEC;
                 const int kq = k0 + (u % KQ) * 4;
@@ -137,7 +138,7 @@ struct Loader {
         } else {
 #pragma unroll
             for (int q = 0; q < ROUNDS_T; ++q) {
-                const int u = t + q * NT;
+                const int u = PARTIAL_T && t + q * NT >= KQ * RB ? KQ * RB - 1 : t + q * NT;
                 const int row = row0 + (u / KQ) * VEC, kq = k0 + (u % KQ) * 4;
                 for (int kk = 0; kk < 4; ++kk) {
                     for (int j = 0; j < VEC; ++j) {
@@ -160,6 +161,7 @@ struct Loader {
 #pragma unroll
             for (int q = 0; q < ROUNDS_T; ++q) {
                 const int u = t + q * NT;
+                if (PARTIAL_T && u >= KQ * RB) break;  // an idle thread of the last round
                 const int row = (u / KQ) * VEC, kq = (u % KQ) * 4;
                 V z[4];
 #pragma unroll
@@ -267,11 +269,22 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     S* const As0 = (S*)smem;
     S* const Bs0 = As0 + 2 * BM * LD;
 
-    // tile order: blocks of one XCD (block id mod 8) take consecutive tiles,
-    // and tiles go row-group by row-group so that concurrent tiles share A rows
+    // Work order.  The grid is one line of (split, batch, tile) items.  The
+    // hardware deals workgroups to the 8 XCDs round robin (id mod 8).  Without
+    // a k-split each XCD is given one contiguous run of items, so the tiles of
+    // one batch entry and neighbouring row-tiles share its L2.  With a k-split
+    // the panels of one k-range outgrow an L2 anyway, and spreading each
+    // range over all XCDs measures faster: items go in plain order.  Within a
+    // run, tiles go 8 row-tiles at a time across the columns, so that
+    // concurrent tiles share A rows.
     const long long tiles = (long long)g.tiles_m * g.tiles_n;
-    long long bid = blockIdx.x;
-    if (tiles >= 64 && tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
+    const long long total = (long long)gridDim.x;
+    const long long xcd = blockIdx.x % 8, local = blockIdx.x / 8;
+    const long long q8 = total / 8, r8 = total % 8;
+    const long long item = g.splits > 1 ? (long long)blockIdx.x : xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    const int split = (int)(item / (tiles * g.batch));
+    const long long batch = (item / tiles) % g.batch;
+    const long long bid = item % tiles;
     constexpr long long GROUP = 8;
     const long long group_size = GROUP * g.tiles_n;
     const long long grp = bid / group_size;
@@ -280,13 +293,13 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     const long long tm_idx = first_m + (bid % group_size) % gm;
     const long long tn_idx = (bid % group_size) / gm;
     const long long m0 = tm_idx * BM, n0 = tn_idx * BN;
-    const long long batch = blockIdx.y;
-    const int split = blockIdx.z;
 
     const S* A = (const S*)g.A + batch_offset(g, batch, g.sa_b);
     const S* B = (const S*)g.B + batch_offset(g, batch, g.sb_b);
-    const int kbeg = split * (int)g.k_per_split;
-    int kend = kbeg + (int)g.k_per_split;
+    // split s of S takes k-blocks [s*nkb/S, (s+1)*nkb/S)
+    const long long nkb = (g.K + BK - 1) / BK;
+    const int kbeg = (int)((long long)split * nkb / g.splits * BK);
+    int kend = (int)(((long long)split + 1) * nkb / g.splits * BK);
     if (kend > (int)g.K) kend = (int)g.K;
     const int M = (int)g.M, N = (int)g.N;
     const int sa_m = (int)g.sa_m, sa_k = (int)g.sa_k, sb_k = (int)g.sb_k, sb_n = (int)g.sb_n;
@@ -358,7 +371,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     __syncthreads();
 
     constexpr int OV = 16 / (int)sizeof(S);  // output elements per 16-byte store
-    constexpr int TPR = BN / OV, RPR = NT / TPR;
+    constexpr int TPR = BN / OV, RPR = NT / TPR;  // threads past TPR*RPR store nothing
     bool ovf = false;
     const long long cbase = batch_offset(g, batch, g.sc_b);
     S* C = (S*)g.C + cbase;
@@ -372,7 +385,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     for (int e = 0; e < OV; ++e)
         bcol[e] = g.bias && g.bias_kind == 1 && g.splits <= 1 && n + e < N ? load_bias<ST>(g.bias, n + e) : 0.f;
     const float bscalar = g.bias && g.bias_kind == 3 && g.splits <= 1 ? load_bias<ST>(g.bias, 0) : 0.f;
-    for (int rr = threadIdx.x / TPR; rr < BM; rr += RPR) {
+    for (int rr = threadIdx.x < TPR * RPR ? (int)threadIdx.x / TPR : BM; rr < BM; rr += RPR) {
         const int m = (int)m0 + rr;
         if (m >= M || n >= N) continue;
         float v[OV];
@@ -444,7 +457,10 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
 
 template <int ST, int WM, int WN, bool SAFE>
 hipError_t launch_shape(const GemmArgs& g, hipStream_t stream) {
-    dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)g.batch, (unsigned)g.splits);
+    const long long items = (long long)g.tiles_m * g.tiles_n * g.batch * g.splits;
+    if (items <= 0) return hipSuccess;
+    if (items > 0x7fffffffLL) return hipErrorInvalidValue;
+    dim3 grid((unsigned)items, 1, 1);
     if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
     else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
     else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
@@ -457,7 +473,9 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     // the clamped vector loads need each operand's vector axis (k when it is
     // contiguous, else the rows) to hold whole aligned vectors
     const bool fast = g.a_vec && g.b_vec;
-    hipError_t e = fast ? launch_shape<ST, 4, 4, false>(g, stream) : launch_shape<ST, 4, 4, true>(g, stream);
+    hipError_t e;
+    if (g.bn == 96) e = fast ? launch_shape<ST, 4, 3, false>(g, stream) : launch_shape<ST, 4, 3, true>(g, stream);
+    else e = fast ? launch_shape<ST, 4, 4, false>(g, stream) : launch_shape<ST, 4, 4, true>(g, stream);
     if (e != hipSuccess || g.splits <= 1) return e;
     const long long n = g.M * g.N;
     split_reduce_kernel<ST><<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(g);
@@ -468,7 +486,6 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
 
 int gemm_block_k(int storage) { return storage == kF32 ? St<kF32>::BK : St<kBF16>::BK; }
 int gemm_tile_m() { return 128; }
-int gemm_tile_n() { return 128; }
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream) {
     switch (g.storage) {

@@ -27,11 +27,11 @@ struct GemmArgs {
     int splits;
     long long k_per_split;
     int tiles_m, tiles_n;
+    int bn;                         // tile columns: 128, or 96 where that fills the CUs better
 };
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream);
 int gemm_block_k(int storage);
 int gemm_tile_m();
-int gemm_tile_n();
 
 }  // namespace presk
