@@ -207,13 +207,20 @@ int storage_of(Ty t) {
 
 void plan_tiles(GemmArgs& g) {
     g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
-    // tile columns: 128, or 96 when that fills the 512 workgroup slots (two
-    // per CU) in fewer, fuller rounds (N = 384: 4 column tiles, not 3)
-    auto fill = [&](long long bn) {
+    // tile columns: 128, 96 or 64, whichever finishes first when the tiles
+    // run in rounds of 512 (two workgroups per CU) and a tile takes time in
+    // proportion to its width -- N = 384 fills the CUs in 4 columns of 96
+    // rather than 3 of 128, and N = 64 wastes nothing in 64 -- the widest on
+    // a tie (fewer operand bytes per flop)
+    long long best = -1;
+    for (int bn : {128, 96, 64}) {
         const long long t = (long long)g.tiles_m * ((g.N + bn - 1) / bn) * g.batch;
-        return (double)t / (double)(((t + 511) / 512) * 512);
-    };
-    g.bn = fill(96) > fill(128) + 0.05 ? 96 : 128;
+        const long long cost = (t + 511) / 512 * bn;
+        if (best < 0 || cost < best) {
+            best = cost;
+            g.bn = bn;
+        }
+    }
     g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
     g.splits = 1;
     g.k_per_split = g.K;

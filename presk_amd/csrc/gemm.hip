@@ -475,6 +475,7 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     const bool fast = g.a_vec && g.b_vec;
     hipError_t e;
     if (g.bn == 96) e = fast ? launch_shape<ST, 4, 3, false>(g, stream) : launch_shape<ST, 4, 3, true>(g, stream);
+    else if (g.bn == 64) e = fast ? launch_shape<ST, 4, 2, false>(g, stream) : launch_shape<ST, 4, 2, true>(g, stream);
     else e = fast ? launch_shape<ST, 4, 4, false>(g, stream) : launch_shape<ST, 4, 4, true>(g, stream);
     if (e != hipSuccess || g.splits <= 1) return e;
     const long long n = g.M * g.N;

@@ -27,7 +27,7 @@ struct GemmArgs {
     int splits;
     long long k_per_split;
     int tiles_m, tiles_n;
-    int bn;                         // tile columns: 128, or 96 where that fills the CUs better
+    int bn;                         // tile columns: 128, 96 or 64
 };
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream);

@@ -38,9 +38,10 @@ def cases():
         s = O(A(("batch", 2), ("heads", 3), ("seq", 40), ("seq2", 40)))
         out.append((f"ein_qk-{dt}", L.ein([q, kk], [["batch", "heads", "seq", "hd"], ["batch", "heads", "seq2", "hd"]], ["batch", "heads", "seq", "seq2"], dt), None))
         out.append((f"ein_av-{dt}", L.ein([s, kk], [["batch", "heads", "seq", "seq2"], ["batch", "heads", "seq2", "hd"]], ["batch", "heads", "seq", "hd"], dt), None))
-        # 128 x 96 tiles (N = 384 fills the CUs in 4 column tiles): NN and NT
-        xb = O(A(("batch", 2), ("seq", 2048), 200))
-        out.append((f"dot+add-bn96-{dt}", L.dot([xb, O(A(200, 384)), O(A(384))], dt, epilogue=(True, A(("batch", 2), ("seq", 2048), 384))), None))
+        # 128 x 96 tiles (N = 384 over 16384 rows fills the CUs in 4 column
+        # tiles): NN and NT; the 128 x 64 tiles are the ein_av cases above
+        xb = O(A(("batch", 8), ("seq", 2048), 200))
+        out.append((f"dot+add-bn96-{dt}", L.dot([xb, O(A(200, 384)), O(A(384))], dt, epilogue=(True, A(("batch", 8), ("seq", 2048), 384))), None))
         out.append((f"dot_vjp_l-bn96-{dt}", L.dot_vjp_l([xb, O(A(384, 200))], dt), None))
     # a K that is not a multiple of the k-block, M and N below one tile
     out.append(("dot-odd-bf16", L.dot([O(A(("batch", 5), 77)), O(A(77, 24))], "bf16"), None))
