@@ -38,23 +38,47 @@ struct Printer {
     // the register `cell` (its value as stored, i.e. rounded to the storage
     // type) instead of memory: `cell_key` is its index list's text.
     std::string cell_key;
+    // In a coarsened nest (VEC iterations of the innermost grid loop per
+    // thread, `u` the iteration): input loads read ahead into `pre<n>[u]`
+    // (key: buffer and index text), and the output's one store goes to
+    // `post[u]`, written back after the iterations (key: its index text).
+    std::map<std::string, int> pre;
+    std::string post_key;
 
     explicit Printer(const Kernel& k) : k(k) {
         A = k.dtype == Ty::F64 ? "double" : "float";
         for (size_t b = 0; b <= k.inputs.size(); ++b) strides.push_back(k.buf((int)b).strides());
     }
 
-    std::string ptr(int b) const {
-        const BufSpec& s = k.buf(b);
+    // Buffer b as the kernel's local pointer `pb<b>`.  They are declared
+    // __restrict__: the output is never one of the inputs (the host lends
+    // inputs and owns the output, crates/presk-kernel/src/host.rs:28-95), so
+    // loads may move past stores of other iterations and merge.
+    std::string ptr(int b) const { return "pb" + std::to_string(b); }
+
+    // The buffers as __restrict__ parameters of the body function (only
+    // parameters carry the no-alias fact into the compiler), and the casts
+    // the kernel passes them with.
+    std::string ptr_type(int b) const {
         const char* c = b == k.out_buf() ? "" : "const ";
-        switch (s.ty) {
-            case Ty::F64: return std::string("((") + c + "double*)a.buf[" + std::to_string(b) + "])";
-            case Ty::F32: return std::string("((") + c + "float*)a.buf[" + std::to_string(b) + "])";
-            case Ty::BF16: case Ty::F16: return std::string("((") + c + "unsigned short*)a.buf[" + std::to_string(b) + "])";
-            case Ty::E8M15: return std::string("((") + c + "unsigned char*)a.buf[" + std::to_string(b) + "])";
-            case Ty::I64: return std::string("((") + c + "long long*)a.buf[" + std::to_string(b) + "])";
+        switch (k.buf(b).ty) {
+            case Ty::F64: return std::string(c) + "double*";
+            case Ty::F32: return std::string(c) + "float*";
+            case Ty::BF16: case Ty::F16: return std::string(c) + "unsigned short*";
+            case Ty::E8M15: return std::string(c) + "unsigned char*";
+            case Ty::I64: return std::string(c) + "long long*";
         }
         return "";
+    }
+    std::string ptr_params() const {
+        std::string d;
+        for (int b = 0; b <= (int)k.inputs.size(); ++b) d += ", " + ptr_type(b) + " __restrict__ pb" + std::to_string(b);
+        return d;
+    }
+    std::string ptr_args() const {
+        std::string d;
+        for (int b = 0; b <= (int)k.inputs.size(); ++b) d += ", (" + ptr_type(b) + ")a.buf[" + std::to_string(b) + "]";
+        return d;
     }
 
     std::string offset(int b, const std::vector<const Expr*>& ix) {
@@ -66,14 +90,24 @@ struct Printer {
 
     // element `off` of buffer b widened exactly to its own arithmetic type
     std::string load_stored(int b, const std::string& off) {
+        if (k.buf(b).ty == Ty::E8M15) return "pk_e8m15_to_f32(pk_ld24(" + ptr(b) + ", " + off + "))";
+        return widen(b, ptr(b) + "[" + off + "]");
+    }
+    // a stored element `src` (a code) of buffer b as its arithmetic value
+    std::string widen(int b, const std::string& src) const {
         switch (k.buf(b).ty) {
-            case Ty::F64: case Ty::F32: return ptr(b) + "[" + off + "]";
-            case Ty::BF16: return "pk_bf16_to_f32(" + ptr(b) + "[" + off + "])";
-            case Ty::F16: return "pk_f16_to_f32(" + ptr(b) + "[" + off + "])";
-            case Ty::E8M15: return "pk_e8m15_to_f32(pk_ld24(" + ptr(b) + ", " + off + "))";
-            case Ty::I64: return "((double)" + ptr(b) + "[" + off + "])";
+            case Ty::F64: case Ty::F32: return src;
+            case Ty::BF16: return "pk_bf16_to_f32(" + src + ")";
+            case Ty::F16: return "pk_f16_to_f32(" + src + ")";
+            case Ty::I64: return "((double)" + src + ")";
+            case Ty::E8M15: break;
         }
         return "";
+    }
+    // the read-ahead register holding load (b, ix), if there is one
+    std::string pre_of(int b, const std::vector<const Expr*>& ix) const {
+        auto it = pre.find(std::to_string(b) + "|" + index_key(ix));
+        return it == pre.end() ? "" : "pre" + std::to_string(it->second) + "[u]";
     }
 
     std::string real(const Expr* e) {
@@ -81,6 +115,11 @@ struct Printer {
             case Expr::Num: return "((" + A + ")" + hexlit(e->num) + ")";
             case Expr::Load: {
                 if (!cell_key.empty() && e->id == k.out_buf() && index_key(e->kids) == cell_key) return "cell";
+                const std::string r = pre_of(e->id, e->kids);
+                if (!r.empty()) {
+                    if (k.buf(e->id).ty == Ty::I64) return "((" + A + ")(double)" + r + ")";
+                    return "((" + A + ")" + widen(e->id, r) + ")";
+                }
                 std::string off = offset(e->id, e->kids);
                 if (k.buf(e->id).ty == Ty::I64) return "((" + A + ")(double)" + ptr(e->id) + "[" + off + "])";
                 return "((" + A + ")" + load_stored(e->id, off) + ")";
@@ -125,6 +164,11 @@ struct Printer {
             case Expr::Iv: return "i" + std::to_string(e->id);
             case Expr::Si: return "n" + std::to_string(e->id);
             case Expr::Load: {
+                const std::string r = pre_of(e->id, e->kids);
+                if (!r.empty()) {
+                    if (k.buf(e->id).ty == Ty::I64) return r;
+                    return "pk_i64((double)" + widen(e->id, r) + ")";
+                }
                 std::string off = offset(e->id, e->kids);
                 if (k.buf(e->id).ty == Ty::I64) return ptr(e->id) + "[" + off + "]";
                 return "pk_i64((double)" + load_stored(e->id, off) + ")";
@@ -217,6 +261,17 @@ struct Printer {
                     break;
                 }
                 case Stmt::Store: {
+                    if (!post_key.empty() && s->buf == k.out_buf() && index_key(s->index) == post_key) {
+                        const std::string v = real(s->value);
+                        switch (k.output.ty) {
+                            case Ty::BF16: out += pad + "post[u] = pk_f32_to_bf16(" + v + ");\n"; break;
+                            case Ty::F16:
+                                out += pad + "{ float t_ = " + v + "; ovf |= pk_overflows_f16(t_); post[u] = pk_f32_to_f16(t_); }\n";
+                                break;
+                            default: out += pad + "post[u] = " + v + ";\n"; break;
+                        }
+                        break;
+                    }
                     if (!cell_key.empty() && s->buf == k.out_buf() && index_key(s->index) == cell_key) {
                         out += pad + "{ " + A + " t_ = " + real(s->value) + "; " + cell_round("t_") + " stored = true; }\n";
                         break;
@@ -361,6 +416,74 @@ void output_accesses(const Kernel& k, const std::vector<const Stmt*>& body,
     }
 }
 
+// Whether every access to the output in `body` is a scalar element whose
+// index moves by exactly one element when loop `var` does, in its last
+// position only: consecutive iterations of `var` write consecutive elements.
+bool output_unit_stride(const Kernel& k, const std::vector<const Stmt*>& body, int var) {
+    std::vector<std::pair<const std::vector<const Expr*>*, bool>> acc;
+    output_accesses(k, body, acc);
+    if (acc.empty()) return false;
+    for (auto& a : acc) {
+        if (a.second || a.first->empty()) return false;
+        const auto& ix = *a.first;
+        for (size_t p = 0; p < ix.size(); ++p) {
+            Affine f = affine_of(ix[p]);
+            if (!f.ok) return false;
+            const int64_t c = f.coef.count(var) ? f.coef[var] : 0;
+            if (c != (p + 1 == ix.size() ? 1 : 0)) return false;
+        }
+    }
+    return true;
+}
+
+// Storage bytes and C element type of a buffer's elements.
+int elem_bytes(Ty t) {
+    switch (t) {
+        case Ty::F64: case Ty::I64: return 8;
+        case Ty::F32: return 4;
+        case Ty::BF16: case Ty::F16: return 2;
+        case Ty::E8M15: return 3;
+    }
+    return 0;
+}
+const char* elem_type(Ty t) {
+    switch (t) {
+        case Ty::F64: return "double";
+        case Ty::F32: return "float";
+        case Ty::BF16: case Ty::F16: return "unsigned short";
+        case Ty::I64: return "long long";
+        case Ty::E8M15: return "unsigned char";
+    }
+    return "";
+}
+
+// Whether an index list, affine over the loops of `bounds` alone, stays in
+// buffer b's shape over all their iterations (so the element may be read
+// whether or not the nest reads it).
+bool in_bounds(const Kernel& k, int b, const std::vector<const Expr*>& ix, const std::map<int, int64_t>& bounds) {
+    const auto& dims = k.buf(b).dims;
+    if (ix.size() != dims.size()) return false;
+    for (size_t p = 0; p < ix.size(); ++p) {
+        Affine f = affine_of(ix[p]);
+        if (!f.ok) return false;
+        int64_t lo = f.c, hi = f.c;
+        for (auto& kv : f.coef) {
+            auto it = bounds.find(kv.first);
+            if (it == bounds.end()) return false;
+            const int64_t span = kv.second * (it->second - 1);
+            (span < 0 ? lo : hi) += span;
+        }
+        if (lo < 0 || hi >= dims[p]) return false;
+    }
+    return true;
+}
+
+// The loads of an expression tree.
+void loads_of(const Expr* e, std::vector<const Expr*>& out) {
+    if (e->kind == Expr::Load) out.push_back(e);
+    for (auto c : e->kids) loads_of(c, out);
+}
+
 // The loops of `chain` that one output index, shared by every access to the
 // output, maps injectively: each index position that is an affine function
 // of chain loops alone, whose coefficients form a mixed radix over the loops'
@@ -457,6 +580,7 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
     const int64_t split_bound = parallel_outer(k);
     std::string src = "#include \"devfmt.hpp\"\n";
     src += "struct PkArgs { void* buf[" + std::to_string(kMaxBufs) + "]; unsigned* flag; long long lo, hi; };\n";
+    src += "typedef unsigned int pk_u32x4 __attribute__((ext_vector_type(4)));\n";
     int index = 0;
     for (auto& g : groups) {
         Phase ph;
@@ -507,10 +631,23 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
             }
             level = lv;
         }
-        for (auto l : loops) ph.bounds.push_back(l->bound);
         ph.split = !loops.empty() && groups.size() == 1 && split_bound >= 0 && loops[0] == k.body[0];
+        // Each thread takes VEC consecutive iterations of the innermost grid
+        // loop when the nest is all grid (no loop left in the thread) and
+        // those iterations write consecutive output elements: the loads and
+        // stores of the unrolled iterations merge into 16-byte accesses.
+        // The iterations are independent, so running them in one thread in
+        // order changes nothing.
+        int vec = 1;
+        if (!loops.empty() && serial.empty() && !(loops.size() == 1 && ph.split)) {
+            const int want = k.output.ty == Ty::F32 ? 4 : (k.output.ty == Ty::BF16 || k.output.ty == Ty::F16) ? 8 : 1;
+            const Stmt* inner = loops.back();
+            if (want > 1 && inner->bound % want == 0 && output_unit_stride(k, *level, inner->var)) vec = want;
+        }
+        for (auto l : loops) ph.bounds.push_back(l->bound);
+        if (vec > 1) ph.bounds.back() /= vec;
         std::string body;
-        body += "extern \"C\" __global__ void __launch_bounds__(256) " + ph.fn + "(PkArgs a) {\n";
+        body += "__device__ __forceinline__ void " + ph.fn + "_body(const PkArgs& a" + P.ptr_params() + ") {\n";
         for (int v = 0; v < k.nloops; ++v) body += "    long long i" + std::to_string(v) + " = 0; (void)i" + std::to_string(v) + ";\n";
         for (int v = 0; v < k.nreal; ++v) body += "    " + P.A + " s" + std::to_string(v) + " = 0; (void)s" + std::to_string(v) + ";\n";
         for (int v = 0; v < k.nint; ++v) body += "    long long n" + std::to_string(v) + " = 0; (void)n" + std::to_string(v) + ";\n";
@@ -520,15 +657,17 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
         if (!loops.empty()) {
             body += "    long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;\n";
             // the outermost loop runs over [lo, hi) when split, else its bound
-            body += "    const long long n0 = " + std::string(ph.split ? "a.hi - a.lo" : std::to_string(loops[0]->bound) + "LL") + ";\n";
+            const int vec0 = loops.size() == 1 ? vec : 1;  // the outermost loop is also the innermost
+            body += "    const long long n0 = " + std::string(ph.split ? "a.hi - a.lo" : std::to_string(loops[0]->bound / vec0) + "LL") + ";\n";
             std::string total = "n0";
-            for (size_t d = 1; d < loops.size(); ++d) total += " * " + std::to_string(loops[d]->bound) + "LL";
+            for (size_t d = 1; d < loops.size(); ++d)
+                total += " * " + std::to_string(d + 1 == loops.size() ? loops[d]->bound / vec : loops[d]->bound) + "LL";
             body += "    if (t >= " + total + ") return;\n";
             for (size_t d = loops.size(); d-- > 1;) {
-                std::string b = std::to_string(loops[d]->bound) + "LL";
-                body += "    i" + std::to_string(loops[d]->var) + " = t % " + b + "; t /= " + b + ";\n";
+                std::string b = std::to_string(d + 1 == loops.size() ? loops[d]->bound / vec : loops[d]->bound) + "LL";
+                body += "    i" + std::to_string(loops[d]->var) + " = t % " + b + (d + 1 == loops.size() && vec > 1 ? " * " + std::to_string(vec) + "LL" : "") + "; t /= " + b + ";\n";
             }
-            body += "    i" + std::to_string(loops[0]->var) + " = t" + (ph.split ? " + a.lo" : "") + ";\n";
+            body += "    i" + std::to_string(loops[0]->var) + " = t" + (vec0 > 1 ? " * " + std::to_string(vec0) + "LL" : "") + (ph.split ? " + a.lo" : "") + ";\n";
             // the loops left in the thread, in their order around the body;
             // the thread's own output element in a register across them
             std::set<int> grid;
@@ -552,7 +691,81 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
                 close = pad + "}\n" + close;
                 ++depth;
             }
-            P.stmts(*level, depth, body);
+            if (vec > 1) {
+                const int iv = loops.back()->var;
+                const std::string v = "i" + std::to_string(iv), V = std::to_string(vec);
+                body += "    const long long " + v + "_0 = " + v + ";\n";
+                // Read ahead: each input element the iterations read at unit
+                // stride along the coarsened loop, whose index is affine in
+                // the grid loops and in bounds over all of them, is loaded for
+                // all VEC iterations at once (16-byte loads when aligned).
+                std::map<int, int64_t> gb;
+                for (auto l : loops) gb[l->var] = l->bound;
+                std::vector<const Expr*> lds;
+                for (auto st : *level) {
+                    if (st->kind == Stmt::For || st->kind == Stmt::If) continue;
+                    for (auto e : st->index) loads_of(e, lds);
+                    if (st->value) loads_of(st->value, lds);
+                }
+                for (auto e : lds) {
+                    const int b = e->id;
+                    const Ty ty = k.buf(b).ty;
+                    if (b == k.out_buf() || ty == Ty::E8M15 || !in_bounds(k, b, e->kids, gb)) continue;
+                    bool unit = !e->kids.empty();  // (a scalar buffer is the same element for every u)
+                    for (size_t p = 0; p < e->kids.size(); ++p) {
+                        Affine f = affine_of(e->kids[p]);
+                        const int64_t c = f.coef.count(iv) ? f.coef[iv] : 0;
+                        if (c != (p + 1 == e->kids.size() ? 1 : 0)) unit = false;
+                    }
+                    const std::string key = std::to_string(b) + "|" + index_key(e->kids);
+                    if (!unit || P.pre.count(key)) continue;
+                    const int n = (int)P.pre.size();
+                    const std::string T = elem_type(ty), pn = "pre" + std::to_string(n);
+                    const int bytes = vec * elem_bytes(ty);
+                    body += "    " + T + " " + pn + "[" + V + "];\n";
+                    body += "    { const " + T + "* p_ = " + P.ptr(b) + " + " + P.offset(b, e->kids) + ";\n";
+                    if (bytes % 16 == 0) {
+                        body += "      if ((((unsigned long long)p_) & 15ULL) == 0) {\n";
+                        body += "#pragma unroll\n        for (int c = 0; c < " + std::to_string(bytes / 16) +
+                                "; ++c) { pk_u32x4 w_ = ((const pk_u32x4*)p_)[c]; __builtin_memcpy((char*)" + pn + " + 16 * c, &w_, 16); }\n";
+                        body += "      } else {\n#pragma unroll\n        for (int u = 0; u < " + V + "; ++u) " + pn + "[u] = p_[u];\n      }\n";
+                    } else {
+                        body += "#pragma unroll\n      for (int u = 0; u < " + V + "; ++u) " + pn + "[u] = p_[u];\n";
+                    }
+                    body += "    }\n";
+                    P.pre[key] = n;
+                }
+                // The one store of the output, unconditional and read by
+                // nothing: buffered and written back in 16-byte stores.
+                std::vector<std::pair<const std::vector<const Expr*>*, bool>> oacc;
+                output_accesses(k, *level, oacc);
+                const Stmt* ost = nullptr;
+                for (auto st : *level)
+                    if (st->kind == Stmt::Store && st->buf == k.out_buf()) ost = st;
+                const bool post = oacc.size() == 1 && ost && (elem_bytes(k.output.ty) * vec) % 16 == 0;
+                const std::string OT = elem_type(k.output.ty);
+                if (post) {
+                    P.post_key = index_key(ost->index);
+                    body += "    " + OT + " post[" + V + "];\n";
+                    body += "    const long long o_ = " + P.offset(k.out_buf(), ost->index) + ";\n";
+                }
+                body += "#pragma unroll\n    for (int u = 0; u < " + V + "; ++u) {\n";
+                body += "    " + v + " = " + v + "_0 + u;\n";
+                P.stmts(*level, depth + 1, body);
+                body += "    }\n";
+                if (post) {
+                    const int chunks = elem_bytes(k.output.ty) * vec / 16;
+                    body += "    { " + OT + "* p_ = " + P.ptr(k.out_buf()) + " + o_;\n";
+                    body += "      if ((((unsigned long long)p_) & 15ULL) == 0) {\n";
+                    body += "#pragma unroll\n        for (int c = 0; c < " + std::to_string(chunks) +
+                            "; ++c) { pk_u32x4 w_; __builtin_memcpy(&w_, (const char*)post + 16 * c, 16); ((pk_u32x4*)p_)[c] = w_; }\n";
+                    body += "      } else {\n#pragma unroll\n        for (int u = 0; u < " + V + "; ++u) p_[u] = post[u];\n      }\n    }\n";
+                }
+                P.pre.clear();
+                P.post_key.clear();
+            } else {
+                P.stmts(*level, depth, body);
+            }
             body += close;
             if (cell) {
                 P.cell_key.clear();
@@ -574,6 +787,7 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
         }
         if (k.guarded()) body += "    if (ovf) atomicOr(a.flag, 1u);\n";
         body += "}\n";
+        body += "extern \"C\" __global__ void __launch_bounds__(256) " + ph.fn + "(PkArgs a) { " + ph.fn + "_body(a" + P.ptr_args() + "); }\n";
         src += body;
         out->phases.push_back(ph);
     }
