@@ -29,30 +29,30 @@ PK_DEV float pk_float(unsigned b) { return __builtin_bit_cast(float, b); }
 
 // ---- bf16 ---------------------------------------------------------------------
 PK_DEV float pk_bf16_to_f32(unsigned short h) { return pk_float((unsigned)h << 16); }
+// (written as a select, not a branch: in a running sum it is one step of a
+// dependent chain, where a branch costs an exec-mask round trip)
 PK_DEV unsigned short pk_f32_to_bf16(float x) {
-    unsigned b = pk_bits(x);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((b >> 16) | 0x0040u);
-    return (unsigned short)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+    const unsigned b = pk_bits(x);
+    const unsigned nan = (b >> 16) | 0x0040u, rne = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+    return (unsigned short)((b & 0x7fffffffu) > 0x7f800000u ? nan : rne);
 }
 
 // ---- binary16 -----------------------------------------------------------------
 PK_DEV float pk_f16_to_f32(unsigned short c) {
-    unsigned sign = (unsigned)(c & 0x8000u) << 16, field = (c >> 10) & 0x1fu, frac = c & 0x3ffu, mag;
-    if (field == 0x1fu) mag = frac == 0 ? 0x7f800000u : (0x7fc00000u | (frac << 13));
-    else if (field == 0) mag = pk_bits((float)frac * 5.9604644775390625e-8f);   // frac * 2^-24, exact
-    else mag = ((field + 112u) << 23) | (frac << 13);
-    return pk_float(sign | mag);
+    const unsigned sign = (unsigned)(c & 0x8000u) << 16, field = (c >> 10) & 0x1fu, frac = c & 0x3ffu;
+    const unsigned special = frac == 0 ? 0x7f800000u : (0x7fc00000u | (frac << 13));
+    const unsigned sub = pk_bits((float)frac * 5.9604644775390625e-8f);   // frac * 2^-24, exact
+    const unsigned normal = ((field + 112u) << 23) | (frac << 13);
+    return pk_float(sign | (field == 0x1fu ? special : field == 0 ? sub : normal));
 }
 PK_DEV unsigned short pk_f32_to_f16(float x) {
-    unsigned b = pk_bits(x), sign = (b >> 16) & 0x8000u, a = b & 0x7fffffffu, code;
-    if (a > 0x7f800000u) code = 0x7e00u | ((a >> 13) & 0x1ffu);          // NaN, quiet
-    else if (a >= 0x477ff000u) code = 0x7c00u;                           // rounds past 65504: inf
-    else if (a >= 0x38800000u) {                                          // normal binary16
-        unsigned r = a - 0x38000000u;                                     // rebias 127 -> 15
-        code = (r + 0xfffu + ((r >> 13) & 1u)) >> 13;
-    } else {                                                              // subnormal or zero:
-        code = (unsigned)__builtin_rintf(pk_float(a) * 16777216.0f);      // |x| / 2^-24, to even
-    }
+    const unsigned b = pk_bits(x), sign = (b >> 16) & 0x8000u, a = b & 0x7fffffffu;
+    const unsigned nan = 0x7e00u | ((a >> 13) & 0x1ffu);                  // NaN, quiet
+    const unsigned r = a - 0x38000000u;                                   // normal binary16: rebias 127 -> 15
+    const unsigned normal = (r + 0xfffu + ((r >> 13) & 1u)) >> 13;
+    // subnormal or zero: |x| / 2^-24 rounded to even (computed on 0 otherwise)
+    const unsigned sub = (unsigned)__builtin_rintf(pk_float(a < 0x38800000u ? a : 0u) * 16777216.0f);
+    const unsigned code = a > 0x7f800000u ? nan : a >= 0x477ff000u ? 0x7c00u : a >= 0x38800000u ? normal : sub;
     return (unsigned short)(sign | code);
 }
 PK_DEV bool pk_overflows_f16(float x) {
@@ -63,9 +63,9 @@ PK_DEV bool pk_overflows_f16(float x) {
 // ---- e8m15: 3 bytes, little-endian, the f32's top 24 bits ---------------------
 PK_DEV float pk_e8m15_to_f32(unsigned c) { return pk_float(c << 8); }
 PK_DEV unsigned pk_f32_to_e8m15(float x) {
-    unsigned b = pk_bits(x);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 8) | 0x4000u;
-    return (b + 0x7fu + ((b >> 8) & 1u)) >> 8;
+    const unsigned b = pk_bits(x);
+    const unsigned nan = (b >> 8) | 0x4000u, rne = (b + 0x7fu + ((b >> 8) & 1u)) >> 8;
+    return (b & 0x7fffffffu) > 0x7f800000u ? nan : rne;
 }
 PK_DEV bool pk_overflows_e8m15(float x) {
     unsigned a = pk_bits(x) & 0x7fffffffu;
