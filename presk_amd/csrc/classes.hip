@@ -406,11 +406,12 @@ struct ColSumPlan : ClassPlan {
     mutable float* work = nullptr;
     const char* kind() const override { return "colsum"; }
     std::string order() const override { return "chunked(" + std::to_string(a.chunk) + ")-f32"; }
+    int n_in = 2;
     hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
         ColSumArgs x = a;
         x.x = bufs[0];
-        x.out = bufs[2];
-        x.flag = guarded ? (unsigned*)bufs[3] : nullptr;
+        x.out = bufs[n_in];
+        x.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
         hipError_t e = prepare();
         if (e != hipSuccess) return e;
         x.work = work;
@@ -426,9 +427,24 @@ struct ColSumPlan : ClassPlan {
 };
 
 std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
-    if (k.name != "sum_to" || k.inputs.size() != 2) return nullptr;
     const int st = k.dtype == Ty::F32 ? 0 : k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : -1;
-    if (st < 0 || k.inputs[0].ty != k.dtype || k.output.ty != k.dtype) return nullptr;
+    if (st < 0 || k.inputs.empty() || k.inputs[0].ty != k.dtype || k.output.ty != k.dtype) return nullptr;
+    if ((k.name == "sum_all" || k.name == "mean_all") && k.inputs.size() == 1 && k.output.dims.empty()) {
+        // every element, as one column
+        auto p = std::make_unique<ColSumPlan>();
+        p->n_in = 1;
+        p->a.cols = 1;
+        p->a.rows = k.inputs[0].numel();
+        if (p->a.rows < 256) return nullptr;
+        p->a.chunk = 64;
+        p->a.nchunks = (p->a.rows + p->a.chunk - 1) / p->a.chunk;
+        if (p->a.nchunks > 65535) return nullptr;
+        p->a.div = k.name == "mean_all" ? (float)(double)p->a.rows : 0.f;
+        p->a.storage = st;
+        p->guarded = k.guarded();
+        return p;
+    }
+    if (k.name != "sum_to" || k.inputs.size() != 2) return nullptr;
     const BufSpec &x = k.inputs[0], &o = k.output;
     std::vector<int> m;
     if (!align(o, x, &m)) return nullptr;
@@ -490,7 +506,13 @@ std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
         return !x.names.back().empty() && x.names.back() == name;
     };
     std::string rest;
-    if (last_axis("mean axis ", &rest) && rest.empty() && k.inputs.size() == 1) {
+    if ((n == "mean_all" || n == "sum_all") && k.inputs.size() == 1 && k.output.dims.empty()) {
+        // every element as one row, summed in index order (lower.rs:1221-1233)
+        p->a.rows = 1;
+        p->a.n = x.numel();
+        p->a.n_real = (float)(double)p->a.n;
+        p->a.op = n == "mean_all" ? kRowMean : kRowSum;
+    } else if (last_axis("mean axis ", &rest) && rest.empty() && k.inputs.size() == 1) {
         p->a.op = kRowMean;
     } else if (last_axis("sum axis ", &rest) && rest.empty() && k.inputs.size() == 1) {
         p->a.op = kRowSum;
@@ -569,13 +591,14 @@ std::unique_ptr<ClassPlan> classify_scatter(const Kernel& k) {
 }
 
 std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode) {
+    // FAST: column sums and totals in the declared chunked order
+    if (mode == PRESK_HIP_FAST)
+        if (auto p = classify_sum_to(k)) return p;
     // exact in every mode: the interpreter's order, row by row
     if (auto p = classify_rows(k)) return p;
     if (auto p = classify_scatter(k)) return p;
-    if (mode == PRESK_HIP_FAST) {
+    if (mode == PRESK_HIP_FAST)
         if (auto p = classify_gemm(k)) return p;
-        if (auto p = classify_sum_to(k)) return p;
-    }
     return nullptr;
 }
 

@@ -1,6 +1,7 @@
 // Column reductions in a declared chunked order (FAST mode): `sum_to` of a
 // tensor onto its trailing axes (a bias's gradient, lower.rs:1670-1680),
-// out[c] = sum_r x[r][c].
+// out[c] = sum_r x[r][c]; and `sum_all`/`mean_all` (lower.rs:1221-1233) as
+// the one column of all elements, the mean dividing the total once.
 //
 // The interpreter's order adds the R rows one after another into the output
 // (a running sum of R dependent additions per column: latency-bound with one
@@ -76,6 +77,7 @@ __global__ void __launch_bounds__(256) colsum_total(ColSumArgs a) {
         __syncthreads();
     }
     if (w != 0 || !live) return;
+    if (a.div != 0.f) acc = acc / a.div;
     if (ST == 0) {
         ((float*)a.out)[col] = acc;
     } else if (ST == 1) {

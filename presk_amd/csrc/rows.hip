@@ -253,6 +253,84 @@ __global__ void __launch_bounds__(64) rows_kernel(RowArgs a) {
     if (ovf && a.flag) atomicOr(a.flag, 1u);
 }
 
+// A few long rows (a total, `mean_all`, or rows too few to give each lane
+// its own): one workgroup per row stages the row through LDS 4096 elements at
+// a time, the next stage's loads issued before the current one is walked,
+// and one lane adds the stage in index order.
+constexpr int LSTAGE = 4096;
+
+template <int OP, int ST>
+__global__ void __launch_bounds__(256) rows_long_kernel(RowArgs a) {
+    __shared__ __attribute__((aligned(16))) float buf[2][LSTAGE];
+    constexpr int PER = LSTAGE / 256;
+    const int t = threadIdx.x;
+    const long long n = a.n, base = (long long)blockIdx.x * n;
+    float acc = 0.f;
+    bool ovf = false;
+    float nx[PER];
+    auto fetch = [&](long long c0) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const long long c = c0 + j * 256 + t;
+            nx[j] = c < n ? ld<ST>(a.x, base + c) : 0.f;
+        }
+    };
+    auto put = [&](int s) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) buf[s][j * 256 + t] = nx[j];
+    };
+    fetch(0);
+    put(0);
+    __syncthreads();
+    int s = 0;
+    for (long long c0 = 0; c0 < n; c0 += LSTAGE, s ^= 1) {
+        const bool more = c0 + LSTAGE < n;
+        if (more) fetch(c0 + LSTAGE);
+        if (t == 0) {
+            const int cw = (int)(n - c0 < LSTAGE ? n - c0 : LSTAGE);
+            int j = 0;
+            for (; j + 4 <= cw; j += 4) {
+                const float4 q = *(const float4*)&buf[s][j];
+                const float e[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (OP == kSumToRows) {
+                        const float y = acc + e[u];
+                        if (ST == 2) ovf |= pk_overflows_f16(y);
+                        acc = stored<ST>(y);
+                    } else {
+                        acc = acc + e[u];
+                    }
+                }
+            }
+            for (; j < cw; ++j) {
+                if (OP == kSumToRows) {
+                    const float y = acc + buf[s][j];
+                    if (ST == 2) ovf |= pk_overflows_f16(y);
+                    acc = stored<ST>(y);
+                } else {
+                    acc = acc + buf[s][j];
+                }
+            }
+        }
+        if (more) put(s ^ 1);  // the other buffer was walked last round
+        __syncthreads();
+    }
+    if (t == 0) st<ST>(a.out, blockIdx.x, OP == kRowMean ? acc / a.n_real : acc, ovf);
+    if (ovf && a.flag) atomicOr(a.flag, 1u);
+}
+
+template <int OP>
+hipError_t launch_long(const RowArgs& a, hipStream_t stream) {
+    switch (a.storage) {
+        case 0: rows_long_kernel<OP, 0><<<(unsigned)a.rows, 256, 0, stream>>>(a); break;
+        case 1: rows_long_kernel<OP, 1><<<(unsigned)a.rows, 256, 0, stream>>>(a); break;
+        case 2: rows_long_kernel<OP, 2><<<(unsigned)a.rows, 256, 0, stream>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int OP, int R, bool RES>
 hipError_t launch_r(const RowArgs& a, hipStream_t stream) {
     const unsigned grid = (unsigned)((a.rows + R - 1) / R);
@@ -271,6 +349,10 @@ hipError_t launch_r(const RowArgs& a, hipStream_t stream) {
 template <int OP>
 hipError_t launch_op(const RowArgs& a, hipStream_t stream) {
     if (a.rows == 0) return hipSuccess;
+    if constexpr (OP == kRowMean || OP == kRowSum || OP == kSumToRows) {
+        // rows too few for a lane each and long enough to stage
+        if (a.rows < 1024 && a.n >= 1024) return launch_long<OP>(a, stream);
+    }
     if ((OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2) && a.mask_rows <= 0) return hipErrorInvalidValue;
     if ((a.rows + 3) / 4 > 0x7fffffffll) return hipErrorInvalidValue;
     const bool res = a.n <= NRES * CW;

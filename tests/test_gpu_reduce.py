@@ -188,3 +188,60 @@ def test_rows_class_nan_and_empty_rows(dt):
         assert c.kind == "rows", c.kind
         got = out.download(want.dtype, want.size).reshape(want.shape)
         _same_bits_nan_as_nan(got, want, dt)
+
+
+def chunked_total_text(n, dtype, mean, chunk=64):
+    """out = chunked sum of x[0..n) (chunks of 64 from zero, then the chunk sums
+    in order from zero), divided by n for the mean: the declared order."""
+    full, rem = divmod(n, chunk)
+    lines = [f"kernel total (%0 : {dtype}[{n}]) -> %1 : {dtype}[] {{", "  s0 = 0"]
+    if full:
+        lines += [f"  for i1 in 0..{full} {{", "    s1 = 0", f"    for i2 in 0..{chunk} {{",
+                  f"      s1 = (s1 + %0[((i1 * {chunk}) + i2)])", "    }", "    s0 = (s0 + s1)", "  }"]
+    if rem:
+        lines += ["  s1 = 0", f"  for i2 in 0..{rem} {{", f"    s1 = (s1 + %0[(i2 + {full * chunk})])", "  }", "  s0 = (s0 + s1)"]
+    lines += [f"  %1[] = (s0 / {n})" if mean else "  %1[] = s0", "}"]
+    return "\n".join(lines) + "\n"
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("op", ["mean_all", "sum_all"])
+@pytest.mark.parametrize("mode", [hip.FAST, hip.EXACT])
+def test_totals(dt, op, mode):
+    """sum_all / mean_all over 64 x 300 elements: FAST in the chunked(64)
+    order (colsum class), EXACT in index order through the long-row walk
+    (rows class, one workgroup staging 4096 elements at a time)"""
+    rows = O(A(("batch", 64), ("seq", 300)))
+    low = L.reduce_all(op, [rows], dt)
+    ex = hip.HipExec(0, mode=mode)
+    ins = zoo.inputs(low, seed=7)
+    c = ex.compiled(low.text, dt, low.lanes)
+    if mode == hip.FAST:
+        assert c.kind == "colsum", c.kind
+        want, _ = cexec.run(chunked_total_text(64 * 300, dt, op == "mean_all"), dt, ins, lanes=1)
+    else:
+        assert c.kind == "rows", c.kind
+        want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes)
+    nb = hip.STORAGE_BYTES[dt]
+    out = hip.DeviceBuffer(nb)
+    ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+    assert out.download(np.uint8, nb).tobytes() == want.view(np.uint8).tobytes()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_long_rows_exact(dt):
+    """a few long rows (5 x 9000): mean and the stored running sum of
+    `sum_to` onto leading axes, through the long-row walk, in index order"""
+    x = O(A(("batch", 5), ("vocab", 9000)))
+    r = O(A(("batch", 5)))
+    ex = hip.HipExec(0, mode=hip.EXACT)
+    from oracle import kernel_text as kt
+    for low in (L.reduce_axis("mean", "vocab", [x], dt), L.sum_to([x, r], dt)):
+        ins = zoo.inputs(low, seed=9)
+        want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes)
+        k = kt.parse_kernel(low.text)
+        nb = k.output.numel * hip.STORAGE_BYTES[dt]
+        out = hip.DeviceBuffer(nb)
+        c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+        assert c.kind == "rows", c.kind
+        assert out.download(np.uint8, nb).tobytes() == want.view(np.uint8).tobytes(), low.name
