@@ -50,6 +50,44 @@ def workload(name: str, dtype: str, rows=None):
     return p, host, s.B * s.T, gpt.contraction_flops(s, train), cfg
 
 
+def launch_key(ln) -> str:
+    """A launch as the traffic table names it: its kernel's header (name and
+    shapes) and the class and order it runs in."""
+    c = ln.compiled
+    return f"{ln.low.text.splitlines()[0].rstrip(' {')} | {c.kind} {c.order}"
+
+
+def _traffic_table() -> dict:
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, then
+    WRITE_SIZE, each scaled by the copy probe's reading), as committed in
+    profiles/traffic.json: {launch key: bytes}."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return {e["key"]: e["bytes_per_launch"] for e in json.load(f)["launches"]}
+    except (OSError, ValueError, KeyError):
+        return {}
+
+
+TRAFFIC = _traffic_table()
+
+
+def copy_probe():
+    """neg over 64 Mi f32 (256 MiB read, 256 MiB written), three launches."""
+    from presk_amd import hip, lower as L
+    hip.init(0)
+    x = L.Operand(L.ax(("rows", 16384), ("cols", 4096)))
+    low = L.unary("neg", [x], "f32")
+    c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+    n = 16384 * 4096
+    a, b = hip.DeviceBuffer(4 * n), hip.DeviceBuffer(4 * n)
+    a.zero()
+    for _ in range(3):
+        c.run([a.ptr, b.ptr])
+    hip.sync()
+    print(json.dumps({"copy_probe": low.name, "bytes_read": 4 * n, "bytes_written": 4 * n, "runs": 3}), flush=True)
+
+
 def cpu_baseline(name: str, dtype: str, rows: int, threads: int):
     """The oracle (the kernel interpreter's semantics in C, -O3 -march=native,
     the outermost parallel loop split over OpenMP threads as the native
@@ -76,6 +114,10 @@ def main():
     ap.add_argument("--dtype", default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="issue the launches one by one instead of one HIP graph")
+    ap.add_argument("--dominant-only", type=int, default=0, metavar="N",
+                    help="after the timing pass, run the dominant launch alone N times and exit (for rocprofv3 --pmc)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run a plain copy-like nest (neg over 64 Mi f32) 3 times and exit: the counters' calibration")
     ap.add_argument("--cpu-rows", type=int, default=None)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -85,6 +127,9 @@ def main():
 
     from presk_amd import configs, hip
 
+    if args.copy_probe:
+        copy_probe()
+        return
     dtype = args.dtype or ("bf16" if args.workload == "mlp" else "f32")
     p, host, tokens, flops, cfg = workload(args.workload, dtype)
     p.compile()
@@ -109,16 +154,25 @@ def main():
     times = p.kernel_times(reps=max(args.steps, 10))
     ln, ms = max(times, key=lambda t: t[1])
     c = ln.compiled
+    key = launch_key(ln)
+    if args.dominant_only:
+        hip.sync()
+        for _ in range(args.dominant_only):
+            hip.check(hip.lib().presk_hip_run(c.handle, ln.table, 0, max(c.split_bound, 0), None))
+        hip.sync()
+        print(json.dumps({"dominant": key, "runs": args.dominant_only}), flush=True)
+        return
+    traffic = TRAFFIC.get(key)
     if c.flops > 0:
         achieved = c.flops / (ms * 1e-3) / 1e12
         peak = PEAK_TFLOPS[dtype]
         roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "mfma", "achieved": round(achieved, 2),
-                "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                 "ms_per_launch": round(ms, 5), "algorithmic_flops": c.flops}
     else:
         achieved = c.bytes / (ms * 1e-3) / 1e9
         roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "hbm", "achieved": round(achieved, 1),
-                "peak": HBM_GBS, "unit": "GB/s", "frac": round(achieved / HBM_GBS, 4), "traffic": None,
+                "peak": HBM_GBS, "unit": "GB/s", "frac": round(achieved / HBM_GBS, 4), "traffic": traffic,
                 "ms_per_launch": round(ms, 5), "algorithmic_bytes": c.bytes}
     # per nest name: launches and total ms (the step's time by kind of nest)
     agg = {}
@@ -131,7 +185,8 @@ def main():
         e["ms"] = round(e["ms"], 4)
 
     cfg = dict(cfg, launch="eager" if args.eager else "hip graph")
-    rec = {"metric": METRIC, "value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+    metric = METRIC if args.workload == "gpt-step" else f"rows/sec {args.workload} (a supplementary workload)"
+    rec = {"metric": metric, "value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,1) inputs, xavier weights)",
            "config": cfg, "matmul_tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
