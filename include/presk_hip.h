@@ -124,6 +124,18 @@ int presk_hip_stream_destroy(void *stream);
 int presk_hip_time(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi, void *stream, int warmup,
                    int reps, double *ms_per_launch);
 
+/* The host's conversion of a buffer at a kernel's edge, on the device: n
+ * elements of type `from` at src stored as type `to` at dst, as
+ * Buf::of(to, b.to_f64()) stores them (crates/presk-rt/src/lib.rs:868-876,
+ * called at crates/presk-kernel/src/host.rs:793-829 when a mixed realization
+ * hands a kernel a buffer of another type; the C export's presk_convert,
+ * crates/presk-export-c/c/presk_rt.h:409-417).  Types "f64", "f32", "bf16",
+ * "f16", "e8m15".  A buffer of the same type is copied as it is.  When `to` is
+ * f16 or e8m15 and a finite value reaches its overflow threshold, *flag gets
+ * bit 0 (if flag is not null): the host's E7007. */
+int presk_hip_convert(const void *src, const char *from, void *dst, const char *to, int64_t n, uint32_t *flag,
+                      void *stream);
+
 /* A recorded launch sequence: a function body's kernels in the order the
  * host's call loop issues them (crates/presk-kernel/src/host.rs:887-1030 runs
  * each `let` of the body as one or more launches through `KernelExec::run`).
@@ -139,6 +151,9 @@ int presk_hip_time(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int
 typedef struct presk_hip_batch presk_hip_batch;
 int presk_hip_batch_create(presk_hip_batch **out);
 int presk_hip_batch_add(presk_hip_batch *b, const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi);
+/* An edge conversion (presk_hip_convert) as a step of the sequence. */
+int presk_hip_batch_add_convert(presk_hip_batch *b, const void *src, const char *from, void *dst, const char *to,
+                                int64_t n, uint32_t *flag);
 int presk_hip_batch_graph(presk_hip_batch *b);
 int presk_hip_batch_run(presk_hip_batch *b, void *stream);
 void presk_hip_batch_release(presk_hip_batch *b);

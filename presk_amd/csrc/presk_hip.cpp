@@ -17,6 +17,7 @@
 #include <sstream>
 #include <unordered_map>
 
+#include "convert.hpp"
 #include "executor.hpp"
 
 namespace presk {
@@ -384,10 +385,13 @@ int presk_hip_time(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int
 }  // extern "C"
 
 struct presk_hip_batch {
+    // a kernel launch, or (k null) an edge conversion
     struct Item {
         const presk_hip_kernel* k;
         std::vector<void*> bufs;
         int64_t lo, hi;
+        int from = -1, to = -1;
+        int64_t n = 0;
     };
     std::vector<Item> items;
     hipGraph_t graph = nullptr;
@@ -400,8 +404,14 @@ struct presk_hip_batch {
         graph = nullptr;
     }
     int run_each(hipStream_t s) const {
-        for (const Item& it : items)
+        for (const Item& it : items) {
+            if (!it.k) {
+                hipError_t e = convert_launch(it.bufs[0], it.from, it.bufs[1], it.to, it.n, (unsigned*)it.bufs[2], s);
+                if (e != hipSuccess) return hip_fail(e, "edge conversion");
+                continue;
+            }
             if (int rc = presk_hip_run(it.k, it.bufs.data(), it.lo, it.hi, s)) return rc;
+        }
         return PRESK_HIP_OK;
     }
     ~presk_hip_batch() { drop_graph(); }
@@ -423,11 +433,36 @@ int presk_hip_batch_add(presk_hip_batch* b, const presk_hip_kernel* k, void* con
     return PRESK_HIP_OK;
 }
 
+int presk_hip_convert(const void* src, const char* from, void* dst, const char* to, int64_t n, uint32_t* flag,
+                      void* stream) {
+    const int f = convert_type(from), t = convert_type(to);
+    if (f < 0 || t < 0) return fail(PRESK_HIP_ERR, "E10001: a conversion between `" + std::string(from ? from : "") +
+                                                       "` and `" + std::string(to ? to : "") + "`, not storage types");
+    if (n < 0 || (n > 0 && (!src || !dst))) return fail(PRESK_HIP_ERR, "E10001: bad conversion arguments");
+    hipError_t e = convert_launch(src, f, dst, t, n, flag, (hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "edge conversion");
+}
+
+int presk_hip_batch_add_convert(presk_hip_batch* b, const void* src, const char* from, void* dst, const char* to,
+                                int64_t n, uint32_t* flag) {
+    if (!b) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    const int f = convert_type(from), t = convert_type(to);
+    if (f < 0 || t < 0 || n < 0 || (n > 0 && (!src || !dst))) return fail(PRESK_HIP_ERR, "E10001: bad conversion arguments");
+    b->drop_graph();
+    presk_hip_batch::Item it{nullptr, {const_cast<void*>(src), dst, flag}, 0, 0};
+    it.from = f;
+    it.to = t;
+    it.n = n;
+    b->items.push_back(it);
+    return PRESK_HIP_OK;
+}
+
 int presk_hip_batch_graph(presk_hip_batch* b) {
     if (!b) return fail(PRESK_HIP_ERR, "E10001: null argument");
     b->drop_graph();
     for (const auto& it : b->items)
-        if (int rc = prepare_kernel(it.k)) return rc;
+        if (it.k)
+            if (int rc = prepare_kernel(it.k)) return rc;
     hipStream_t cs = nullptr;
     hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
     if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
