@@ -23,10 +23,12 @@ PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}   # MI355X dense MFM
 HBM_GBS = 8000.0
 
 
-def workload(name: str, dtype: str, rows=None):
+def workload(name: str, dtype: str, rows=None, realize=None):
     """(program, host inputs, tokens per step, contraction flops, config record)
-    of a workload; `rows` shrinks it for the CPU sample."""
+    of a workload; `rows` shrinks it for the CPU sample; `realize` (`@FILE`)
+    gives the GPT's sites their storage types (a mixed realization)."""
     from presk_amd import configs, gpt
+    from presk_amd.realize import Realization
 
     if name == "mlp":
         r = rows or 8192
@@ -41,12 +43,14 @@ def workload(name: str, dtype: str, rows=None):
         return p, host, r, flops, cfg
     train = name == "gpt-step"
     s = gpt.COURSE if rows is None else gpt.GptShape(B=max(rows // gpt.COURSE.T, 1))
-    p, b, names = gpt.build(s, dtype, train=train)
+    r = Realization.parse(realize) if realize else None
+    p, b, names = gpt.build(s, dtype, train=train, realize=r)
     host = gpt.host_inputs(s)
     cfg = {"workload": ("config 4: course GPT training step (loss value and gradient of every parameter)" if train
                         else "config 3: course GPT forward and loss"),
            "L": s.L, "d_model": s.D, "heads": s.H, "vocab": s.V, "batch": s.B, "seq": s.T,
-           "storage": dtype, "compute": "f32", "launches": len(p.launches), "dropout": 0.0}
+           "storage": dtype if r is None else f"mixed ({realize})", "compute": "f32", "launches": len(p.launches),
+           "dropout": 0.0}
     return p, host, s.B * s.T, gpt.contraction_flops(s, train), cfg
 
 
@@ -88,13 +92,13 @@ def copy_probe():
     print(json.dumps({"copy_probe": low.name, "bytes_read": 4 * n, "bytes_written": 4 * n, "runs": 3}), flush=True)
 
 
-def cpu_baseline(name: str, dtype: str, rows: int, threads: int):
+def cpu_baseline(name: str, dtype: str, rows: int, threads: int, realize=None):
     """The oracle (the kernel interpreter's semantics in C, -O3 -march=native,
     the outermost parallel loop split over OpenMP threads as the native
     executor splits it) on a bounded sample of the workload's rows."""
     from tests import cpu_program
 
-    p, host, tokens, _, _ = workload(name, dtype, rows)
+    p, host, tokens, _, _ = workload(name, dtype, rows, realize)
     cpu_program.compile_all(p, native=True, workers=threads)
     best = None
     for _ in range(1 if name.startswith("gpt") else 2):
@@ -112,6 +116,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="gpt-step", choices=["gpt-step", "gpt-forward", "mlp", "linear"])
     ap.add_argument("--dtype", default=None)
+    ap.add_argument("--realize", default=None, metavar="@FILE",
+                    help="a realization file (the reference's schema) for the GPT workloads: storage type per site")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="issue the launches one by one instead of one HIP graph")
     ap.add_argument("--dominant-only", type=int, default=0, metavar="N",
@@ -131,7 +137,7 @@ def main():
         copy_probe()
         return
     dtype = args.dtype or ("bf16" if args.workload == "mlp" else "f32")
-    p, host, tokens, flops, cfg = workload(args.workload, dtype)
+    p, host, tokens, flops, cfg = workload(args.workload, dtype, realize=args.realize)
     p.compile()
     configs.load_inputs(p, host)
     p.prepare()
@@ -165,7 +171,7 @@ def main():
     traffic = TRAFFIC.get(key)
     if c.flops > 0:
         achieved = c.flops / (ms * 1e-3) / 1e12
-        peak = PEAK_TFLOPS[dtype]
+        peak = PEAK_TFLOPS[ln.low.dtype]
         roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "mfma", "achieved": round(achieved, 2),
                 "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                 "ms_per_launch": round(ms, 5), "algorithmic_flops": c.flops}
@@ -185,17 +191,22 @@ def main():
         e["ms"] = round(e["ms"], 4)
 
     cfg = dict(cfg, launch="eager" if args.eager else "hip graph")
-    metric = METRIC if args.workload == "gpt-step" else f"rows/sec {args.workload} (a supplementary workload)"
+    # the contractions' time at the MFMA peak of each one's storage type over
+    # the step's time: flops / peak for one type, weighted for a mixed one
+    bound_ms = sum(l.compiled.flops / (PEAK_TFLOPS.get(l.low.dtype, PEAK_TFLOPS["f32"]) * 1e12) * 1e3
+                   for l in p.launches if l.compiled.kind == "gemm")
+    metric = {"gpt-step": METRIC, "gpt-forward": "tokens/sec course-GPT forward and loss (config 3)"}.get(
+        args.workload, f"rows/sec {args.workload} (a supplementary workload)")
     rec = {"metric": metric, "value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,1) inputs, xavier weights)",
            "config": cfg, "matmul_tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
-           "matmul_frac_of_peak": round(flops / (ms_step * 1e-3) / 1e12 / PEAK_TFLOPS[dtype], 4), "roofline": roof,
+           "matmul_frac_of_peak": round(bound_ms / ms_step, 4), "roofline": roof,
            "kernels": per_kernel}
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)
         rows = args.cpu_rows or {"mlp": 4096, "linear": 1024, "gpt-step": 2048, "gpt-forward": 4096}[args.workload]
-        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads)
+        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads, args.realize)
         rec["cpu_baseline"] = {"value": round(v, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
                                "sample": f"{n} of {tokens} tokens (rows) of the same workload: the oracle's C restatement of "
                                          f"the same default-layout nests (-O3 -march=native, -ffp-contract=off, sequential "

@@ -94,6 +94,7 @@ def storage_inputs(p: Program, host: dict) -> dict:
     env = {}
     for ln in p.launches:
         for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
+            ty = p.input_types.get(name, ty) if ty != "i64" else ty
             if name in host and name not in env:
                 v = host[name]
                 if ty == "i64":
@@ -107,8 +108,8 @@ def load_inputs(p: Program, host: dict):
     """Declares and uploads every host input in the program's storage type."""
     specs = {}
     for ln in p.launches:
-        for name, spec in zip(ln.ins, _input_specs(ln.low)):
-            specs.setdefault(name, spec)
+        for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
+            specs.setdefault(name, (p.input_types.get(name, ty) if ty != "i64" else ty, count))
     for name, arr in storage_inputs(p, host).items():
         ty, count = specs[name]
         p.declare(name, ty, max(count, 1))

@@ -24,7 +24,9 @@ gradient against torch autograd, tests/test_gpt_program.py).
 """
 from __future__ import annotations
 
+import contextlib
 import math
+import re
 from dataclasses import dataclass
 
 import numpy as np
@@ -54,13 +56,27 @@ COURSE = GptShape()
 
 
 class Builder:
-    """Buffers by name with their axes and kind; each primitive one launch."""
+    """Buffers by name with their axes and kind; each primitive one launch.
 
-    def __init__(self, prog: Program, dtype: str):
-        self.p, self.dt = prog, dtype
+    Each launch is a site, `<function>/<let>` (crates/presk-rt/src/lib.rs:370-373):
+    the function is the builder's current one (`func`), the let the result's
+    name.  Its storage type is the realization's for the site when one is
+    given (`Realization.dtype_at`), else the builder's one type."""
+
+    def __init__(self, prog: Program, dtype: str, realize=None):
+        self.p, self.dt, self.realize = prog, dtype, realize
         self.axes: dict = {}
         self.kind: dict = {}
         self.n = 0
+        self.fn = "MiniGPT.apply"
+
+    @contextlib.contextmanager
+    def func(self, name: str):
+        prev, self.fn = self.fn, name
+        try:
+            yield
+        finally:
+            self.fn = prev
 
     def input(self, name, axes, kind="real"):
         self.axes[name], self.kind[name] = list(axes), kind
@@ -69,92 +85,110 @@ class Builder:
     def op(self, name):
         return O(self.axes[name], self.kind[name])
 
-    def _out(self, low, ins, name=None):
+    def _name(self, name):
         if name is None:
             self.n += 1
             name = f"t{self.n}"
+        return name
+
+    def _dt(self, name):
+        """The site's storage type; the site's let is the result's name
+        without its layer (`b3.scores` -> `scores`), so that one entry names a
+        let of every layer, as a site of a function does in the reference."""
+        if self.realize is None:
+            return self.dt
+        return self.realize.dtype_at(f"{self.fn}/{re.sub(r'^b[0-9]+[.]', '', name)}")
+
+    def _out(self, low, ins, name):
         self.p.add(low, ins, name)
         self.axes[name], self.kind[name] = list(low.out_axes), low.out_kind
         return name
 
+    def _prim(self, make, ins, name):
+        """One primitive: `make(dtype)` lowers it at the site's storage type."""
+        name = self._name(name)
+        return self._out(make(self._dt(name)), ins, name)
+
     # --- primitives -----------------------------------------------------------
     def binary(self, op, a, b, name=None):
-        return self._out(L.elementwise_binary(op, [self.op(a), self.op(b)], self.dt), [a, b], name)
+        return self._prim(lambda dt: L.elementwise_binary(op, [self.op(a), self.op(b)], dt), [a, b], name)
 
     def unary(self, op, a, name=None):
-        return self._out(L.unary(op, [self.op(a)], self.dt), [a], name)
+        return self._prim(lambda dt: L.unary(op, [self.op(a)], dt), [a], name)
 
     def fused(self, steps, ins, out_like, name=None):
-        return self._out(L.fused(steps, [self.op(i) for i in ins], self.axes[out_like], self.dt), ins, name)
+        return self._prim(lambda dt: L.fused(steps, [self.op(i) for i in ins], self.axes[out_like], dt), ins, name)
 
     def dot(self, x, w, b=None, name=None):
-        d = L.dot([self.op(x), self.op(w)], self.dt)
-        if b is None:
-            return self._out(d, [x, w], name)
-        return self._out(L.dot([self.op(x), self.op(w), self.op(b)], self.dt, epilogue=(True, d.out_axes)), [x, w, b], name)
+        def make(dt):
+            d = L.dot([self.op(x), self.op(w)], dt)
+            if b is None:
+                return d
+            return L.dot([self.op(x), self.op(w), self.op(b)], dt, epilogue=(True, d.out_axes))
+        return self._prim(make, [x, w] if b is None else [x, w, b], name)
 
     def dot_vjp_l(self, ct, b, name=None):
-        return self._out(L.dot_vjp_l([self.op(ct), self.op(b)], self.dt), [ct, b], name)
+        return self._prim(lambda dt: L.dot_vjp_l([self.op(ct), self.op(b)], dt), [ct, b], name)
 
     def dot_vjp_r(self, a, ct, name=None):
-        return self._out(L.dot_vjp_r([self.op(a), self.op(ct)], self.dt), [a, ct], name)
+        return self._prim(lambda dt: L.dot_vjp_r([self.op(a), self.op(ct)], dt), [a, ct], name)
 
     def ein(self, a, b, la, lb, out, name=None, like=None):
         """`like`: the value whose type the result has -- an operand's, for the
         `ein` of its cotangent (rules.rs:151-169 gives it `tys[j]`)."""
-        r = self._out(L.ein([self.op(a), self.op(b)], [la, lb], out, self.dt), [a, b], name)
+        r = self._prim(lambda dt: L.ein([self.op(a), self.op(b)], [la, lb], out, dt), [a, b], name)
         if like is not None:
             self.axes[r] = list(self.axes[like])
         return r
 
     def mean(self, x, axis, name=None):
-        return self._out(L.reduce_axis("mean", axis, [self.op(x)], self.dt), [x], name)
+        return self._prim(lambda dt: L.reduce_axis("mean", axis, [self.op(x)], dt), [x], name)
 
     def sum(self, x, axis, name=None):
-        return self._out(L.reduce_axis("sum", axis, [self.op(x)], self.dt), [x], name)
+        return self._prim(lambda dt: L.reduce_axis("sum", axis, [self.op(x)], dt), [x], name)
 
     def mean_all(self, x, name=None):
-        return self._out(L.reduce_all("mean_all", [self.op(x)], self.dt), [x], name)
+        return self._prim(lambda dt: L.reduce_all("mean_all", [self.op(x)], dt), [x], name)
 
     def mean_vjp(self, ct, like, axis, name=None):
-        return self._out(L.mean_vjp(axis, [self.op(ct), self.op(like)], self.dt), [ct, like], name)
+        return self._prim(lambda dt: L.mean_vjp(axis, [self.op(ct), self.op(like)], dt), [ct, like], name)
 
     def sum_to(self, x, like, name=None):
-        return self._out(L.sum_to([self.op(x), self.op(like)], self.dt), [x, like], name)
+        return self._prim(lambda dt: L.sum_to([self.op(x), self.op(like)], dt), [x, like], name)
 
     def broadcast_like(self, x, like, name=None):
-        return self._out(L.broadcast_like([self.op(x), self.op(like)], self.dt), [x, like], name)
+        return self._prim(lambda dt: L.broadcast_like([self.op(x), self.op(like)], dt), [x, like], name)
 
     def masked_softmax(self, x, mask, axis, name=None):
-        return self._out(L.masked_softmax(axis, [self.op(x), self.op(mask)], self.dt), [x, mask], name)
+        return self._prim(lambda dt: L.masked_softmax(axis, [self.op(x), self.op(mask)], dt), [x, mask], name)
 
     def embed(self, table, ids, name=None):
-        out = self._out(L.embed([self.op(table), self.op(ids)], self.dt), [table, ids], name)
+        out = self._prim(lambda dt: L.embed([self.op(table), self.op(ids)], dt), [table, ids], name)
         # the result's last axis is the table's (its type names it)
         last = self.axes[table][-1]
         self.axes[out][-1] = L.Axis(last.name, last.len)
         return out
 
     def embed_vjp(self, table, ids, ct, name=None):
-        return self._out(L.embed_vjp([self.op(table), self.op(ids), self.op(ct)], self.dt), [table, ids, ct], name)
+        return self._prim(lambda dt: L.embed_vjp([self.op(table), self.op(ids), self.op(ct)], dt), [table, ids, ct], name)
 
     def split_heads(self, x, h, hd, name=None):
-        return self._out(L.split_heads(h, hd, [self.op(x)], self.dt), [x], name)
+        return self._prim(lambda dt: L.split_heads(h, hd, [self.op(x)], dt), [x], name)
 
     def merge_heads(self, x, h, hd, name=None):
-        return self._out(L.merge_heads(h, hd, [self.op(x)], self.dt), [x], name)
+        return self._prim(lambda dt: L.merge_heads(h, hd, [self.op(x)], dt), [x], name)
 
     def cross_entropy(self, logits, y, name=None):
-        return self._out(L.cross_entropy([self.op(logits), self.op(y)], self.dt), [logits, y], name)
+        return self._prim(lambda dt: L.cross_entropy([self.op(logits), self.op(y)], dt), [logits, y], name)
 
     def cross_entropy_vjp(self, logits, y, ct, name=None):
-        return self._out(L.cross_entropy_vjp([self.op(logits), self.op(y), self.op(ct)], self.dt), [logits, y, ct], name)
+        return self._prim(lambda dt: L.cross_entropy_vjp([self.op(logits), self.op(y), self.op(ct)], dt), [logits, y, ct], name)
 
     def causal_mask(self, T, name):
-        return self._out(L.causal_mask("seq", T, self.dt), [], name)
+        return self._prim(lambda dt: L.causal_mask("seq", T, dt), [], name)
 
     def positions(self, T, name):
-        return self._out(L.positions("seq", T, self.dt), [], name)
+        return self._prim(lambda dt: L.positions("seq", T, dt), [], name)
 
 
 def param_shapes(s: GptShape) -> dict:
@@ -199,6 +233,11 @@ def _layernorm(b: Builder, x, g, bias, keep: bool, tag: str):
     """examples/corpus/nlp/05_gpt.psk LayerNorm: (x - mu) / sqrt(var + eps) * g + b.
     `keep`: the training entry keeps the values the gradient reads
     (x - mu, sqrt(var + eps), the normalized x), so they reach memory."""
+    with b.func("LayerNorm.apply"):
+        return _layernorm_in(b, x, g, bias, keep, tag)
+
+
+def _layernorm_in(b: Builder, x, g, bias, keep: bool, tag: str):
     mu = b.mean(x, "model", name=f"{tag}.mu")
     if not keep:
         sq = b.fused([("sub", [("in", 0), ("in", 1)]), ("pow2", [("step", 0)])], [x, mu], x)
@@ -219,6 +258,11 @@ def _layernorm_vjp(b: Builder, saved, dy, tag):
     """The LayerNorm's reverse mode (rules.rs: add, mul, div, sqrt, pow(2),
     mean, sub), cotangents added where a value has two consumers.  Returns dx,
     dg, dbias."""
+    with b.func("LayerNorm.apply.vjp"):
+        return _layernorm_vjp_in(b, saved, dy, tag)
+
+
+def _layernorm_vjp_in(b: Builder, saved, dy, tag):
     xm, sd, xh, g = saved["xm"], saved["sd"], saved["xh"], saved["g"]
     db = b.sum_to(dy, saved["b"], name=f"{tag}.dbias")                      # add: sum_to to b's axes
     dg = b.sum_to(b.binary("mul", dy, xh), g, name=f"{tag}.dg")            # mul by g: ct * xh, to g's axes
@@ -240,13 +284,22 @@ def _layernorm_vjp(b: Builder, saved, dy, tag):
     return dx, dg, db
 
 
-def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None) -> tuple:
+def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realize=None) -> tuple:
     """The program of config 3 (`train=False`: loss only) or config 4.
     Returns (program, builder, names) with names["loss"] and, for training,
-    names["grads"][param] = buffer of its gradient."""
+    names["grads"][param] = buffer of its gradient.  `realize`: a
+    Realization giving each site its storage type (else `dtype` everywhere);
+    parameters are held at rest in its `params` types (else f32) and every
+    kernel reads its inputs converted at its edge."""
     from . import hip
-    p = Program(f"gpt-{'step' if train else 'forward'}-{dtype}", mode=hip.FAST if mode is None else mode)
-    b = Builder(p, dtype)
+    tag = dtype if realize is None else "mixed"
+    p = Program(f"gpt-{'step' if train else 'forward'}-{tag}", mode=hip.FAST if mode is None else mode)
+    b = Builder(p, dtype, realize)
+    if realize is not None:
+        for name in param_shapes(s):
+            p.input_types[name] = realize.param_dtype(name)
+        for name in ("eps", "scale", "two", "one"):
+            p.input_types[name] = "f32"
     for name, axes in param_shapes(s).items():
         b.input(name, axes)
     b.input("ids", A(("batch", s.B), ("seq", s.T)), "idx")
@@ -257,9 +310,10 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None) -> tup
     b.input("one", A())         # the loss's cotangent
     mask = b.causal_mask(s.T, "mask")
     pos_ids = b.positions(s.T, "pos_ids")
-    te = b.embed("tok", "ids", name="te")
-    pe = b.embed("pos", pos_ids, name="pe")
-    x = b.binary("add", te, pe, name="h0")
+    with b.func("Embedding.apply"):
+        te = b.embed("tok", "ids", name="te")
+        pe = b.embed("pos", pos_ids, name="pe")
+        x = b.binary("add", te, pe, name="h0")
     saved = []
     H, HD = s.H, s.HD
     lbl_q = ["batch", "heads", "seq", "hd"]
@@ -268,22 +322,28 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None) -> tup
     for l in range(s.L):
         pr = f"b{l}."
         xn1, ln1 = _layernorm(b, x, pr + "ln1.g", pr + "ln1.b", train, f"b{l}.ln1")
-        q = b.dot(xn1, pr + "wq", pr + "wq.b")
-        k = b.dot(xn1, pr + "wk", pr + "wk.b")
-        v = b.dot(xn1, pr + "wv", pr + "wv.b")
-        qh, kh, vh = b.split_heads(q, H, HD), b.split_heads(k, H, HD), b.split_heads(v, H, HD)
-        sc = b.ein(qh, kh, lbl_q, lbl_k, lbl_s)
-        sc2 = b.binary("div", sc, "scale")
-        a = b.masked_softmax(sc2, mask, "seq2")
-        o = b.ein(a, vh, lbl_s, lbl_k, lbl_q)
-        om = b.merge_heads(o, H, HD)
-        ao = b.dot(om, pr + "wo", pr + "wo.b")
-        h = b.binary("add", x, ao)
+        with b.func("SelfAttention.apply"):
+            q = b.dot(xn1, pr + "wq", pr + "wq.b", name=pr + "q")
+            k = b.dot(xn1, pr + "wk", pr + "wk.b", name=pr + "k")
+            v = b.dot(xn1, pr + "wv", pr + "wv.b", name=pr + "v")
+            qh = b.split_heads(q, H, HD, name=pr + "qh")
+            kh = b.split_heads(k, H, HD, name=pr + "kh")
+            vh = b.split_heads(v, H, HD, name=pr + "vh")
+            sc = b.ein(qh, kh, lbl_q, lbl_k, lbl_s, name=pr + "scores")
+            sc2 = b.binary("div", sc, "scale", name=pr + "scaled")
+            a = b.masked_softmax(sc2, mask, "seq2", name=pr + "probs")
+            o = b.ein(a, vh, lbl_s, lbl_k, lbl_q, name=pr + "o")
+            om = b.merge_heads(o, H, HD, name=pr + "om")
+            ao = b.dot(om, pr + "wo", pr + "wo.b", name=pr + "ao")
+        with b.func("Block.apply"):
+            h = b.binary("add", x, ao, name=pr + "h")
         xn2, ln2 = _layernorm(b, h, pr + "ln2.g", pr + "ln2.b", train, f"b{l}.ln2")
-        u = b.dot(xn2, pr + "up", pr + "up.b")
-        g = b.unary("gelu", u)
-        dn = b.dot(g, pr + "down", pr + "down.b")
-        xo = b.binary("add", h, dn)
+        with b.func("MLP.apply"):
+            u = b.dot(xn2, pr + "up", pr + "up.b", name=pr + "u")
+            g = b.unary("gelu", u, name=pr + "g")
+            dn = b.dot(g, pr + "down", pr + "down.b", name=pr + "dn")
+        with b.func("Block.apply"):
+            xo = b.binary("add", h, dn, name=pr + "xo")
         saved.append(dict(x=x, xn1=xn1, ln1=ln1, qh=qh, kh=kh, vh=vh, a=a, om=om, h=h, xn2=xn2, ln2=ln2, u=u, g=g))
         x = xo
     xf, lnf = _layernorm(b, x, "lnf.g", "lnf.b", train, "lnf")
@@ -295,54 +355,60 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None) -> tup
         return p, b, names
     G = names["grads"]
     # ---- reverse mode -------------------------------------------------------
-    dce = b.mean_vjp("one", ce, None)
-    dlogits = b.cross_entropy_vjp(logits, "y", dce)
-    dxf = b.dot_vjp_l(dlogits, "head")
-    G["head"] = b.dot_vjp_r(xf, dlogits, name="d.head")
+    with b.func("MiniGPT.apply.vjp"):
+        dce = b.mean_vjp("one", ce, None)
+        dlogits = b.cross_entropy_vjp(logits, "y", dce)
+        dxf = b.dot_vjp_l(dlogits, "head")
+        G["head"] = b.dot_vjp_r(xf, dlogits, name="d.head")
     dx, G["lnf.g"], G["lnf.b"] = _layernorm_vjp(b, lnf, dxf, "lnf")
     for l in reversed(range(s.L)):
         pr, sv = f"b{l}.", saved[l]
         # xo = h + dn
         ddn = dx
-        dg_ = b.dot_vjp_l(ddn, pr + "down")
-        G[pr + "down"] = b.dot_vjp_r(sv["g"], ddn, name="d." + pr + "down")
-        G[pr + "down.b"] = b.sum_to(ddn, pr + "down.b", name="d." + pr + "down.b")
-        du = b.fused([("gelu_deriv", [("in", 1)]), ("mul", [("in", 0), ("step", 0)])], [dg_, sv["u"]], sv["u"])
-        dxn2 = b.dot_vjp_l(du, pr + "up")
-        G[pr + "up"] = b.dot_vjp_r(sv["xn2"], du, name="d." + pr + "up")
-        G[pr + "up.b"] = b.sum_to(du, pr + "up.b", name="d." + pr + "up.b")
+        with b.func("MLP.apply.vjp"):
+            dg_ = b.dot_vjp_l(ddn, pr + "down")
+            G[pr + "down"] = b.dot_vjp_r(sv["g"], ddn, name="d." + pr + "down")
+            G[pr + "down.b"] = b.sum_to(ddn, pr + "down.b", name="d." + pr + "down.b")
+            du = b.fused([("gelu_deriv", [("in", 1)]), ("mul", [("in", 0), ("step", 0)])], [dg_, sv["u"]], sv["u"])
+            dxn2 = b.dot_vjp_l(du, pr + "up")
+            G[pr + "up"] = b.dot_vjp_r(sv["xn2"], du, name="d." + pr + "up")
+            G[pr + "up.b"] = b.sum_to(du, pr + "up.b", name="d." + pr + "up.b")
         dh_ln, G[pr + "ln2.g"], G[pr + "ln2.b"] = _layernorm_vjp(b, sv["ln2"], dxn2, f"b{l}.ln2")
-        dh = b.binary("add", dx, dh_ln)
+        with b.func("Block.apply.vjp"):
+            dh = b.binary("add", dx, dh_ln)
         # h = x + ao
         dao = dh
-        dom = b.dot_vjp_l(dao, pr + "wo")
-        G[pr + "wo"] = b.dot_vjp_r(sv["om"], dao, name="d." + pr + "wo")
-        G[pr + "wo.b"] = b.sum_to(dao, pr + "wo.b", name="d." + pr + "wo.b")
-        do = b.split_heads(dom, H, HD)
-        da = b.ein(do, sv["vh"], lbl_q, lbl_k, lbl_s, like=sv["a"])
-        dvh = b.ein(do, sv["a"], lbl_q, lbl_s, lbl_k, like=sv["vh"])
-        # softmax: a * (da - broadcast(sum(da * a)))
-        t = b.binary("mul", da, sv["a"])
-        ssum = b.sum(t, "seq2")
-        sb = b.broadcast_like(ssum, da)
-        dsc2 = b.fused([("sub", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("step", 0)])], [da, sb, sv["a"]], da)
-        dsc = b.binary("div", dsc2, "scale")
-        dqh = b.ein(dsc, sv["kh"], lbl_s, lbl_k, lbl_q, like=sv["qh"])
-        dkh = b.ein(dsc, sv["qh"], lbl_s, lbl_q, lbl_k, like=sv["kh"])
-        dq, dk, dv = b.merge_heads(dqh, H, HD), b.merge_heads(dkh, H, HD), b.merge_heads(dvh, H, HD)
-        dxq = b.dot_vjp_l(dq, pr + "wq")
-        dxk = b.dot_vjp_l(dk, pr + "wk")
-        dxv = b.dot_vjp_l(dv, pr + "wv")
-        for w, dw in (("wq", dq), ("wk", dk), ("wv", dv)):
-            G[pr + w] = b.dot_vjp_r(sv["xn1"], dw, name="d." + pr + w)
-            G[pr + w + ".b"] = b.sum_to(dw, pr + w + ".b", name="d." + pr + w + ".b")
-        dxn1 = b.fused([("add", [("in", 0), ("in", 1)]), ("add", [("step", 0), ("in", 2)])], [dxq, dxk, dxv], dxq)
+        with b.func("SelfAttention.apply.vjp"):
+            dom = b.dot_vjp_l(dao, pr + "wo")
+            G[pr + "wo"] = b.dot_vjp_r(sv["om"], dao, name="d." + pr + "wo")
+            G[pr + "wo.b"] = b.sum_to(dao, pr + "wo.b", name="d." + pr + "wo.b")
+            do = b.split_heads(dom, H, HD)
+            da = b.ein(do, sv["vh"], lbl_q, lbl_k, lbl_s, like=sv["a"])
+            dvh = b.ein(do, sv["a"], lbl_q, lbl_s, lbl_k, like=sv["vh"])
+            # softmax: a * (da - broadcast(sum(da * a)))
+            t = b.binary("mul", da, sv["a"])
+            ssum = b.sum(t, "seq2")
+            sb = b.broadcast_like(ssum, da)
+            dsc2 = b.fused([("sub", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("step", 0)])], [da, sb, sv["a"]], da)
+            dsc = b.binary("div", dsc2, "scale")
+            dqh = b.ein(dsc, sv["kh"], lbl_s, lbl_k, lbl_q, like=sv["qh"])
+            dkh = b.ein(dsc, sv["qh"], lbl_s, lbl_q, lbl_k, like=sv["kh"])
+            dq, dk, dv = b.merge_heads(dqh, H, HD), b.merge_heads(dkh, H, HD), b.merge_heads(dvh, H, HD)
+            dxq = b.dot_vjp_l(dq, pr + "wq")
+            dxk = b.dot_vjp_l(dk, pr + "wk")
+            dxv = b.dot_vjp_l(dv, pr + "wv")
+            for w, dw in (("wq", dq), ("wk", dk), ("wv", dv)):
+                G[pr + w] = b.dot_vjp_r(sv["xn1"], dw, name="d." + pr + w)
+                G[pr + w + ".b"] = b.sum_to(dw, pr + w + ".b", name="d." + pr + w + ".b")
+            dxn1 = b.fused([("add", [("in", 0), ("in", 1)]), ("add", [("step", 0), ("in", 2)])], [dxq, dxk, dxv], dxq)
         dx_ln, G[pr + "ln1.g"], G[pr + "ln1.b"] = _layernorm_vjp(b, sv["ln1"], dxn1, f"b{l}.ln1")
-        dx = b.binary("add", dh, dx_ln)
+        with b.func("Block.apply.vjp"):
+            dx = b.binary("add", dh, dx_ln)
     # h0 = te + pe: te's cotangent dx; pe's sum_to over the batch
-    G["tok"] = b.embed_vjp("tok", "ids", dx, name="d.tok")
-    dpe = b.sum_to(dx, pe)
-    G["pos"] = b.embed_vjp("pos", pos_ids, dpe, name="d.pos")
+    with b.func("Embedding.apply.vjp"):
+        G["tok"] = b.embed_vjp("tok", "ids", dx, name="d.tok")
+        dpe = b.sum_to(dx, pe)
+        G["pos"] = b.embed_vjp("pos", pos_ids, dpe, name="d.pos")
     return p, b, names
 
 

@@ -73,6 +73,12 @@ class Program:
         self.bufs = Buffers()
         self._flag = None
         self._batch = None
+        # a host input's storage type when it is not its first reader's (a
+        # mixed realization's parameters at rest)
+        self.input_types: dict = {}
+        # the prepared sequence: ("launch", Launch) and, where a kernel reads a
+        # buffer of another storage type, ("convert", src, from, dst, to, n)
+        self.steps: list = []
 
     def add(self, low: L.Lowered, ins: list, out: str) -> str:
         """Appends one launch of `low` reading buffers `ins`, writing `out`."""
@@ -96,16 +102,42 @@ class Program:
         return self.bufs.alloc(name, ty, count)
 
     def prepare(self):
+        """Allocates every output and builds each launch's pointer table.  A
+        kernel that reads a real buffer of another storage type reads it
+        converted at its edge (crates/presk-kernel/src/host.rs:793-829): one
+        conversion per buffer and type, before its first such reader -- every
+        buffer is written once per call, so later readers see the same
+        values."""
+        self.steps = []
+        converted = {}
         for ln in self.launches:
             c = ln.compiled
             ty = ln.low.dtype if ln.low.out_kind == "real" else "i64"
+            names = []
+            for n in ln.ins:
+                src_ty, count = self.bufs.meta[n]
+                if src_ty != "i64" and src_ty != ln.low.dtype:
+                    key = (n, ln.low.dtype)
+                    if key not in converted:
+                        dst = f"{n}@{ln.low.dtype}"
+                        self.bufs.alloc(dst, ln.low.dtype, count)
+                        self.steps.append(("convert", n, src_ty, dst, ln.low.dtype, count))
+                        converted[key] = dst
+                    n = converted[key]
+                names.append(n)
             self.bufs.alloc(ln.out, ty, numel(ln.low.out_axes))
-            ptrs = [self.bufs.dev[n].ptr for n in ln.ins] + [self.bufs.dev[ln.out].ptr]
+            ptrs = [self.bufs.dev[n].ptr for n in names] + [self.bufs.dev[ln.out].ptr]
             if c.guarded:
                 ptrs.append(self._flag.ptr)
             ln.table = (ctypes.c_void_p * len(ptrs))(*ptrs)
+            self.steps.append(("launch", ln))
         self._flag.zero()
         return self
+
+    def _convert(self, step, stream=None):
+        _, src, frm, dst, to, n = step
+        hip.check(hip.lib().presk_hip_convert(self.bufs.dev[src].ptr, frm.encode(), self.bufs.dev[dst].ptr, to.encode(),
+                                              n, self._flag.ptr, stream))
 
     def record(self, graph: bool = True):
         """Hands the prepared launch sequence to the executor: `run` then
@@ -115,9 +147,14 @@ class Program:
         b = ctypes.c_void_p()
         hip.check(lib.presk_hip_batch_create(ctypes.byref(b)))
         self._batch = b
-        for ln in self.launches:
-            c = ln.compiled
-            hip.check(lib.presk_hip_batch_add(b, c.handle, ln.table, 0, max(c.split_bound, 0)))
+        for st in self.steps:
+            if st[0] == "convert":
+                _, src, frm, dst, to, n = st
+                hip.check(lib.presk_hip_batch_add_convert(b, self.bufs.dev[src].ptr, frm.encode(), self.bufs.dev[dst].ptr,
+                                                          to.encode(), n, self._flag.ptr))
+                continue
+            c = st[1].compiled
+            hip.check(lib.presk_hip_batch_add(b, c.handle, st[1].table, 0, max(c.split_bound, 0)))
         if graph:
             hip.check(lib.presk_hip_batch_graph(b))
         return self
@@ -138,9 +175,12 @@ class Program:
         if self._batch is not None:
             hip.check(lib.presk_hip_batch_run(self._batch, stream))
             return
-        for ln in self.launches:
-            c = ln.compiled
-            rc = lib.presk_hip_run(c.handle, ln.table, 0, max(c.split_bound, 0), stream)
+        for st in self.steps:
+            if st[0] == "convert":
+                self._convert(st, stream)
+                continue
+            c = st[1].compiled
+            rc = lib.presk_hip_run(c.handle, st[1].table, 0, max(c.split_bound, 0), stream)
             if rc:
                 hip.check(rc)
 
