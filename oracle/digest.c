@@ -25,6 +25,8 @@
 #define F_LOG presk_logf
 #define F_TANH presk_tanhf
 #define F_ERF presk_erff
+#define F_SIN presk_sinf
+#define F_COS presk_cosf
 static inline uint16_t C_BF16(float x) { return presk_f32_to_bf16(x); }
 static inline uint16_t C_F16(float x) { return presk_f32_to_f16(x); }
 static inline uint32_t C_E8(float x) { return presk_f32_to_e8m15_code(x); }
@@ -41,6 +43,10 @@ float ok_expf(float);
 float ok_logf(float);
 float ok_tanhf(float);
 float ok_erff(float);
+float ok_sinf(float);
+float ok_cosf(float);
+#define F_SIN ok_sinf
+#define F_COS ok_cosf
 #define F_EXP ok_expf
 #define F_LOG ok_logf
 #define F_TANH ok_tanhf
@@ -82,7 +88,7 @@ uint64_t pd_sample_f64_bits(uint64_t i)
     return (r & (1ull << 63)) | (e << 52) | frac;
 }
 
-/* Function ids: 0 expf, 1 logf, 2 tanhf, 3 erff (every f32);
+/* Function ids: 0 expf, 1 logf, 2 tanhf, 3 erff, 4 sinf, 5 cosf (every f32);
  * 10 f32->bf16, 11 f32->f16, 12 f32->e8m15, 32 f16 guard, 33 e8m15 guard
  * (every f32); 20 bf16->f32, 21 f16->f32 (every code of 16 bits),
  * 22 e8m15->f32 (every 24-bit code); 30 f64->f16, 31 f64->e8m15 (the sample). */
@@ -94,6 +100,8 @@ static inline uint32_t eval1(int fn, uint64_t i, int *ok)
     case 1: return b_of(F_LOG(f_of((uint32_t)i)));
     case 2: return b_of(F_TANH(f_of((uint32_t)i)));
     case 3: return b_of(F_ERF(f_of((uint32_t)i)));
+    case 4: return b_of(F_SIN(f_of((uint32_t)i)));
+    case 5: return b_of(F_COS(f_of((uint32_t)i)));
     case 10: return C_BF16(f_of((uint32_t)i));
     case 11: return C_F16(f_of((uint32_t)i));
     case 12: return C_E8(f_of((uint32_t)i));

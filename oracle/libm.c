@@ -307,3 +307,249 @@ float ok_erff(float x)
         y = 1 - 0x1p-120f;
     return neg ? -y : y;
 }
+
+/* ---- sinf / cosf --------------------------------------------------------
+ * fdlibm's method in f64 arithmetic (presk_libm.c:672-746 the kernels
+ * __sindf/__cosdf, 1372-1447 __rem_pio2f, 749-1189 __rem_pio2_large,
+ * 2054-2111 sinf, 2213-2272 cosf): |x| <= pi/4 direct; up to 9pi/4 one
+ * subtraction of a multiple of pi/2 rounded to f64; below 2^28*pi/2 the
+ * reduction by 25+53 bits of pi/2; beyond it Payne-Hanek with the 24-bit
+ * digits of 2/pi (one piece of x, single precision: fdlibm's jk = 3). */
+
+/* minimax polynomials of sin(x) on [-pi/4, pi/4] (odd) and cos(x) (even) */
+static float lm_ksin(double x)
+{
+    const double S1 = -0x15555554cbac77.0p-55, S2 = 0x111110896efbb2.0p-59,
+                 S3 = -0x1a00f9e2cae774.0p-65, S4 = 0x16cd878c3b46a7.0p-71;
+    const double z = x * x, w = z * z, r = S3 + z * S4, s = z * x;
+    return (float)((x + s * (S1 + z * S2)) + s * w * r);
+}
+static float lm_kcos(double x)
+{
+    const double C0 = -0x1ffffffd0c5e81.0p-54, C1 = 0x155553e1053a42.0p-57,
+                 C2 = -0x16c087e80f1e27.0p-62, C3 = 0x199342e0ee5069.0p-68;
+    const double z = x * x, w = z * z, r = C2 + z * C3;
+    return (float)(((1.0 + z * C0) + w * C1) + (w * z) * r);
+}
+
+/* the first 24-bit digits of 2/pi after the binary point: digit i is
+ * ipio2[i] * 2^(-24(i+1)); an f32 argument needs no more than these */
+static const int32_t lm_ipio2[] = {
+    0xA2F983, 0x6E4E44, 0x1529FC, 0x2757D1, 0xF534DD, 0xC0DB62, 0x95993C, 0x439041, 0xFE5163, 0xABDEBB,
+    0xC561B7, 0x246E3A, 0x424DD2, 0xE00649, 0x2EEA09, 0xD1921C, 0xFE1DEB, 0x1CB129, 0xA73EE8, 0x8235F5,
+    0x2EBB44, 0x84E99C, 0x7026B4, 0x5F7E41, 0x3991D6, 0x398353, 0x39F49C, 0x845F8B, 0xBDF928, 0x3B1FF8,
+};
+/* pi/2 cut into 24-bit pieces */
+static const double lm_pio2_24[] = {
+    1.57079625129699707031e+00, 7.54978941586159635335e-08, 5.39030252995776476554e-15, 3.28200341580791294123e-22,
+};
+
+/* x (a positive f32 of exponent e0 + 23, as an integer of 24 bits times
+ * 2^e0) reduced mod pi/2: returns the quotient's low bits, the remainder in
+ * *y.  The steps of fdlibm's k_rem_pio2 with one piece and jk = 3. */
+static int lm_rem_pio2_big(double x0, int e0, double *y)
+{
+    enum { JK = 3 };
+    int32_t iq[20];
+    double f[20], q[20], fq[20] = {0};
+    int jv = (e0 - 3) / 24;
+    if (jv < 0)
+        jv = 0;
+    int q0 = e0 - 24 * (jv + 1);
+    for (int i = 0; i <= JK; i++) {
+        const int j = jv + i;
+        f[i] = j < 0 ? 0.0 : (double)lm_ipio2[j];
+    }
+    for (int i = 0; i <= JK; i++)
+        q[i] = 0.0 + x0 * f[i];
+    int jz = JK, n, ih;
+    double z;
+    for (;;) {
+        /* the product's 24-bit digits, most significant last */
+        z = q[jz];
+        for (int i = 0, j = jz; j > 0; i++, j--) {
+            const double hi = (double)(int32_t)(0x1p-24 * z);
+            iq[i] = (int32_t)(z - 0x1p24 * hi);
+            z = q[j - 1] + hi;
+        }
+        /* the integer part mod 8 */
+        z = ldexp(z, q0);
+        z -= 8.0 * floor(z * 0.125);
+        n = (int32_t)z;
+        z -= (double)n;
+        ih = 0;
+        if (q0 > 0) {
+            const int32_t top = iq[jz - 1] >> (24 - q0);
+            n += top;
+            iq[jz - 1] -= top << (24 - q0);
+            ih = iq[jz - 1] >> (23 - q0);
+        } else if (q0 == 0) {
+            ih = iq[jz - 1] >> 23;
+        } else if (z >= 0.5) {
+            ih = 2;
+        }
+        if (ih > 0) { /* fraction >= 1/2: take 1 - fraction, n + 1 */
+            n += 1;
+            int carry = 0;
+            for (int i = 0; i < jz; i++) {
+                const int32_t d = iq[i];
+                if (carry == 0) {
+                    if (d != 0) {
+                        carry = 1;
+                        iq[i] = 0x1000000 - d;
+                    }
+                } else {
+                    iq[i] = 0xffffff - d;
+                }
+            }
+            if (q0 == 1)
+                iq[jz - 1] &= 0x7fffff;
+            else if (q0 == 2)
+                iq[jz - 1] &= 0x3fffff;
+            if (ih == 2) {
+                z = 1.0 - z;
+                if (carry != 0)
+                    z -= ldexp(1.0, q0);
+            }
+        }
+        /* all digits of the fraction cancelled: take more of 2/pi */
+        if (z == 0.0) {
+            int32_t any = 0;
+            for (int i = jz - 1; i >= JK; i--)
+                any |= iq[i];
+            if (any == 0) {
+                int k = 1;
+                while (iq[JK - k] == 0)
+                    k++;
+                for (int i = jz + 1; i <= jz + k; i++) {
+                    f[i] = (double)lm_ipio2[jv + i];
+                    q[i] = 0.0 + x0 * f[i];
+                }
+                jz += k;
+                continue;
+            }
+        }
+        break;
+    }
+    /* drop the zero digits, or split a fraction past 24 bits */
+    if (z == 0.0) {
+        jz -= 1;
+        q0 -= 24;
+        while (iq[jz] == 0) {
+            jz--;
+            q0 -= 24;
+        }
+    } else {
+        z = ldexp(z, -q0);
+        if (z >= 0x1p24) {
+            const double hi = (double)(int32_t)(0x1p-24 * z);
+            iq[jz] = (int32_t)(z - 0x1p24 * hi);
+            jz += 1;
+            q0 += 24;
+            iq[jz] = (int32_t)hi;
+        } else {
+            iq[jz] = (int32_t)z;
+        }
+    }
+    double fw = ldexp(1.0, q0);
+    for (int i = jz; i >= 0; i--) {
+        q[i] = fw * (double)iq[i];
+        fw *= 0x1p-24;
+    }
+    /* times pi/2, digit by digit */
+    for (int i = jz; i >= 0; i--) {
+        fw = 0.0;
+        for (int k = 0; k <= JK && k <= jz - i; k++)
+            fw += lm_pio2_24[k] * q[i + k];
+        fq[jz - i] = fw;
+    }
+    fw = 0.0;
+    for (int i = jz; i >= 0; i--)
+        fw += fq[i];
+    *y = ih == 0 ? fw : -fw;
+    return n;
+}
+
+/* x mod pi/2 in *y (f64), the quotient's low bits returned */
+static int lm_rem_pio2f(float x, double *y)
+{
+    const double toint = 1.5 / 0x1p-52, invpio2 = 6.36619772367581382433e-01,
+                 pio2_1 = 1.57079631090164184570e+00, pio2_1t = 1.58932547735281966916e-08;
+    const uint32_t b = lm_bits(x), ix = b & 0x7fffffffu;
+    if (ix < 0x4dc90fdbu) {  /* |x| < 2^28 pi/2: 25 + 53 bits of pi/2 */
+        const double fn = (double)x * invpio2 + toint - toint;
+        *y = x - fn * pio2_1 - fn * pio2_1t;
+        return (int32_t)fn;
+    }
+    if (ix >= 0x7f800000u) {
+        *y = x - x;
+        return 0;
+    }
+    const int e0 = (int)(ix >> 23) - (0x7f + 23);
+    double r;
+    const int n = lm_rem_pio2_big((double)lm_from(ix - ((uint32_t)e0 << 23)), e0, &r);
+    if (b >> 31) {
+        *y = -r;
+        return -n;
+    }
+    *y = r;
+    return n;
+}
+
+float ok_sinf(float x)
+{
+    const double p1 = 1 * 1.57079632679489661923, p2 = 2 * 1.57079632679489661923,
+                 p3 = 3 * 1.57079632679489661923, p4 = 4 * 1.57079632679489661923;
+    const uint32_t b = lm_bits(x), ix = b & 0x7fffffffu;
+    const int neg = (int)(b >> 31);
+    if (ix <= 0x3f490fdau)
+        return ix < 0x39800000u ? x : lm_ksin(x);
+    if (ix <= 0x407b53d1u) {
+        if (ix <= 0x4016cbe3u)
+            return neg ? -lm_kcos(x + p1) : lm_kcos(x - p1);
+        return lm_ksin(neg ? -(x + p2) : -(x - p2));
+    }
+    if (ix <= 0x40e231d5u) {
+        if (ix <= 0x40afeddfu)
+            return neg ? lm_kcos(x + p3) : -lm_kcos(x - p3);
+        return lm_ksin(neg ? x + p4 : x - p4);
+    }
+    if (ix >= 0x7f800000u)
+        return x - x;
+    double y;
+    switch (lm_rem_pio2f(x, &y) & 3) {
+    case 0: return lm_ksin(y);
+    case 1: return lm_kcos(y);
+    case 2: return lm_ksin(-y);
+    default: return -lm_kcos(y);
+    }
+}
+
+float ok_cosf(float x)
+{
+    const double p1 = 1 * 1.57079632679489661923, p2 = 2 * 1.57079632679489661923,
+                 p3 = 3 * 1.57079632679489661923, p4 = 4 * 1.57079632679489661923;
+    const uint32_t b = lm_bits(x), ix = b & 0x7fffffffu;
+    const int neg = (int)(b >> 31);
+    if (ix <= 0x3f490fdau)
+        return ix < 0x39800000u ? 1.0f : lm_kcos(x);
+    if (ix <= 0x407b53d1u) {
+        if (ix > 0x4016cbe3u)
+            return -lm_kcos(neg ? x + p2 : x - p2);
+        return neg ? lm_ksin(x + p1) : lm_ksin(p1 - x);
+    }
+    if (ix <= 0x40e231d5u) {
+        if (ix > 0x40afeddfu)
+            return lm_kcos(neg ? x + p4 : x - p4);
+        return neg ? lm_ksin(-x - p3) : lm_ksin(x - p3);
+    }
+    if (ix >= 0x7f800000u)
+        return x - x;
+    double y;
+    switch ((unsigned)lm_rem_pio2f(x, &y) & 3) {
+    case 0: return lm_kcos(y);
+    case 1: return lm_ksin(-y);
+    case 2: return -lm_kcos(y);
+    default: return lm_ksin(y);
+    }
+}

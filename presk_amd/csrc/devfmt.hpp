@@ -16,7 +16,8 @@
 // Transcendentals: the kernel interpreter's (exec.rs:158-170), the `libm`
 // crate 0.2.16 = musl 1.1.22 = fdlibm's f32 method; same reductions,
 // coefficients and operation order as crates/presk-export-c/c/presk_libm.c
-// (expf :1605, logf :1811, expm1f :436, tanhf :1915, erff :2542).
+// (expf :1605, logf :1811, expm1f :436, tanhf :1915, erff :2542, sinf :2054,
+// cosf :2213).
 //
 // Each is checked over every f32 input on the GPU against the reference's
 // compiled C (tests/test_gpu_scalar.py, digests in tests/golden/digests.json).
@@ -301,4 +302,206 @@ PK_DEV float pk_erff(float x) {
     if (ax < 0x40c00000u) y = 1.0f - pk_erfc_tail(ax, x);
     else y = 1.0f - 0x1p-120f;
     return neg ? -y : y;
+}
+
+// ---- sinf / cosf: fdlibm's method in f64 (presk_libm.c:672-746 the
+// kernels, 1372-1447 the reduction, 749-1189 its large-argument form,
+// 2054-2111 sinf, 2213-2272 cosf) ---------------------------------------------
+PK_DEV float pk_ksin(double x) {
+    const double S1 = -0x15555554cbac77.0p-55, S2 = 0x111110896efbb2.0p-59, S3 = -0x1a00f9e2cae774.0p-65,
+                 S4 = 0x16cd878c3b46a7.0p-71;
+    const double z = x * x, w = z * z, r = S3 + z * S4, s = z * x;
+    return (float)((x + s * (S1 + z * S2)) + s * w * r);
+}
+PK_DEV float pk_kcos(double x) {
+    const double C0 = -0x1ffffffd0c5e81.0p-54, C1 = 0x155553e1053a42.0p-57, C2 = -0x16c087e80f1e27.0p-62,
+                 C3 = 0x199342e0ee5069.0p-68;
+    const double z = x * x, w = z * z, r = C2 + z * C3;
+    return (float)(((1.0 + z * C0) + w * C1) + (w * z) * r);
+}
+
+// |x| past 2^28 pi/2: Payne-Hanek with the 24-bit digits of 2/pi, one piece
+// of x (an integer of 24 bits times 2^e0), single precision (3 + 1 digits
+// of the product kept, more taken when the fraction cancels)
+__device__ __noinline__ int pk_rem_pio2_big(double x0, int e0, double* y) {
+    const int ipio2[] = {0xA2F983, 0x6E4E44, 0x1529FC, 0x2757D1, 0xF534DD, 0xC0DB62, 0x95993C, 0x439041,
+                         0xFE5163, 0xABDEBB, 0xC561B7, 0x246E3A, 0x424DD2, 0xE00649, 0x2EEA09, 0xD1921C,
+                         0xFE1DEB, 0x1CB129, 0xA73EE8, 0x8235F5, 0x2EBB44, 0x84E99C, 0x7026B4, 0x5F7E41,
+                         0x3991D6, 0x398353, 0x39F49C, 0x845F8B, 0xBDF928, 0x3B1FF8};
+    const double pio2_24[] = {1.57079625129699707031e+00, 7.54978941586159635335e-08, 5.39030252995776476554e-15,
+                              3.28200341580791294123e-22};
+    constexpr int JK = 3;
+    int iq[20];
+    double f[20], q[20], fq[20];
+    for (int i = 0; i < 20; ++i) fq[i] = 0.0;
+    int jv = (e0 - 3) / 24;
+    if (jv < 0) jv = 0;
+    int q0 = e0 - 24 * (jv + 1);
+    for (int i = 0; i <= JK; ++i) {
+        f[i] = (double)ipio2[jv + i];
+        q[i] = 0.0 + x0 * f[i];
+    }
+    int jz = JK, n, ih;
+    double z;
+    for (;;) {
+        z = q[jz];
+        for (int i = 0, j = jz; j > 0; ++i, --j) {
+            const double hi = (double)(int)(0x1p-24 * z);
+            iq[i] = (int)(z - 0x1p24 * hi);
+            z = q[j - 1] + hi;
+        }
+        z = __builtin_ldexp(z, q0);
+        z -= 8.0 * __builtin_floor(z * 0.125);
+        n = (int)z;
+        z -= (double)n;
+        ih = 0;
+        if (q0 > 0) {
+            const int top = iq[jz - 1] >> (24 - q0);
+            n += top;
+            iq[jz - 1] -= top << (24 - q0);
+            ih = iq[jz - 1] >> (23 - q0);
+        } else if (q0 == 0) {
+            ih = iq[jz - 1] >> 23;
+        } else if (z >= 0.5) {
+            ih = 2;
+        }
+        if (ih > 0) {
+            n += 1;
+            int carry = 0;
+            for (int i = 0; i < jz; ++i) {
+                const int d = iq[i];
+                if (carry == 0) {
+                    if (d != 0) {
+                        carry = 1;
+                        iq[i] = 0x1000000 - d;
+                    }
+                } else {
+                    iq[i] = 0xffffff - d;
+                }
+            }
+            if (q0 == 1) iq[jz - 1] &= 0x7fffff;
+            else if (q0 == 2) iq[jz - 1] &= 0x3fffff;
+            if (ih == 2) {
+                z = 1.0 - z;
+                if (carry != 0) z -= __builtin_ldexp(1.0, q0);
+            }
+        }
+        if (z == 0.0) {
+            int any = 0;
+            for (int i = jz - 1; i >= JK; --i) any |= iq[i];
+            if (any == 0) {
+                int k = 1;
+                while (iq[JK - k] == 0) ++k;
+                for (int i = jz + 1; i <= jz + k; ++i) {
+                    f[i] = (double)ipio2[jv + i];
+                    q[i] = 0.0 + x0 * f[i];
+                }
+                jz += k;
+                continue;
+            }
+        }
+        break;
+    }
+    if (z == 0.0) {
+        jz -= 1;
+        q0 -= 24;
+        while (iq[jz] == 0) {
+            --jz;
+            q0 -= 24;
+        }
+    } else {
+        z = __builtin_ldexp(z, -q0);
+        if (z >= 0x1p24) {
+            const double hi = (double)(int)(0x1p-24 * z);
+            iq[jz] = (int)(z - 0x1p24 * hi);
+            jz += 1;
+            q0 += 24;
+            iq[jz] = (int)hi;
+        } else {
+            iq[jz] = (int)z;
+        }
+    }
+    double fw = __builtin_ldexp(1.0, q0);
+    for (int i = jz; i >= 0; --i) {
+        q[i] = fw * (double)iq[i];
+        fw *= 0x1p-24;
+    }
+    for (int i = jz; i >= 0; --i) {
+        fw = 0.0;
+        for (int k = 0; k <= JK && k <= jz - i; ++k) fw += pio2_24[k] * q[i + k];
+        fq[jz - i] = fw;
+    }
+    fw = 0.0;
+    for (int i = jz; i >= 0; --i) fw += fq[i];
+    *y = ih == 0 ? fw : -fw;
+    return n;
+}
+
+// x mod pi/2 in *y, the quotient's low bits returned
+PK_DEV int pk_rem_pio2f(float x, double* y) {
+    const double toint = 1.5 / 0x1p-52, invpio2 = 6.36619772367581382433e-01, pio2_1 = 1.57079631090164184570e+00,
+                 pio2_1t = 1.58932547735281966916e-08;
+    const unsigned b = pk_bits(x), ix = b & 0x7fffffffu;
+    if (ix < 0x4dc90fdbu) {
+        const double fn = (double)x * invpio2 + toint - toint;
+        *y = x - fn * pio2_1 - fn * pio2_1t;
+        return (int)fn;
+    }
+    if (ix >= 0x7f800000u) {
+        *y = x - x;
+        return 0;
+    }
+    const int e0 = (int)(ix >> 23) - (0x7f + 23);
+    double r;
+    const int n = pk_rem_pio2_big((double)pk_float(ix - ((unsigned)e0 << 23)), e0, &r);
+    *y = (b >> 31) ? -r : r;
+    return (b >> 31) ? -n : n;
+}
+
+PK_DEV float pk_sinf(float x) {
+    const double p1 = 1 * 1.57079632679489661923, p2 = 2 * 1.57079632679489661923, p3 = 3 * 1.57079632679489661923,
+                 p4 = 4 * 1.57079632679489661923;
+    const unsigned b = pk_bits(x), ix = b & 0x7fffffffu;
+    const bool neg = (b >> 31) != 0;
+    if (ix <= 0x3f490fdau) return ix < 0x39800000u ? x : pk_ksin(x);
+    if (ix <= 0x407b53d1u) {
+        if (ix <= 0x4016cbe3u) return neg ? -pk_kcos(x + p1) : pk_kcos(x - p1);
+        return pk_ksin(neg ? -(x + p2) : -(x - p2));
+    }
+    if (ix <= 0x40e231d5u) {
+        if (ix <= 0x40afeddfu) return neg ? pk_kcos(x + p3) : -pk_kcos(x - p3);
+        return pk_ksin(neg ? x + p4 : x - p4);
+    }
+    if (ix >= 0x7f800000u) return x - x;
+    double y;
+    switch (pk_rem_pio2f(x, &y) & 3) {
+        case 0: return pk_ksin(y);
+        case 1: return pk_kcos(y);
+        case 2: return pk_ksin(-y);
+        default: return -pk_kcos(y);
+    }
+}
+
+PK_DEV float pk_cosf(float x) {
+    const double p1 = 1 * 1.57079632679489661923, p2 = 2 * 1.57079632679489661923, p3 = 3 * 1.57079632679489661923,
+                 p4 = 4 * 1.57079632679489661923;
+    const unsigned b = pk_bits(x), ix = b & 0x7fffffffu;
+    const bool neg = (b >> 31) != 0;
+    if (ix <= 0x3f490fdau) return ix < 0x39800000u ? 1.0f : pk_kcos(x);
+    if (ix <= 0x407b53d1u) {
+        if (ix > 0x4016cbe3u) return -pk_kcos(neg ? x + p2 : x - p2);
+        return neg ? pk_ksin(x + p1) : pk_ksin(p1 - x);
+    }
+    if (ix <= 0x40e231d5u) {
+        if (ix > 0x40afeddfu) return pk_kcos(neg ? x + p4 : x - p4);
+        return neg ? pk_ksin(-x - p3) : pk_ksin(x - p3);
+    }
+    if (ix >= 0x7f800000u) return x - x;
+    double y;
+    switch ((unsigned)pk_rem_pio2f(x, &y) & 3) {
+        case 0: return pk_kcos(y);
+        case 1: return pk_ksin(-y);
+        case 2: return -pk_kcos(y);
+        default: return pk_ksin(y);
+    }
 }

@@ -141,7 +141,8 @@ struct Printer {
                     case Un::Log: if (f) return "pk_logf(" + a + ")"; break;
                     case Un::Tanh: if (f) return "pk_tanhf(" + a + ")"; break;
                     case Un::Erf: if (f) return "pk_erff(" + a + ")"; break;
-                    case Un::Sin: case Un::Cos: break;
+                    case Un::Sin: if (f) return "pk_sinf(" + a + ")"; break;
+                    case Un::Cos: if (f) return "pk_cosf(" + a + ")"; break;
                 }
                 err = "the function " + show_expr(*e) + " is not on this executor yet";
                 return "0";

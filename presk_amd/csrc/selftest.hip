@@ -54,6 +54,8 @@ __device__ unsigned eval1(int fn, unsigned long long i) {
         case 1: return pk_bits(pk_logf(x));
         case 2: return pk_bits(pk_tanhf(x));
         case 3: return pk_bits(pk_erff(x));
+        case 4: return pk_bits(pk_sinf(x));
+        case 5: return pk_bits(pk_cosf(x));
         case 10: return pk_f32_to_bf16(x);
         case 11: return pk_f32_to_f16(x);
         case 12: return pk_f32_to_e8m15(x);
@@ -90,7 +92,7 @@ __global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long 
 }  // namespace
 
 hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
-    const int known[] = {0, 1, 2, 3, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
+    const int known[] = {0, 1, 2, 3, 4, 5, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
     bool ok = false;
     for (int f : known) ok |= f == fn;
     if (!ok || hi < lo) return hipErrorInvalidValue;

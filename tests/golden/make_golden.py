@@ -8,7 +8,9 @@ blocks of inputs (every f32 for the f32 functions and conversions, every code
 for the widenings, a fixed sample for the narrowings from f64), plus a few
 hundred sample input/output pairs per function for readable failures.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [NAME ...]
+
+With names, only those functions are (re)computed and merged into the file.
 """
 import ctypes
 import json
@@ -26,8 +28,16 @@ def main():
     lib.pd_digest.restype = ctypes.c_uint64
     lib.pd_digest.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64]
     lib.pd_eval.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32), ctypes.c_size_t]
-    out = {"about": "digests of the reference's presk_rt.h / presk_libm.c (crates/presk-export-c/c), see oracle/digest.c", "functions": {}}
+    path = os.path.join(HERE, "digests.json")
+    only = sys.argv[1:]
+    if only and os.path.exists(path):
+        with open(path) as f:
+            out = json.load(f)
+    else:
+        out = {"about": "digests of the reference's presk_rt.h / presk_libm.c (crates/presk-export-c/c), see oracle/digest.c", "functions": {}}
     for name, (fid, domain) in spec.FUNCTIONS.items():
+        if only and name not in only:
+            continue
         blocks = spec.blocks(domain)
         digs = [format(lib.pd_digest(fid, lo, hi), "016x") for lo, hi in blocks]
         ins = spec.sample_inputs(domain)
@@ -36,7 +46,7 @@ def main():
         assert lib.pd_eval(fid, arr_in, arr_out, len(ins)) == 0
         out["functions"][name] = {"id": fid, "domain": domain, "blocks": digs, "samples": [[i, o] for i, o in zip(ins, arr_out)]}
         print(name, digs[0], flush=True)
-    with open(os.path.join(HERE, "digests.json"), "w") as f:
+    with open(path, "w") as f:
         json.dump(out, f, indent=0)
 
 

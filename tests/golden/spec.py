@@ -7,6 +7,8 @@ FUNCTIONS = {
     "logf": (1, 1 << 32),
     "tanhf": (2, 1 << 32),
     "erff": (3, 1 << 32),
+    "sinf": (4, 1 << 32),
+    "cosf": (5, 1 << 32),
     "f32_to_bf16": (10, 1 << 32),
     "f32_to_f16": (11, 1 << 32),
     "f32_to_e8m15": (12, 1 << 32),

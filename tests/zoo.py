@@ -46,6 +46,8 @@ def _gpt_like(dt, B=2, T=8, D=16, H=2, V=11):
         "gelu": L.unary("gelu", [h4], dt),
         "gelu_deriv": L.unary("gelu_deriv", [h4], dt),
         "tanh": L.unary("tanh", [x], dt),
+        "sin": L.unary("sin", [x], dt),
+        "cos": L.unary("cos", [x], dt),
         "sub": L.elementwise_binary("sub", [x, O(A(("batch", B), ("seq", T)))], dt),
         "max": L.elementwise_binary("max", [x, b], dt),
         "layernorm_tail": L.fused([("sub", [("in", 0), ("in", 1)]), ("add", [("in", 2), ("in", 3)]), ("sqrt", [("step", 1)]),
