@@ -21,14 +21,28 @@ sys.path.insert(0, ROOT)
 METRIC = "tokens/sec course-GPT fwd+bwd; matmul TFLOP/s as % of MFMA peak"
 PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}   # MI355X dense MFMA
 HBM_GBS = 8000.0
+DATA = {"gpt-step": "synthetic (seeded ids and targets uniform over the vocabulary, N(0,0.02) weights)",
+        "gpt-forward": "synthetic (seeded ids and targets uniform over the vocabulary, N(0,0.02) weights)",
+        "llama": "synthetic (ids uniform over the vocabulary; N(0,0.02) weights drawn on the device, "
+                 "presk_hip_fill_normal)"}
 
 
 def workload(name: str, dtype: str, rows=None, realize=None):
     """(program, host inputs, tokens per step, contraction flops, config record)
     of a workload; `rows` shrinks it for the CPU sample; `realize` (`@FILE`)
-    gives the GPT's sites their storage types (a mixed realization)."""
-    from presk_amd import configs, gpt
+    gives the GPT's sites their storage types (a mixed realization).  The
+    Llama forward's inputs are made on the device (`host` None)."""
+    from presk_amd import configs, gpt, llama
     from presk_amd.realize import Realization
+
+    if name == "llama":
+        s = llama.LLAMA_7B
+        p, _, _ = llama.build(s, dtype)
+        cfg = {"workload": "config 5: Llama-7B-shaped decoder forward (logits of a full context, as presk serve "
+                           "recomputes them)", "L": s.L, "d_model": s.D, "heads": s.H, "kv_heads": s.G, "ffn": s.FF,
+               "vocab": s.V, "batch": s.B, "seq": s.T, "rope_base": s.base, "rmsnorm_eps": s.eps, "storage": dtype,
+               "compute": "f32", "params": llama.param_count(s), "launches": len(p.launches)}
+        return p, None, s.B * s.T, llama.contraction_flops(s), cfg
 
     if name == "mlp":
         r = rows or 8192
@@ -114,7 +128,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="gpt-step", choices=["gpt-step", "gpt-forward", "mlp", "linear"])
+    ap.add_argument("--workload", default="gpt-step", choices=["gpt-step", "gpt-forward", "mlp", "linear", "llama"])
     ap.add_argument("--dtype", default=None)
     ap.add_argument("--realize", default=None, metavar="@FILE",
                     help="a realization file (the reference's schema) for the GPT workloads: storage type per site")
@@ -136,10 +150,14 @@ def main():
     if args.copy_probe:
         copy_probe()
         return
-    dtype = args.dtype or ("bf16" if args.workload == "mlp" else "f32")
+    dtype = args.dtype or ("bf16" if args.workload in ("mlp", "llama") else "f32")
     p, host, tokens, flops, cfg = workload(args.workload, dtype, realize=args.realize)
     p.compile()
-    configs.load_inputs(p, host)
+    if host is None:
+        from presk_amd import llama
+        llama.load_device_inputs(p, llama.LLAMA_7B)
+    else:
+        configs.load_inputs(p, host)
     p.prepare()
     if not args.eager:
         # the step's 587 launches recorded once and replayed as one HIP graph
@@ -195,11 +213,12 @@ def main():
     # the step's time: flops / peak for one type, weighted for a mixed one
     bound_ms = sum(l.compiled.flops / (PEAK_TFLOPS.get(l.low.dtype, PEAK_TFLOPS["f32"]) * 1e12) * 1e3
                    for l in p.launches if l.compiled.kind == "gemm")
-    metric = {"gpt-step": METRIC, "gpt-forward": "tokens/sec course-GPT forward and loss (config 3)"}.get(
+    metric = {"gpt-step": METRIC, "gpt-forward": "tokens/sec course-GPT forward and loss (config 3)",
+              "llama": "tokens/sec Llama-7B-shaped forward (config 5); matmul TFLOP/s as % of MFMA peak"}.get(
         args.workload, f"rows/sec {args.workload} (a supplementary workload)")
     rec = {"metric": metric, "value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,1) inputs, xavier weights)",
+           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": DATA.get(args.workload, "synthetic (seeded N(0,1) inputs, xavier weights)"),
            "config": cfg, "matmul_tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
            "matmul_frac_of_peak": round(bound_ms / ms_step, 4), "roofline": roof,
            "kernels": per_kernel}

@@ -158,6 +158,16 @@ int presk_hip_batch_graph(presk_hip_batch *b);
 int presk_hip_batch_run(presk_hip_batch *b, void *stream);
 void presk_hip_batch_release(presk_hip_batch *b);
 
+/* Seeded synthetic values written in place: n elements mean + std * z of
+ * type "f32", "bf16" or "f16", z ~ N(0, 1) a function of (seed, element
+ * index) alone (a splitmix64 hash and Box-Muller in f32).  Stands in for the
+ * host's parameter initialization (`Normal` and `ones` are host primitives,
+ * crates/presk-kernel/src/host.rs:1476; their draws come from ChaCha20 keys,
+ * crates/presk-interp/src/run.rs:56-100) where a model's parameters are too
+ * large to draw on the host and copy: the values are seeded N(0, std) but not
+ * the reference's draws.  std = 0 fills the constant `mean`. */
+int presk_hip_fill_normal(void *dst, const char *type, int64_t n, uint64_t seed, double mean, double std, void *stream);
+
 /* Self-test of the device's scalar functions over a domain block: the digest
  * (sum of splitmix64 finalizers of (i << 32 | out_i)) of function `fn` over
  * inputs [lo, hi), as tests/golden/digests.json holds the reference's.  No

@@ -6,8 +6,10 @@
 // nest computes the same values (lower.rs:846-905).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <functional>
+#include <map>
 #include <mutex>
 
 #include "devfmt.hpp"
@@ -114,6 +116,7 @@ struct GemmPlan : ClassPlan {
     int64_t split_bound = -1;  // the KernelFn split loop's bound
     bool split_on_batch = false;
     bool swapped = false;          // operand 1 is A (an `ein` whose operand 1 carries I)
+    bool whole_only = false;       // no partial range of the split loop (an `ein` whose first axis is J)
     long long rows_per_iter = 0;   // M rows (or batch entries) one outer iteration covers
     mutable float* work = nullptr;
     mutable size_t work_floats = 0;
@@ -136,6 +139,7 @@ struct GemmPlan : ClassPlan {
         if (split_bound >= 0 && !(lo == 0 && hi == split_bound)) {
             if (lo < 0 || hi > split_bound || lo > hi) return hipErrorInvalidValue;
             if (lo == hi) return hipSuccess;
+            if (whole_only) return hipErrorInvalidValue;
             if (split_on_batch) {
                 a.A = (const char*)a.A + lo * a.sa_b[0] * esz;
                 a.B = (const char*)a.B + lo * a.sb_b[0] * esz;
@@ -145,7 +149,7 @@ struct GemmPlan : ClassPlan {
             } else {
                 const long long m0 = lo * rows_per_iter;
                 a.A = (const char*)a.A + m0 * a.sa_m * esz;
-                a.C = (char*)a.C + m0 * a.N * esz;
+                a.C = (char*)a.C + m0 * a.sc_m * esz;
                 a.M = (hi - lo) * rows_per_iter;
                 a.tiles_m = (int)((a.M + gemm_tile_m() - 1) / gemm_tile_m());
                 if (a.bias && a.bias_kind == 2) a.bias = (const char*)a.bias + m0 * a.N * esz;
@@ -272,7 +276,7 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
         g.N = w.dims[1];
         g.M = x.numel() / g.K;
         if (o.numel() != g.M * g.N || o.dims.back() != g.N) return nullptr;
-        g.sa_m = g.K; g.sa_k = 1; g.sb_k = g.N; g.sb_n = 1;
+        g.sa_m = g.K; g.sa_k = 1; g.sb_k = g.N; g.sb_n = 1; g.sc_m = g.N;
         p->rows_per_iter = x.dims.size() >= 1 ? g.M / x.dims[0] : 0;
     } else if (is_l) {
         // ct[outer..., I, N] . b[J, N]^T -> [outer..., I, J]   (lower.rs:715-726)
@@ -281,7 +285,7 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
         g.N = w.dims[0];
         g.M = x.numel() / g.K;
         if (o.numel() != g.M * g.N) return nullptr;
-        g.sa_m = g.K; g.sa_k = 1; g.sb_k = 1; g.sb_n = g.K;
+        g.sa_m = g.K; g.sa_k = 1; g.sb_k = 1; g.sb_n = g.K; g.sc_m = g.N;
         p->rows_per_iter = g.M / x.dims[0];
     } else if (is_r) {
         // a[lead..., I], ct[lead..., J] -> [I, J], summed over lead   (lower.rs:730-739)
@@ -292,84 +296,142 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
         g.N = w.dims.back();
         g.K = prod(x.dims, 0, x.dims.size() - 1);
         if (o.dims.size() != 2 || o.dims[0] != g.M || o.dims[1] != g.N) return nullptr;
-        g.sa_m = 1; g.sa_k = g.M; g.sb_k = g.N; g.sb_n = 1;
+        g.sa_m = 1; g.sa_k = g.M; g.sb_k = g.N; g.sb_n = 1; g.sc_m = g.N;
         p->rows_per_iter = 1;
     } else {
-        // ein: the roles of the operands' axes from the product's index pattern
+        // ein: the roles of the operands' axes from the product's index
+        // pattern.  An output axis both operands carry, or one carries and
+        // the other broadcasts over (stride 0), is a batch axis; J is the
+        // output's last axis (unit stride), carried by one operand only (B);
+        // I is the longest output axis A alone carries; the summed axes, in
+        // loop order, must read as one K of uniform stride in both operands
+        // (`ein[batch, seq, model](o * w)` over groups, per, hd).
         std::vector<int> v0, v1, vo;
         if (!product_pattern(k, &v0, &v1, &vo)) return nullptr;
-        if (vo.size() < 2 || v0.size() != x.dims.size() || v1.size() != w.dims.size() || vo.size() != o.dims.size()) return nullptr;
-        for (int v : vo)
-            if (v < 0) return nullptr;
-        const int vi = vo[vo.size() - 2], vj = vo.back();
-        const size_t nouter = vo.size() - 2;
-        int vk = -1;
-        for (int v : v0) {
-            bool in_out = false;
-            for (int u : vo) in_out |= u == v;
-            if (!in_out) {
-                if (vk >= 0 && vk != v) return nullptr;   // one summed axis
-                vk = v;
-            }
-        }
-        if (vk < 0) return nullptr;
-        auto pos = [](const std::vector<int>& v, int var) {
-            int p = -1, c = 0;
-            for (size_t i = 0; i < v.size(); ++i)
-                if (v[i] == var) { p = (int)i; ++c; }
-            return c == 1 ? p : -1;
+        if (vo.empty() || v0.size() != x.dims.size() || v1.size() != w.dims.size() || vo.size() != o.dims.size())
+            return nullptr;
+        auto count = [](const std::vector<int>& v, int var) {
+            int c = 0;
+            for (int u : v) c += u == var;
+            return c;
         };
-        // operand roles: A carries I, B carries J; the generic `ein` form may
-        // have them the other way round (the product commutes exactly)
+        auto pos = [](const std::vector<int>& v, int var) {
+            for (size_t i = 0; i < v.size(); ++i)
+                if (v[i] == var) return (int)i;
+            return -1;
+        };
+        for (const auto* vs : {&v0, &v1, &vo})
+            for (int v : *vs)
+                if (v < 0 || count(*vs, v) != 1) return nullptr;
+        // summed axes: in both operands, not in the output
+        std::vector<int> summed;
+        for (int v : v0)
+            if (pos(vo, v) < 0) {
+                if (pos(v1, v) < 0) return nullptr;
+                summed.push_back(v);
+            }
+        for (int v : v1)
+            if (pos(vo, v) < 0 && pos(v0, v) < 0) return nullptr;
+        if (summed.empty()) return nullptr;
+        // the loops' nesting depth: the summed axes outermost first
+        std::map<int, int> depth;
+        std::function<void(const std::vector<const Stmt*>&, int)> walk = [&](const std::vector<const Stmt*>& body, int d) {
+            for (auto st : body)
+                if (st->kind == Stmt::For) {
+                    depth.emplace(st->var, d);
+                    walk(st->body, d + 1);
+                }
+        };
+        walk(k.body, 0);
+        for (int v : summed)
+            if (!depth.count(v)) return nullptr;
+        std::sort(summed.begin(), summed.end(), [&](int a, int b) { return depth[a] < depth[b]; });
+        // operand roles: B carries J, the output's last axis
+        const int vj = vo.back();
         const BufSpec* xa = &x;
         const BufSpec* wb = &w;
         std::vector<int> va = v0, vb = v1;
         bool swapped = false;
-        if (pos(v0, vi) < 0 && pos(v1, vi) >= 0 && pos(v0, vj) >= 0) {
+        if (pos(v0, vj) >= 0 && pos(v1, vj) < 0) {
             std::swap(va, vb);
             std::swap(xa, wb);
             swapped = true;
         }
+        if (pos(vb, vj) < 0 || pos(va, vj) >= 0) return nullptr;
         p->swapped = swapped;
-        const auto s0 = xa->strides(), s1 = wb->strides(), so = o.strides();
-        const int a_i = pos(va, vi), a_k = pos(va, vk), b_j = pos(vb, vj), b_k = pos(vb, vk);
-        if (a_i < 0 || a_k < 0 || b_j < 0 || b_k < 0 || pos(va, vj) >= 0 || pos(vb, vi) >= 0) return nullptr;
-        if (va.size() != nouter + 2 || vb.size() != nouter + 2) return nullptr;
-        g.M = xa->dims[a_i];
-        g.K = xa->dims[a_k];
-        g.N = wb->dims[b_j];
-        if (wb->dims[b_k] != g.K || o.dims[nouter] != g.M || o.dims[nouter + 1] != g.N) return nullptr;
-        g.sa_m = s0[a_i]; g.sa_k = s0[a_k]; g.sb_k = s1[b_k]; g.sb_n = s1[b_j];
-        // outer axes, collapsed where all three operands allow it
-        std::vector<long long> bd, sa, sb, sc;
-        for (size_t q = 0; q < nouter; ++q) {
-            const int pa = pos(va, vo[q]), pb = pos(vb, vo[q]);
-            if (pa < 0 || pb < 0 || xa->dims[pa] != o.dims[q] || wb->dims[pb] != o.dims[q]) return nullptr;
-            if (bd.size() > 1 && sa.back() == s0[pa] * o.dims[q] && sb.back() == s1[pb] * o.dims[q] && sc.back() == so[q] * o.dims[q]) {
-                bd.back() *= o.dims[q];
-                sa.back() = s0[pa];
-                sb.back() = s1[pb];
-                sc.back() = so[q];
+        const auto sa = xa->strides(), sb = wb->strides(), so = o.strides();
+        if (so.back() != 1) return nullptr;
+        auto len_of = [&](int v) {
+            const int q = pos(vo, v);
+            if (q >= 0) return (long long)o.dims[q];
+            return (long long)xa->dims[pos(va, v)];
+        };
+        // K: the summed axes as one, each outer one's stride the next one's
+        // times its length, in both operands
+        for (int v : summed)
+            if (xa->dims[pos(va, v)] != wb->dims[pos(vb, v)]) return nullptr;
+        for (size_t i = 0; i + 1 < summed.size(); ++i) {
+            const int u = summed[i], v = summed[i + 1];
+            if (sa[pos(va, u)] != sa[pos(va, v)] * len_of(v) || sb[pos(vb, u)] != sb[pos(vb, v)] * len_of(v)) return nullptr;
+        }
+        g.K = 1;
+        for (int v : summed) g.K *= len_of(v);
+        g.sa_k = sa[pos(va, summed.back())];
+        g.sb_k = sb[pos(vb, summed.back())];
+        // I: the longest output axis of A alone (the later one on a tie)
+        int vi = -1;
+        for (int v : vo)
+            if (pos(va, v) >= 0 && pos(vb, v) < 0 && (vi < 0 || len_of(v) >= len_of(vi))) vi = v;
+        if (vi < 0) return nullptr;
+        g.M = len_of(vi);
+        g.N = len_of(vj);
+        g.sa_m = sa[pos(va, vi)];
+        g.sb_n = sb[pos(vb, vj)];
+        g.sc_m = so[pos(vo, vi)];
+        // batch axes in output order; length-1 axes dropped except the
+        // first output axis (the KernelFn split loop), which is never merged
+        // into; the others collapsed where all three strides allow it
+        std::vector<long long> bd, ba, bb, bc;
+        bool first_is_batch = false;
+        for (size_t q = 0; q < vo.size(); ++q) {
+            const int v = vo[q];
+            if (v == vi || v == vj) continue;
+            const long long n = o.dims[q];
+            const int pa = pos(va, v), pb = pos(vb, v);
+            if ((pa >= 0 && xa->dims[pa] != n) || (pb >= 0 && wb->dims[pb] != n)) return nullptr;
+            const long long s_a = pa >= 0 ? sa[pa] : 0, s_b = pb >= 0 ? sb[pb] : 0, s_c = so[q];
+            if (q == 0) first_is_batch = true;
+            else if (n == 1) continue;
+            const bool mergeable = !bd.empty() && !(first_is_batch && bd.size() == 1);
+            if (mergeable && ba.back() == s_a * n && bb.back() == s_b * n && bc.back() == s_c * n) {
+                bd.back() *= n;
+                ba.back() = s_a;
+                bb.back() = s_b;
+                bc.back() = s_c;
             } else {
-                bd.push_back(o.dims[q]);
-                sa.push_back(s0[pa]);
-                sb.push_back(s1[pb]);
-                sc.push_back(so[q]);
+                bd.push_back(n);
+                ba.push_back(s_a);
+                bb.push_back(s_b);
+                bc.push_back(s_c);
             }
         }
         if (bd.size() > 3) return nullptr;
         g.nbatch = (int)bd.size();
         for (size_t q = 0; q < bd.size(); ++q) {
             g.bdim[q] = bd[q];
-            g.sa_b[q] = sa[q];
-            g.sb_b[q] = sb[q];
-            g.sc_b[q] = sc[q];
+            g.sa_b[q] = ba[q];
+            g.sb_b[q] = bb[q];
+            g.sc_b[q] = bc[q];
             g.batch *= bd[q];
         }
-        p->split_on_batch = nouter > 0;
-        p->rows_per_iter = nouter > 0 ? 0 : 1;
+        // a partial range of the split loop (the first output axis): a batch
+        // range, a row range, or (J first) not offered
+        p->split_on_batch = first_is_batch;
+        p->rows_per_iter = vo[0] == vi ? 1 : 0;
+        p->whole_only = !first_is_batch && vo[0] != vi;
     }
     if (epi) {
+        if (g.sc_m != g.N) return nullptr;
         std::vector<int> m;
         const BufSpec& b = k.inputs[2];
         if (!align(b, o, &m)) return nullptr;
@@ -394,7 +456,7 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     if (g.batch > 65535 || g.splits > 65535) return nullptr;
     // 32-bit element offsets inside one batch entry
     const double lim = 2147483647.0;
-    if ((double)g.M * g.N > lim || (double)g.M * g.K > lim || (double)g.K * g.N > lim ||
+    if ((double)g.M * g.N > lim || (double)g.M * g.sc_m > lim || (double)g.M * g.K > lim || (double)g.K * g.N > lim ||
         (double)x.numel() > lim || (double)w.numel() > lim) return nullptr;
     return p;
 }

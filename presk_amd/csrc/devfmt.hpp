@@ -323,7 +323,7 @@ PK_DEV float pk_kcos(double x) {
 // |x| past 2^28 pi/2: Payne-Hanek with the 24-bit digits of 2/pi, one piece
 // of x (an integer of 24 bits times 2^e0), single precision (3 + 1 digits
 // of the product kept, more taken when the fraction cancels)
-__device__ __noinline__ int pk_rem_pio2_big(double x0, int e0, double* y) {
+static __device__ __noinline__ int pk_rem_pio2_big(double x0, int e0, double* y) {
     const int ipio2[] = {0xA2F983, 0x6E4E44, 0x1529FC, 0x2757D1, 0xF534DD, 0xC0DB62, 0x95993C, 0x439041,
                          0xFE5163, 0xABDEBB, 0xC561B7, 0x246E3A, 0x424DD2, 0xE00649, 0x2EEA09, 0xD1921C,
                          0xFE1DEB, 0x1CB129, 0xA73EE8, 0x8235F5, 0x2EBB44, 0x84E99C, 0x7026B4, 0x5F7E41,

@@ -377,7 +377,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     S* C = (S*)g.C + cbase;
     const int nl = (threadIdx.x % TPR) * OV;
     const int n = (int)n0 + nl;
-    const bool cvec = N % OV == 0 && (uintptr_t)C % 16 == 0;
+    const bool cvec = N % OV == 0 && g.sc_m % OV == 0 && (uintptr_t)C % 16 == 0;
     const bool wvec = N % 4 == 0;
     // a per-column bias is the same for every row this thread stores
     float bcol[OV];
@@ -415,7 +415,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
             if (g.bias && g.bias_kind == 2 && n + e < N) b = load_bias<ST>(g.bias, (long long)m * N + n + e);
             out[e] = round_out<ST>(v[e], g.bias != nullptr, b, ovf);
         }
-        S* c = C + (long long)m * N + n;
+        S* c = C + (long long)m * g.sc_m + n;
         if (full && cvec) {
             typename St<ST>::V w;
             __builtin_memcpy(&w, out, 16);
@@ -450,8 +450,7 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     if (g.bias_kind == 1) b = load_bias<ST>(g.bias, n);
     else if (g.bias_kind == 2) b = load_bias<ST>(g.bias, idx);
     else if (g.bias_kind == 3) b = load_bias<ST>(g.bias, 0);
-    (void)m;
-    store_out<ST>(g.C, idx, s, g.bias != nullptr, b, ovf);
+    store_out<ST>(g.C, m * g.sc_m + n, s, g.bias != nullptr, b, ovf);
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
 

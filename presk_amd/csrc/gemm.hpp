@@ -11,11 +11,12 @@ struct GemmArgs {
     const void* A;        // operand 0, element (b, m, k) at A + batch + m*sa_m + k*sa_k
     const void* B;        // operand 1, element (b, k, n) at B + batch + k*sb_k + n*sb_n
     const void* bias;     // the epilogue's operand or null
-    void* C;              // output, row-major [batch][M][N]
+    void* C;              // output, element (b, m, n) at C + batch + m*sc_m + n
     float* work;          // split-K partials [splits][M][N] (splits > 1)
     unsigned* flag;       // overflow guard (f16 output) or null
     long long M, N, K;
     long long sa_m, sa_k, sb_k, sb_n;
+    long long sc_m;                 // output row stride: N, or wider when an `ein` puts batch axes inside a row
     int nbatch;                     // batch axes (outer axes of an `ein`), at most 3
     long long bdim[3], sa_b[3], sb_b[3], sc_b[3];
     long long batch;                // product of bdim

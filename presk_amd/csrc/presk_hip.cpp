@@ -18,6 +18,7 @@
 #include <unordered_map>
 
 #include "convert.hpp"
+#include "synth.hpp"
 #include "executor.hpp"
 
 namespace presk {
@@ -501,6 +502,15 @@ int presk_hip_batch_run(presk_hip_batch* b, void* stream) {
 }
 
 void presk_hip_batch_release(presk_hip_batch* b) { delete b; }
+
+int presk_hip_fill_normal(void* dst, const char* type, int64_t n, uint64_t seed, double mean, double std, void* stream) {
+    const int t = convert_type(type);
+    if (t != 1 && t != 2 && t != 4)
+        return fail(PRESK_HIP_ERR, "E10001: a fill of type `" + std::string(type ? type : "") + "` (f32, bf16 or f16)");
+    if (n < 0 || (n > 0 && !dst)) return fail(PRESK_HIP_ERR, "E10001: bad fill arguments");
+    hipError_t e = synth_normal_launch(dst, t, n, seed, (float)mean, (float)std, (hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "fill");
+}
 
 int presk_hip_scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
     hipError_t e = scalar_digest(fn, lo, hi, digest);

@@ -67,6 +67,9 @@ class Builder:
         self.p, self.dt, self.realize = prog, dtype, realize
         self.axes: dict = {}
         self.kind: dict = {}
+        # a view's buffer (`split`/`merge` read one buffer under other axes,
+        # crates/presk-kernel/src/host.rs:1510-1536: no launch)
+        self.base: dict = {}
         self.n = 0
         self.fn = "MiniGPT.apply"
 
@@ -99,8 +102,39 @@ class Builder:
             return self.dt
         return self.realize.dtype_at(f"{self.fn}/{re.sub(r'^b[0-9]+[.]', '', name)}")
 
+    def view(self, src, axes, name=None):
+        """`src` under other axes of the same element count, no launch."""
+        name = self._name(name)
+        n0 = 1
+        for a in self.axes[src]:
+            n0 *= a.len
+        n1 = 1
+        for a in axes:
+            n1 *= a.len
+        if n0 != n1:
+            raise ValueError(f"view {name}: {n1} elements of {src}'s {n0}")
+        self.axes[name], self.kind[name] = list(axes), self.kind[src]
+        self.base[name] = self.base.get(src, src)
+        return name
+
+    def split(self, src, axis, n1, l1, n2, l2, name=None):
+        """`split(axis a, n1: l1, n2: l2, x)` (host.rs:1523-1536)."""
+        ax = self.axes[src]
+        p = next(i for i, a in enumerate(ax) if a.name == axis)
+        if l1 * l2 != ax[p].len:
+            raise ValueError(f"split: `{axis}` has length {ax[p].len}")
+        return self.view(src, ax[:p] + [L.Axis(n1, l1), L.Axis(n2, l2)] + ax[p + 1:], name)
+
+    def merge(self, src, a, b_, name=None):
+        """`merge(axis a, axis b, x)` (host.rs:1510-1522): the joined axis is unnamed."""
+        ax = self.axes[src]
+        p = next(i for i, x in enumerate(ax) if x.name == a)
+        if p + 1 >= len(ax) or ax[p + 1].name != b_:
+            raise ValueError(f"merge: `{a}` is not immediately followed by `{b_}`")
+        return self.view(src, ax[:p] + [L.Axis(None, ax[p].len * ax[p + 1].len)] + ax[p + 2:], name)
+
     def _out(self, low, ins, name):
-        self.p.add(low, ins, name)
+        self.p.add(low, [self.base.get(i, i) for i in ins], name)
         self.axes[name], self.kind[name] = list(low.out_axes), low.out_kind
         return name
 
@@ -184,11 +218,17 @@ class Builder:
     def cross_entropy_vjp(self, logits, y, ct, name=None):
         return self._prim(lambda dt: L.cross_entropy_vjp([self.op(logits), self.op(y), self.op(ct)], dt), [logits, y, ct], name)
 
+    def slice(self, x, axis, lo, hi, name=None):
+        return self._prim(lambda dt: L.slice_(axis, lo, hi, [self.op(x)], dt), [x], name)
+
+    def concat(self, x, y, axis, name=None):
+        return self._prim(lambda dt: L.concat(axis, [self.op(x), self.op(y)], dt), [x, y], name)
+
     def causal_mask(self, T, name):
         return self._prim(lambda dt: L.causal_mask("seq", T, dt), [], name)
 
-    def positions(self, T, name):
-        return self._prim(lambda dt: L.positions("seq", T, dt), [], name)
+    def positions(self, T, name, axis="seq"):
+        return self._prim(lambda dt: L.positions(axis, T, dt), [], name)
 
 
 def param_shapes(s: GptShape) -> dict:

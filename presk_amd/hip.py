@@ -25,7 +25,8 @@ SYMBOLS = ["presk_hip_init", "presk_hip_last_error", "presk_hip_compile", "presk
            "presk_hip_release", "presk_hip_kernel_text", "presk_hip_alloc", "presk_hip_free", "presk_hip_h2d", "presk_hip_d2h", "presk_hip_memset",
            "presk_hip_sync", "presk_hip_stream_create", "presk_hip_stream_destroy", "presk_hip_time",
            "presk_hip_scalar_digest", "presk_hip_batch_create", "presk_hip_batch_add", "presk_hip_batch_graph",
-           "presk_hip_batch_run", "presk_hip_batch_release", "presk_hip_convert", "presk_hip_batch_add_convert"]
+           "presk_hip_batch_run", "presk_hip_batch_release", "presk_hip_convert", "presk_hip_batch_add_convert",
+           "presk_hip_fill_normal"]
 
 
 class HipError(RuntimeError):
@@ -81,6 +82,7 @@ def lib():
         L.presk_hip_batch_release.argtypes = [vp]
         L.presk_hip_batch_release.restype = None
         L.presk_hip_convert.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_char_p, i64, vp, vp]
+        L.presk_hip_fill_normal.argtypes = [vp, ctypes.c_char_p, i64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]
         L.presk_hip_batch_add_convert.argtypes = [vp, vp, ctypes.c_char_p, vp, ctypes.c_char_p, i64, vp]
         _lib = L
     return _lib

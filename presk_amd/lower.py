@@ -878,6 +878,45 @@ def merge_heads(h, hd, ins, dtype) -> Lowered:
     return kernel(f"merge_heads {h}x{hd}", dtype, ins, out, "real", bd, body)
 
 
+def slice_(axis, lo, hi, ins, dtype) -> Lowered:
+    """lower.rs:1554-1572: the elements lo..hi of one axis, which keeps its
+    name at length hi - lo."""
+    t = ins[0]
+    p = _axis_pos(t.axes, axis)
+    if lo > hi or hi > t.axes[p].len:
+        raise ValueError(f"slice {lo}..{hi} outside the axis `{axis}`, of length {t.axes[p].len}")
+    out = list(t.axes)
+    out[p] = Axis(out[p].name, hi - lo)
+    bd = B()
+    ov = bd.loops(dims(out))
+    src = ivs(ov)
+    src[p] = bin_("+", iv(ov[p]), str(lo))
+    if t.kind != "real":
+        raise ValueError("slice: an index operand (the reference's StoreI form) is not restated")
+    body = [Store(1, ivs(ov), load(0, src))]
+    return kernel(f"slice {axis}: {lo}..{hi}", dtype, ins, out, "real", bd, nest(ov, dims(out), body))
+
+
+def concat(axis, ins, dtype) -> Lowered:
+    """lower.rs:1592-1612: `x` into the first part of the axis, `y` into
+    the rest, each element written once."""
+    x, y = ins
+    p, q = _axis_pos(x.axes, axis), _axis_pos(y.axes, axis)
+    if not (p == q and len(x.axes) == len(y.axes) and all(k == p or u.len == v.len for k, (u, v) in enumerate(zip(x.axes, y.axes)))):
+        raise ValueError(f"concat {axis}: shapes differ off the axis")
+    m = x.axes[p].len
+    out = list(x.axes)
+    out[p] = Axis(out[p].name, m + y.axes[p].len)
+    bd = B()
+    xv = bd.loops(dims(x.axes))
+    body = nest(xv, dims(x.axes), [Store(2, ivs(xv), load(0, ivs(xv)))])
+    yv = bd.loops(dims(y.axes))
+    dst = ivs(yv)
+    dst[p] = bin_("+", iv(yv[p]), str(m))
+    body += nest(yv, dims(y.axes), [Store(2, dst, load(1, ivs(yv)))])
+    return kernel(f"concat {axis}", dtype, ins, out, "real", bd, body)
+
+
 def causal_mask(axis, n, dtype) -> Lowered:
     """lower.rs:1717-1726."""
     out = [Axis(axis, n), Axis(f"{axis}2", n)]

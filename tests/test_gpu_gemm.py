@@ -43,6 +43,26 @@ def cases():
         xb = O(A(("batch", 8), ("seq", 2048), 200))
         out.append((f"dot+add-bn96-{dt}", L.dot([xb, O(A(200, 384)), O(A(384))], dt, epilogue=(True, A(("batch", 8), ("seq", 2048), 384))), None))
         out.append((f"dot_vjp_l-bn96-{dt}", L.dot_vjp_l([xb, O(A(384, 200))], dt), None))
+        # the Llama attention's `ein`s (grouped-query: 2 groups of 3 heads):
+        # projections that broadcast an operand over batch axes, scores and
+        # values whose rows are not the output's second-last axis, and an
+        # output projection summed over three axes read as one K
+        xq = O(A(("batch", 2), ("seq", 100), ("model", 64)))
+        wq3 = O(A(("model", 64), ("groups", 2), ("per", 3), ("hd", 32)))
+        out.append((f"ein_qproj-{dt}", L.ein([xq, wq3], [["batch", "seq", "model"], ["model", "groups", "per", "hd"]],
+                                             ["batch", "groups", "per", "seq", "hd"], dt), None))
+        qg = O(A(("batch", 2), ("groups", 2), ("per", 3), ("seq", 100), ("hd", 32)))
+        kg = O(A(("batch", 2), ("groups", 2), ("seq", 100), 32))
+        out.append((f"ein_gqa_scores-{dt}", L.ein([qg, kg], [["batch", "groups", "per", "seq", "hd"], ["batch", "groups", "seq2", "hd"]],
+                                                  ["batch", "groups", "per", "seq", "seq2"], dt), None))
+        ag = O(A(("batch", 2), ("groups", 2), ("per", 3), ("seq", 100), ("seq2", 100)))
+        vg = O(A(("batch", 2), ("seq", 100), ("groups", 2), ("hd", 32)))
+        out.append((f"ein_gqa_values-{dt}", L.ein([ag, vg], [["batch", "groups", "per", "seq", "seq2"], ["batch", "seq2", "groups", "hd"]],
+                                                  ["batch", "seq", "groups", "per", "hd"], dt), None))
+        og = O(A(("batch", 2), ("seq", 100), ("groups", 2), ("per", 3), ("hd", 32)))
+        w2 = O(A(("groups", 2), ("per", 3), ("hd", 32), ("model", 72)))
+        out.append((f"ein_oproj-{dt}", L.ein([og, w2], [["batch", "seq", "groups", "per", "hd"], ["groups", "per", "hd", "model"]],
+                                             ["batch", "seq", "model"], dt), None))
     # a K that is not a multiple of the k-block, M and N below one tile
     out.append(("dot-odd-bf16", L.dot([O(A(("batch", 5), 77)), O(A(77, 24))], "bf16"), None))
     return out
