@@ -531,10 +531,20 @@ struct RowPlan : ClassPlan {
     RowArgs a{};
     int n_in = 1;
     bool guarded = false;
+    mutable unsigned* mbits = nullptr;   // the mask as bits (long masked rows)
     const char* kind() const override { return "rows"; }
     std::string order() const override { return "sequential"; }
+    hipError_t prepare() const override {
+        if (mbits || !rows_need_mask_bits(a)) return hipSuccess;
+        return hipMalloc(&mbits, (size_t)a.mask_rows * rows_mask_words(a.n) * sizeof(unsigned));
+    }
+    ~RowPlan() override {
+        if (mbits) hipFree(mbits);
+    }
     hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
+        if (hipError_t e = prepare(); e != hipSuccess) return e;
         RowArgs x = a;
+        x.mbits = mbits;
         x.x = bufs[0];
         if (a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2) x.mask = bufs[1];
         if (a.op == kCrossEntropy || a.op == kCrossEntropyVjp) x.y = bufs[1];

@@ -111,36 +111,60 @@ PK_DEV float pk_ldexpf(float y, int n) {
     return y * pk_float((unsigned)(0x7f + n) << 23);
 }
 
+// fdlibm's expf, its branches written as selects (the same operations on
+// every path, so the same bits): k = 0 is the general reduction with k = 0
+// (x - 0 * ln2_hi is x, 0 * ln2_lo is 0), scalbnf's one pre-scaling step is
+// a select of the factor, and the special inputs are chosen last.
 PK_DEV float pk_expf(float x) {
     const float ln2_hi = 6.9314575195e-1f, ln2_lo = 1.4286067653e-6f, inv_ln2 = 1.4426950216e+0f;
     const float p1 = 1.6666625440e-1f, p2 = -2.7667332906e-3f;
-    unsigned ax = pk_bits(x);
-    const int neg = (int)(ax >> 31);
-    ax &= 0x7fffffffu;
-    if (ax >= 0x42aeac50u) {
-        if (ax > 0x7f800000u) return x;
-        if (ax >= 0x42b17218u && !neg) return x * 0x1p127f;
-        if (neg && ax >= 0x42cff1b5u) return 0.0f;
-    }
-    float hi, lo;
-    int k;
-    if (ax > 0x3eb17218u) {
-        if (ax > 0x3f851592u) k = (int)(inv_ln2 * x + (neg ? -0.5f : 0.5f));
-        else k = 1 - neg - neg;
-        hi = x - (float)k * ln2_hi;
-        lo = (float)k * ln2_lo;
-        x = hi - lo;
-    } else if (ax > 0x39000000u) {
-        k = 0;
-        hi = x;
-        lo = 0.0f;
-    } else {
-        return 1.0f + x;
-    }
-    const float xx = x * x;
-    const float c = x - xx * (p1 + xx * p2);
-    const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
-    return k == 0 ? y : pk_ldexpf(y, k);
+    const unsigned bx = pk_bits(x);
+    const bool neg = (bx >> 31) != 0;
+    const unsigned ax = bx & 0x7fffffffu;
+    // the reduction's multiple of ln2 (|x| below 104 here, so in range of int)
+    const float xk = ax < 0x42d00000u ? x : 0.0f;
+    const int kbig = (int)(inv_ln2 * xk + (neg ? -0.5f : 0.5f));
+    const int k = ax > 0x3f851592u ? kbig : ax > 0x3eb17218u ? 1 - 2 * (int)neg : 0;
+    const float fk = (float)k;
+    const float hi = xk - fk * ln2_hi;
+    const float lo = fk * ln2_lo;
+    const float r = hi - lo;
+    const float rr = r * r;
+    const float c = r - rr * (p1 + rr * p2);
+    const float y = 1.0f + (r * c / (2.0f - c) - lo + hi);
+    // y * 2^k as scalbnf computes it (k lies in [-150, 150])
+    const bool up = k > 127, down = k < -126;
+    const float s = up ? 0x1p127f : down ? 0x1p-102f : 1.0f;
+    const int kk = up ? k - 127 : down ? k + 102 : k;
+    const float scaled = (y * s) * pk_float((unsigned)(0x7f + kk) << 23);
+    float res = k == 0 ? y : scaled;
+    res = ax <= 0x39000000u ? 1.0f + x : res;
+    res = neg && ax >= 0x42cff1b5u ? 0.0f : res;
+    res = !neg && ax >= 0x42b17218u ? x * 0x1p127f : res;
+    return ax > 0x7f800000u ? x : res;
+}
+
+// pk_expf on (-87.34, 0] (a softmax's exp(x - m)): there no special input
+// occurs and k lies in [-126, 0], so the same operations without the special
+// cases' selects and scalbnf's pre-scaling give the same bits.
+PK_DEV bool pk_expf_le0_ok(float x) {
+    const unsigned b = pk_bits(x);
+    return b == 0u || (b >= 0x80000000u && b < 0xc2aeac50u);
+}
+PK_DEV float pk_expf_le0(float x) {
+    const float ln2_hi = 6.9314575195e-1f, ln2_lo = 1.4286067653e-6f, inv_ln2 = 1.4426950216e+0f;
+    const float p1 = 1.6666625440e-1f, p2 = -2.7667332906e-3f;
+    const unsigned ax = pk_bits(x) & 0x7fffffffu;
+    const int k = ax > 0x3f851592u ? (int)(inv_ln2 * x + -0.5f) : ax > 0x3eb17218u ? -1 : 0;
+    const float fk = (float)k;
+    const float hi = x - fk * ln2_hi;
+    const float lo = fk * ln2_lo;
+    const float r = hi - lo;
+    const float rr = r * r;
+    const float c = r - rr * (p1 + rr * p2);
+    const float y = 1.0f + (r * c / (2.0f - c) - lo + hi);
+    const float res = k == 0 ? y : y * pk_float((unsigned)(0x7f + k) << 23);
+    return ax <= 0x39000000u ? 1.0f + x : res;
 }
 
 PK_DEV float pk_logf(float x) {

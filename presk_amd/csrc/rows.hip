@@ -331,6 +331,456 @@ hipError_t launch_long(const RowArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// ---- long rows, many of them: every lane walks a row ---------------------------
+//
+// A wave owns R rows (a lane each, R <= 64) and streams them in chunks of
+// WE = 4096 elements (R rows x CW = WE / R columns).  Each chunk is loaded
+// coalesced (16-byte vectors where the rows allow), parked in LDS as f32,
+// and walked: lane i runs row i's part of the pass in index order -- the
+// nest's own loop, so every running sum is the interpreter's -- while the
+// next chunk's loads are already in flight.  (Row means and sums, and `sum_to`
+// onto leading axes.)  The mask of a masked softmax over long rows is read as
+// bits, packed once per launch (pack_mask_kernel): allowed <=> real(mask) >
+// 0.5 <=> mask > 0 for an integer.
+constexpr int WE = 4096;
+
+__host__ __device__ constexpr long long mask_words(long long n) { return (n + 63) / 64 * 2; }
+
+
+
+__global__ void __launch_bounds__(256) pack_mask_kernel(const long long* mask, unsigned* bits, long long n,
+                                                        long long words) {
+    const long long r = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const long long c0 = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64;
+    if (c0 >= n) return;
+    const long long c = c0 + lane;
+    const unsigned long long b = __ballot(c < n && mask[r * n + c] > 0);
+    if (lane < 2) bits[r * words + c0 / 32 + lane] = (unsigned)(lane == 0 ? b : b >> 32);
+}
+
+template <int ST>
+struct Raw {
+    // storage elements per 16-byte vector
+    static constexpr int V = ST == 0 ? 4 : 8;
+};
+
+template <int OP, int ST, int R, int VEC>
+__global__ void __launch_bounds__(64) rows_walk_kernel(RowArgs a) {
+    constexpr int CW = WE / R, TS = CW + 4;     // TS = 4 (mod 32): a b128 walk read is conflict-free
+    constexpr int NV = WE / 64 / VEC;            // vectors per lane per chunk
+    constexpr int ESZ = ST == 0 ? 4 : 2;
+    static_assert(CW % 64 == 0 && CW % VEC == 0, "chunk geometry");
+    __shared__ __attribute__((aligned(16))) float tile[R * TS];
+    const int lane = threadIdx.x;
+    const long long row0 = (long long)blockIdx.x * R;
+    const long long n = a.n;
+    const int nr = (int)(a.rows - row0 < R ? a.rows - row0 : R);
+    const bool walker = lane < nr;
+    bool ovf = false;
+    const long long nch = (n + CW - 1) / CW;
+    using W = unsigned __attribute__((ext_vector_type(VEC * ESZ / 4 > 0 ? VEC * ESZ / 4 : 1)));
+    // storage words of this lane's part of a chunk
+    typedef unsigned short H;
+    W wv[VEC * ESZ >= 4 ? NV : 1];
+    H hv[VEC * ESZ >= 4 ? 1 : NV];
+    (void)wv;
+    (void)hv;
+    auto slot = [&](int q, int& row, int& col) {
+        const int e = (q * 64 + lane) * VEC;
+        row = e / CW;
+        col = e % CW;
+    };
+    auto fetch = [&](long long c0, int cw) {
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            int row, col;
+            slot(q, row, col);
+            row = row < nr ? row : nr - 1;
+            col = col < cw ? col : cw - VEC;
+            const long long off = (row0 + row) * n + c0 + col;
+            if constexpr (VEC * ESZ >= 4) wv[q] = *(const W*)((const char*)a.x + off * ESZ);
+            else hv[q] = ((const H*)a.x)[off];
+        }
+    };
+    auto put = [&]() {
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            int row, col;
+            slot(q, row, col);
+            float f[VEC];
+            if constexpr (VEC * ESZ >= 4) {
+                if constexpr (ST == 0) {
+#pragma unroll
+                    for (int u = 0; u < VEC; ++u) f[u] = __uint_as_float(wv[q][u]);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < VEC; ++u) {
+                        const H h = (H)(wv[q][u / 2] >> (16 * (u & 1)));
+                        f[u] = ST == 1 ? pk_bf16_to_f32(h) : pk_f16_to_f32(h);
+                    }
+                }
+            } else {
+                f[0] = ST == 1 ? pk_bf16_to_f32(hv[q]) : pk_f16_to_f32(hv[q]);
+            }
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) tile[row * TS + col + u] = f[u];
+        }
+    };
+    // the row in index order: visit(x) in the walking lane
+    auto pass = [&](auto&& visit) {
+        int cw = (int)(n < CW ? n : CW);
+        fetch(0, cw);
+        for (long long ch = 0; ch < nch; ++ch) {
+            const long long c0 = ch * CW;
+            cw = (int)(n - c0 < CW ? n - c0 : CW);
+            __syncthreads();
+            put();
+            __syncthreads();
+            if (ch + 1 < nch) fetch(c0 + CW, (int)(n - c0 - CW < CW ? n - c0 - CW : CW));
+            if (walker) {
+                const float* t = &tile[lane * TS];
+                int j = 0;
+#pragma unroll 8
+                for (; j + 4 <= cw; j += 4) {
+                    const float4 q = *(const float4*)&t[j];
+                    visit(q.x);
+                    visit(q.y);
+                    visit(q.z);
+                    visit(q.w);
+                }
+                for (; j < cw; ++j) visit(t[j]);
+            }
+        }
+    };
+    const long long r = row0 + lane;
+    if (OP == kRowMean || OP == kRowSum) {
+        float acc = 0.f;
+        pass([&](float x) { acc = acc + x; });
+        if (walker) st<ST>(a.out, r, OP == kRowMean ? acc / a.n_real : acc, ovf);
+    } else if (OP == kSumToRows) {
+        float acc = 0.f;
+        pass([&](float x) {
+            const float s = acc + x;
+            if (ST == 2) ovf |= pk_overflows_f16(s);
+            acc = stored<ST>(s);
+        });
+        if (walker) st<ST>(a.out, r, acc, ovf);
+    }
+    if (ovf && a.flag) atomicOr(a.flag, 1u);
+}
+
+template <int OP, int ST, int R>
+hipError_t launch_walk_v(const RowArgs& a, hipStream_t stream) {
+    constexpr int V = Raw<ST>::V;
+    const unsigned grid = (unsigned)((a.rows + R - 1) / R);
+    const int esz = ST == 0 ? 4 : 2;
+    const bool vec = (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.out % 16 == 0 && (a.n * esz) % 16 == 0;
+    if (vec) rows_walk_kernel<OP, ST, R, V><<<grid, 64, 0, stream>>>(a);
+    else rows_walk_kernel<OP, ST, R, 1><<<grid, 64, 0, stream>>>(a);
+    return hipGetLastError();
+}
+
+template <int OP, int R>
+hipError_t launch_walk_r(const RowArgs& a, hipStream_t stream) {
+    switch (a.storage) {
+        case 0: return launch_walk_v<OP, 0, R>(a, stream);
+        case 1: return launch_walk_v<OP, 1, R>(a, stream);
+        case 2: return launch_walk_v<OP, 2, R>(a, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+// ---- softmax over long rows, streamed ------------------------------------------
+//
+// One wave owns R = 16 rows and streams them in chunks of 64 columns, lane j
+// on column c0 + j of every row, the next chunk's loads in flight while the
+// current one is worked; the nest's three loops are three passes:
+// * the max.  The nest's running max (from element 0, or from the first
+//   allowed element; a strict `>` after it) is the max over the non-NaN
+//   (allowed) elements unless that first element is NaN (then NaN), or 0
+//   when nothing is allowed: order-free apart from the first element, so each
+//   lane keeps its own and a wave reduction joins them (a max over +0 and -0
+//   may differ in sign, which no exp(x - m) can see);
+// * z.  Each exponential is computed in the coalesced layout, parked in LDS,
+//   and lane i adds row i's in index order -- the interpreter's running sum,
+//   bit for bit.  Sixteen sums a wave and several waves a SIMD keep these
+//   dependent chains from waiting on each other;
+// * the outputs, e / z (3 passes) or stored(e) / z (2 passes), the
+//   exponential computed again as the nest computes it again, stored
+//   coalesced.
+// The mask arrives as bits (pack_mask_kernel), one uniform 64-bit word per
+// row and chunk.
+// f[u] <- exp(f[u] - m) where bit u of `al` allows it, else 0: the nest's
+// select(allowed, exp(x - m), 0).  A refused element's exponent is taken at
+// 0 (its value is never used), so that a group whose allowed exponents all
+// lie in (-87.34, 0] -- a softmax's, unless a NaN or an infinity is about --
+// takes expf's shorter path (pk_expf_le0, the same bits there).
+template <int VEC>
+__device__ __forceinline__ void exps(float (&f)[VEC], float m, unsigned al) {
+    float arg[VEC];
+    bool ok = true;
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+        arg[u] = ((al >> u) & 1u) != 0 ? f[u] - m : 0.f;
+        ok = ok && pk_expf_le0_ok(arg[u]);
+    }
+    if (__all(ok)) {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) f[u] = ((al >> u) & 1u) != 0 ? pk_expf_le0(arg[u]) : 0.f;
+    } else {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) f[u] = ((al >> u) & 1u) != 0 ? pk_expf(arg[u]) : 0.f;
+    }
+}
+
+constexpr int SR = 16, SCW = 64, STS = SCW + 4;   // STS = 4 (mod 32): b128 tile reads and writes
+
+// A lane moves 16 bytes a load: VEC elements of one row.  Lane l in slot q of
+// a chunk holds row q * RPI + l / LPR, columns (l % LPR) * VEC ..+VEC.
+template <int ST>
+struct SGeo {
+    static constexpr int VEC = ST == 0 ? 4 : 8;
+    static constexpr int LPR = SCW / VEC;      // lanes a row
+    static constexpr int RPI = 64 / LPR;       // rows an instruction
+    static constexpr int NQ = SR / RPI;        // vectors a lane a chunk
+};
+
+template <int OP, int ST>
+__global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
+    constexpr bool MASKED = OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2;
+    constexpr bool TWO = OP == kSoftmax2 || OP == kMaskedSoftmax2;
+    using G = SGeo<ST>;
+    constexpr int VEC = G::VEC, LPR = G::LPR, RPI = G::RPI, NQ = G::NQ;
+    typedef unsigned U4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) float tile[SR * STS];
+    const int lane = threadIdx.x;
+    const long long row0 = (long long)blockIdx.x * SR;
+    const long long n = a.n;
+    const int nr = (int)(a.rows - row0 < SR ? a.rows - row0 : SR);
+    const long long MW = mask_words(n);
+    const int lc = (lane % LPR) * VEC;              // this lane's first column in a chunk
+    bool ovf = false;
+    int myrow[NQ];
+    const unsigned* mrow[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int r = q * RPI + lane / LPR;
+        myrow[q] = r < nr ? r : nr - 1;             // clamped: a dead row's values are never used
+        mrow[q] = MASKED ? a.mbits + ((row0 + myrow[q]) % a.mask_rows) * MW : nullptr;
+    }
+    // the 16-byte vectors of the chunk at c0 (columns clamped into the row)
+    auto load = [&](long long c0, U4 (&w)[NQ]) {
+        const long long col = c0 + lc < n ? c0 + lc : n - VEC;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) w[q] = *(const U4*)((const char*)a.x + ((row0 + myrow[q]) * n + col) * (ST == 0 ? 4 : 2));
+    };
+    auto unpack = [&](const U4& w, float (&f)[VEC]) {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+            if (ST == 0) f[u] = __uint_as_float(w[u]);
+            else {
+                const unsigned short h = (unsigned short)(w[u / 2] >> (16 * (u & 1)));
+                f[u] = ST == 1 ? pk_bf16_to_f32(h) : pk_f16_to_f32(h);
+            }
+        }
+    };
+    // this lane's VEC columns at c0 in slot q: allowed and inside the row, as bits
+    auto bits = [&](int q, long long c0) -> unsigned {
+        const long long c = c0 + lc;
+        const unsigned live = c >= n ? 0u : n - c >= VEC ? (1u << VEC) - 1u : (1u << (n - c)) - 1u;
+        if (!MASKED) return live;
+        return (mrow[q][c >> 5] >> (c & 31)) & live;
+    };
+    auto pass = [&](auto&& body) {
+        U4 w[NQ], nx[NQ];
+        load(0, w);
+        for (long long c0 = 0; c0 < n; c0 += SCW) {
+            const bool more = c0 + SCW < n;
+            if (more) load(c0 + SCW, nx);
+            body(c0, w);
+            if (more) {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) w[q] = nx[q];
+            }
+        }
+    };
+
+    // 1. the max: each lane's allowed non-NaN max and first allowed column,
+    //    per row it holds; joined over the row's lanes
+    const int BIG = 0x7fffffff;
+    float pm[NQ];
+    int fa[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        pm[q] = -__builtin_inff();
+        fa[q] = BIG;
+    }
+    pass([&](long long c0, U4 (&w)[NQ]) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            float f[VEC];
+            unpack(w[q], f);
+            const unsigned al = bits(q, c0);
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) {
+                const bool ok = ((al >> u) & 1u) != 0;
+                pm[q] = ok && f[u] > pm[q] ? f[u] : pm[q];
+                fa[q] = ok && fa[q] == BIG ? (int)(c0 + lc + u) : fa[q];
+            }
+        }
+    });
+    float mq[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        float m = pm[q];
+        int f = fa[q];
+        for (int off = LPR / 2; off > 0; off >>= 1) {
+            const float o = __shfl_xor(m, off, 64);
+            const int g = __shfl_xor(f, off, 64);
+            m = o > m ? o : m;
+            f = g < f ? g : f;
+        }
+        // the first allowed element NaN: the max is NaN; none allowed: 0
+        const float first = f == BIG ? 0.f : ld<ST>(a.x, (row0 + myrow[q]) * n + f);
+        mq[q] = f == BIG ? 0.f : first != first ? first : m;
+    }
+
+    // 2. z: the exponentials into the tile, lane i walking row i in order
+    float z = 0.f;
+    pass([&](long long c0, U4 (&w)[NQ]) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            float f[VEC];
+            unpack(w[q], f);
+            const unsigned al = bits(q, c0);
+            exps<VEC>(f, mq[q], al);
+            float* t = &tile[(q * RPI + lane / LPR) * STS + lc];
+#pragma unroll
+            for (int u = 0; u < VEC; u += 4) *(float4*)&t[u] = float4{f[u], f[u + 1], f[u + 2], f[u + 3]};
+        }
+        __syncthreads();
+        if (lane < nr) {
+            const float* t = &tile[lane * STS];
+            const int cw = (int)(n - c0 < SCW ? n - c0 : SCW);
+            if (cw == SCW) {
+#pragma unroll
+                for (int j = 0; j < SCW; j += 4) {
+                    const float4 v = *(const float4*)&t[j];
+                    z = z + v.x;
+                    z = z + v.y;
+                    z = z + v.z;
+                    z = z + v.w;
+                }
+            } else {
+                for (int j = 0; j < cw; ++j) z = z + t[j];
+            }
+        }
+        __syncthreads();
+    });
+    float zq[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        // row q * RPI + lane / LPR's z, from its walking lane
+        const int src = q * RPI + lane / LPR;
+        zq[q] = __shfl(z, src, 64);
+    }
+
+    // 3. the outputs, 16 bytes a lane
+    pass([&](long long c0, U4 (&w)[NQ]) {
+        if (c0 + lc >= n) return;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int row = q * RPI + lane / LPR;
+            if (row >= nr) continue;
+            float f[VEC];
+            unpack(w[q], f);
+            const unsigned al = bits(q, c0);
+            exps<VEC>(f, mq[q], al);
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) {
+                const bool ok = ((al >> u) & 1u) != 0;
+                const float e = f[u];
+                float v;
+                if (TWO) {
+                    if (ST == 2) ovf |= pk_overflows_f16(e);
+                    v = stored<ST>(e) / zq[q];
+                } else {
+                    v = e / zq[q];
+                }
+                f[u] = ok ? v : 0.f;
+            }
+            U4 o;
+            if (ST == 0) {
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) o[u] = __float_as_uint(f[u]);
+            } else {
+                o = U4{0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) {
+                    if (ST == 2) ovf |= pk_overflows_f16(f[u]);
+                    const unsigned h = ST == 1 ? pk_f32_to_bf16(f[u]) : pk_f32_to_f16(f[u]);
+                    o[u / 2] |= h << (16 * (u & 1));
+                }
+            }
+            *(U4*)((char*)a.out + ((row0 + row) * n + c0 + lc) * (ST == 0 ? 4 : 2)) = o;
+        }
+    });
+    if (ovf && a.flag) atomicOr(a.flag, 1u);
+}
+
+template <int OP, int R, bool RES>
+hipError_t launch_r(const RowArgs& a, hipStream_t stream);
+
+template <int OP>
+hipError_t launch_stream(const RowArgs& a, hipStream_t stream) {
+    // whole 16-byte vectors: rows of a multiple of 64 columns on aligned
+    // buffers (the last chunk of a row is then whole too); others take the
+    // general row kernel
+    const int esz = a.storage == 0 ? 4 : 2;
+    if (a.n % SCW != 0 || (uintptr_t)a.x % 16 != 0 || (uintptr_t)a.out % 16 != 0 || (a.n * esz) % 16 != 0)
+        return launch_r<OP, 16, false>(a, stream);
+    const unsigned grid = (unsigned)((a.rows + SR - 1) / SR);
+    switch (a.storage) {
+        case 0: softmax_stream_kernel<OP, 0><<<grid, 64, 0, stream>>>(a); break;
+        case 1: softmax_stream_kernel<OP, 1><<<grid, 64, 0, stream>>>(a); break;
+        case 2: softmax_stream_kernel<OP, 2><<<grid, 64, 0, stream>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Rows per wave for the walk: 64 (every lane walks) where that still leaves
+// 1024 waves, else fewer, down to 4, to keep some 512 waves in flight.
+template <int OP>
+hipError_t launch_walk(const RowArgs& a, hipStream_t stream) {
+    constexpr bool SOFTMAX = OP == kSoftmax3 || OP == kSoftmax2 || OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2;
+    if (OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2) {
+        if (!a.mbits) return hipErrorInvalidValue;
+        const long long words = mask_words(a.n);
+        const dim3 grid((unsigned)((a.n + 255) / 256), (unsigned)a.mask_rows);
+        pack_mask_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, a.mbits, a.n, words);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if constexpr (SOFTMAX) {
+        return launch_stream<OP>(a, stream);
+    } else {
+        const long long r = a.rows;
+        if (r >= 64 * 1024) return launch_walk_r<OP, 64>(a, stream);
+        if (r >= 32 * 512) return launch_walk_r<OP, 32>(a, stream);
+        if (r >= 16 * 512) return launch_walk_r<OP, 16>(a, stream);
+        if (r >= 8 * 512) return launch_walk_r<OP, 8>(a, stream);
+        return launch_walk_r<OP, 4>(a, stream);
+    }
+}
+
+// the long-row walk serves these nests when their rows do not fit in registers
+constexpr bool walks(int op) {
+    return op == kRowMean || op == kRowSum || op == kSumToRows || op == kSoftmax3 || op == kSoftmax2 ||
+           op == kMaskedSoftmax3 || op == kMaskedSoftmax2;
+}
+
 template <int OP, int R, bool RES>
 hipError_t launch_r(const RowArgs& a, hipStream_t stream) {
     const unsigned grid = (unsigned)((a.rows + R - 1) / R);
@@ -356,12 +806,21 @@ hipError_t launch_op(const RowArgs& a, hipStream_t stream) {
     if ((OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2) && a.mask_rows <= 0) return hipErrorInvalidValue;
     if ((a.rows + 3) / 4 > 0x7fffffffll) return hipErrorInvalidValue;
     const bool res = a.n <= NRES * CW;
+    if constexpr (walks(OP)) {
+        if (!res) return launch_walk<OP>(a, stream);
+    }
     if (a.rows >= 8192)
         return res ? launch_r<OP, 16, true>(a, stream) : launch_r<OP, 16, false>(a, stream);
     return res ? launch_r<OP, 4, true>(a, stream) : launch_r<OP, 4, false>(a, stream);
 }
 
 }  // namespace
+
+long long rows_mask_words(long long n) { return mask_words(n); }
+
+bool rows_need_mask_bits(const RowArgs& a) {
+    return (a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2) && a.rows > 0 && a.n > NRES * CW;
+}
 
 hipError_t rows_launch(const RowArgs& a, hipStream_t stream) {
     switch (a.op) {

@@ -20,8 +20,14 @@ struct RowArgs {
     long long rows, n, mask_rows;
     float n_real;         // n as the nest's f32 constant (mean)
     int op, storage;      // RowOp; 0 f32, 1 bf16, 2 f16
+    unsigned* mbits;      // masked softmax over long rows: the mask as bits, [mask_rows][mask_words(n)]
 };
 
 hipError_t rows_launch(const RowArgs& a, hipStream_t stream);
+
+// Whether a launch of these arguments reads the mask as bits (a workspace
+// of mask_rows * mask_words(n) words the caller provides in `mbits`).
+bool rows_need_mask_bits(const RowArgs& a);
+long long rows_mask_words(long long n);
 
 }  // namespace presk

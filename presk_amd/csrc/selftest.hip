@@ -56,6 +56,8 @@ __device__ unsigned eval1(int fn, unsigned long long i) {
         case 3: return pk_bits(pk_erff(x));
         case 4: return pk_bits(pk_sinf(x));
         case 5: return pk_bits(pk_cosf(x));
+        // expf through the softmax's fast path where it applies: expf's bits
+        case 6: return pk_bits(pk_expf_le0_ok(x) ? pk_expf_le0(x) : pk_expf(x));
         case 10: return pk_f32_to_bf16(x);
         case 11: return pk_f32_to_f16(x);
         case 12: return pk_f32_to_e8m15(x);
@@ -92,7 +94,7 @@ __global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long 
 }  // namespace
 
 hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
-    const int known[] = {0, 1, 2, 3, 4, 5, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
+    const int known[] = {0, 1, 2, 3, 4, 5, 6, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
     bool ok = false;
     for (int f : known) ok |= f == fn;
     if (!ok || hi < lo) return hipErrorInvalidValue;

@@ -280,11 +280,14 @@ def _layernorm(b: Builder, x, g, bias, keep: bool, tag: str):
 def _layernorm_in(b: Builder, x, g, bias, keep: bool, tag: str):
     mu = b.mean(x, "model", name=f"{tag}.mu")
     if not keep:
+        # fusion groups (crates/presk-core/src/fusion.rs:138) join only
+        # values of one result type: {x - mu, ^2} and {x - mu, /, *, +} of
+        # [batch, seq, model], {var + eps, sqrt} of [batch, seq]
         sq = b.fused([("sub", [("in", 0), ("in", 1)]), ("pow2", [("step", 0)])], [x, mu], x)
         var = b.mean(sq, "model")
-        return b.fused([("sub", [("in", 0), ("in", 1)]), ("add", [("in", 2), ("in", 3)]), ("sqrt", [("step", 1)]),
-                        ("div", [("step", 0), ("step", 2)]), ("mul", [("step", 3), ("in", 4)]), ("add", [("step", 4), ("in", 5)])],
-                       [x, mu, var, "eps", g, bias], x), {}
+        sd = b.fused([("add", [("in", 0), ("in", 1)]), ("sqrt", [("step", 0)])], [var, "eps"], var, name=f"{tag}.sd")
+        return b.fused([("sub", [("in", 0), ("in", 1)]), ("div", [("step", 0), ("in", 2)]), ("mul", [("step", 1), ("in", 3)]),
+                        ("add", [("step", 2), ("in", 4)])], [x, mu, sd, g, bias], x), {}
     xm = b.binary("sub", x, mu, name=f"{tag}.xm")
     sq = b.unary("pow2", xm, name=f"{tag}.sq")
     var = b.mean(sq, "model", name=f"{tag}.var")

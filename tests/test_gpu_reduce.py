@@ -157,11 +157,13 @@ def _same_bits_nan_as_nan(got, want, dt):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-def test_rows_class_nan_and_empty_rows(dt):
+@pytest.mark.parametrize("T", [40, 300])
+def test_rows_class_nan_and_empty_rows(dt, T):
     """the masked max's corner cases: a NaN first allowed element (the max is
     NaN), a NaN later allowed element and a NaN disallowed one (both passed
-    over), -inf first, and a row the mask allows nowhere (all zeros)"""
-    B, H, T = 2, 3, 40
+    over), -inf first, and a row the mask allows nowhere (all zeros); rows
+    that stay in registers (40) and rows the long-row walk streams (300)"""
+    B, H = 2, 3
     s = O(A(("batch", B), ("heads", H), ("seq", T), ("seq2", T)))
     mask = O(A(("seq", T), ("seq2", T)), "idx")
     ex = hip.HipExec(0, mode=hip.EXACT)
@@ -245,3 +247,45 @@ def test_long_rows_exact(dt):
         c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
         assert c.kind == "rows", c.kind
         assert out.download(np.uint8, nb).tobytes() == want.view(np.uint8).tobytes(), low.name
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_long_row_walk_attention_shape(dt):
+    """softmax over 2048-wide rows as an attention at Llama's context makes
+    them (8192 rows, a causal mask over 2048 x 2048, the mask packed to bits):
+    3 and 2 passes, masked and not, with NaNs, -inf and an empty mask row;
+    and a row mean over 2048 x 4096 (RMSNorm's) -- every byte as the oracle's"""
+    H, T = 4, 2048
+    s = O(A(("batch", 1), ("heads", H), ("seq", T), ("seq2", T)))
+    mask = O(A(("seq", T), ("seq2", T)), "idx")
+    ex = hip.HipExec(0, mode=hip.EXACT)
+    from oracle import kernel_text as kt
+    cases = [L.masked_softmax("seq2", [s, mask], dt), L.masked_softmax("seq2", [s, mask], dt, two_passes=True),
+             L.softmax("seq2", [s], dt), L.softmax_two_pass("seq2", [s], dt),
+             L.reduce_axis("mean", "model", [O(A(("batch", 1), ("seq", 2048), ("model", 4096)))], dt)]
+    for low in cases:
+        print(f"[walk] {low.name} {dt}", flush=True)
+        ins = zoo.inputs(low, seed=21, scale=4.0)
+        if low.name.startswith("softmax"):
+            x = fmt.decode(ins[0], dt).reshape(H, T, T).copy()
+            x[0, 7, 0] = np.nan
+            x[1, 9, 4] = np.nan
+            x[2, 3, 1500] = np.nan
+            x[3, 10, 0] = -np.inf
+            x[0, 2047, 2047] = np.inf
+            ins[0] = fmt.encode(x.astype(np.float32), dt)
+        if len(ins) == 2:
+            m = np.tril(np.ones((T, T), np.int64))
+            m[5, :] = 0
+            m[100, 50] = -3
+            m[200, 300] = 7
+            ins[1] = m.ravel()
+        want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes, threads=8)
+        k = kt.parse_kernel(low.text)
+        nbytes = k.output.numel * hip.STORAGE_BYTES[dt]
+        out = hip.DeviceBuffer(nbytes)
+        out.upload(np.full(nbytes, 0xFF, np.uint8))
+        c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+        assert c.kind == "rows", c.kind
+        got = out.download(want.dtype, want.size)
+        _same_bits_nan_as_nan(got.reshape(-1), want.reshape(-1), dt)

@@ -26,3 +26,18 @@ def test_device_function_everywhere(name, golden):
             bad.append(i)
     print(f"[scalar] {name}: {len(bad)} of {len(spec.blocks(domain))} blocks differ", flush=True)
     assert not bad, f"{name}: blocks {bad[:8]} differ from the reference"
+
+
+def test_expf_fast_path_is_expf(golden):
+    """the softmax's exp on (-87.34, 0] (pk_expf_le0, taken where
+    pk_expf_le0_ok holds, pk_expf elsewhere) has expf's digest over every f32"""
+    hip.init(0)
+    g = golden["functions"]["expf"]
+    _, domain = spec.FUNCTIONS["expf"]
+    bad = []
+    for i, (lo, hi) in enumerate(spec.blocks(domain)):
+        d = ctypes.c_uint64()
+        hip.check(hip.lib().presk_hip_scalar_digest(6, lo, hi, ctypes.byref(d)))
+        if format(d.value, "016x") != g["blocks"][i]:
+            bad.append(i)
+    assert not bad, f"blocks {bad[:8]} differ from the reference's expf"
