@@ -27,7 +27,7 @@ DATA = {"gpt-step": "synthetic (seeded ids and targets uniform over the vocabula
                  "presk_hip_fill_normal)"}
 
 
-def workload(name: str, dtype: str, rows=None, realize=None):
+def workload(name: str, dtype: str, rows=None, realize=None, dropout=0.0):
     """(program, host inputs, tokens per step, contraction flops, config record)
     of a workload; `rows` shrinks it for the CPU sample; `realize` (`@FILE`)
     gives the GPT's sites their storage types (a mixed realization).  The
@@ -58,13 +58,13 @@ def workload(name: str, dtype: str, rows=None, realize=None):
     train = name == "gpt-step"
     s = gpt.COURSE if rows is None else gpt.GptShape(B=max(rows // gpt.COURSE.T, 1))
     r = Realization.parse(realize) if realize else None
-    p, b, names = gpt.build(s, dtype, train=train, realize=r)
+    p, b, names = gpt.build(s, dtype, train=train, realize=r, dropout=dropout if train else 0.0)
     host = gpt.host_inputs(s)
     cfg = {"workload": ("config 4: course GPT training step (loss value and gradient of every parameter)" if train
                         else "config 3: course GPT forward and loss"),
            "L": s.L, "d_model": s.D, "heads": s.H, "vocab": s.V, "batch": s.B, "seq": s.T,
            "storage": dtype if r is None else f"mixed ({realize})", "compute": "f32", "launches": len(p.launches),
-           "dropout": 0.0}
+           "dropout": dropout if train else 0.0}
     return p, host, s.B * s.T, gpt.contraction_flops(s, train), cfg
 
 
@@ -106,13 +106,13 @@ def copy_probe():
     print(json.dumps({"copy_probe": low.name, "bytes_read": 4 * n, "bytes_written": 4 * n, "runs": 3}), flush=True)
 
 
-def cpu_baseline(name: str, dtype: str, rows: int, threads: int, realize=None):
+def cpu_baseline(name: str, dtype: str, rows: int, threads: int, realize=None, dropout=0.0):
     """The oracle (the kernel interpreter's semantics in C, -O3 -march=native,
     the outermost parallel loop split over OpenMP threads as the native
     executor splits it) on a bounded sample of the workload's rows."""
     from tests import cpu_program
 
-    p, host, tokens, _, _ = workload(name, dtype, rows, realize)
+    p, host, tokens, _, _ = workload(name, dtype, rows, realize, dropout)
     cpu_program.compile_all(p, native=True, workers=threads)
     best = None
     for _ in range(1 if name.startswith("gpt") else 2):
@@ -132,6 +132,9 @@ def main():
     ap.add_argument("--dtype", default=None)
     ap.add_argument("--realize", default=None, metavar="@FILE",
                     help="a realization file (the reference's schema) for the GPT workloads: storage type per site")
+    ap.add_argument("--dropout", type=float, default=0.0,
+                    help="the training step's dropout rate (the course's 0.2): masks drawn on the device, a new "
+                         "step key each step")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="issue the launches one by one instead of one HIP graph")
     ap.add_argument("--dominant-only", type=int, default=0, metavar="N",
@@ -151,7 +154,14 @@ def main():
         copy_probe()
         return
     dtype = args.dtype or ("bf16" if args.workload in ("mlp", "llama") else "f32")
-    p, host, tokens, flops, cfg = workload(args.workload, dtype, realize=args.realize)
+    p, host, tokens, flops, cfg = workload(args.workload, dtype, realize=args.realize, dropout=args.dropout)
+    # a training run's keys: step i draws from Key::child(run key, i); the site
+    # keys are derived before the timed region, uploaded (608 bytes) each step
+    step_keys = []
+    if p.masks:
+        from presk_amd import gpt, keys
+        run_key = keys.from_seed(0)
+        step_keys = [gpt.site_keys(gpt.COURSE, keys.child(run_key, i)) for i in range(args.warmup + args.steps)]
     p.compile()
     if host is None:
         from presk_amd import llama
@@ -162,11 +172,15 @@ def main():
     if not args.eager:
         # the step's 587 launches recorded once and replayed as one HIP graph
         p.record(graph=True)
-    for _ in range(args.warmup):
+    for i in range(args.warmup):
+        if step_keys:
+            p.set_keys(step_keys[i])
         p.run()
     hip.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        if step_keys:
+            p.set_keys(step_keys[args.warmup + i])
         p.run()
     hip.sync()
     dt = time.perf_counter() - t0
@@ -225,7 +239,7 @@ def main():
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)
         rows = args.cpu_rows or {"mlp": 4096, "linear": 1024, "gpt-step": 2048, "gpt-forward": 4096}[args.workload]
-        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads, args.realize)
+        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads, args.realize, args.dropout)
         rec["cpu_baseline"] = {"value": round(v, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
                                "sample": f"{n} of {tokens} tokens (rows) of the same workload: the oracle's C restatement of "
                                          f"the same default-layout nests (-O3 -march=native, -ffp-contract=off, sequential "

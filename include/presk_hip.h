@@ -154,9 +154,25 @@ int presk_hip_batch_add(presk_hip_batch *b, const presk_hip_kernel *k, void *con
 /* An edge conversion (presk_hip_convert) as a step of the sequence. */
 int presk_hip_batch_add_convert(presk_hip_batch *b, const void *src, const char *from, void *dst, const char *to,
                                 int64_t n, uint32_t *flag);
+/* A training dropout mask (presk_hip_dropout_mask) as a step of the sequence:
+ * the key is read from device memory at each run, so a replayed graph draws
+ * the mask of whatever key the host last wrote there. */
+int presk_hip_batch_add_dropout(presk_hip_batch *b, const void *key, double rate, const char *type, int64_t n,
+                                void *dst);
 int presk_hip_batch_graph(presk_hip_batch *b);
 int presk_hip_batch_run(presk_hip_batch *b, void *stream);
 void presk_hip_batch_release(presk_hip_batch *b);
+
+/* A training dropout mask on the device: `DropoutMask` with training on
+ * (crates/presk-kernel/src/host.rs:1610-1627 calling dropout_mask,
+ * host.rs:1893-1926, which draws it on the host's workers).  n elements of
+ * type "f64", "f32", "bf16", "f16" or "e8m15": element e is 1/(1-rate) where
+ * the key's e-th uniform draw (uniform01 of its ChaCha20Rng stream read from
+ * word 2e, crates/presk-interp/src/key.rs:43-55) is below 1-rate, else 0,
+ * rounded as Buf::of rounds it -- the host's bits.  `key`: the 32-byte key in
+ * device memory (4-byte aligned).  A rate outside [0, 1) is E7001, as the
+ * host refuses it. */
+int presk_hip_dropout_mask(const void *key, double rate, const char *type, int64_t n, void *dst, void *stream);
 
 /* Seeded synthetic values written in place: n elements mean + std * z of
  * type "f32", "bf16" or "f16", z ~ N(0, 1) a function of (seed, element

@@ -123,6 +123,56 @@ hipError_t launch_from(int to, const void* src, void* dst, long long n, unsigned
 
 size_t width(int t) { return t == 0 ? 8 : t == 1 ? 4 : (t == 2 || t == 4) ? 2 : t == 5 ? 3 : 0; }
 
+
+// ---- dropout masks (crates/presk-kernel/src/host.rs:1893-1926) ----------------
+// Element e is 1/(1-rate) where the key's e-th uniform draw is below 1-rate,
+// else 0, stored as Buf::of stores it (store_f64).  The draw is rand_chacha's
+// ChaCha20Rng read from word 2e: u64 e = words 2e, 2e+1 (the low one first)
+// of the stream -- block e / 8, the counter in state words 12-13, stream 0 in
+// 14-15 -- and uniform01 = (u64 >> 11) / 2^53.  A thread computes one block,
+// eight elements: the mask is counter-based, each piece independent.
+__device__ __forceinline__ unsigned rotl32(unsigned x, int r) { return (x << r) | (x >> (32 - r)); }
+
+__device__ __forceinline__ void chacha20_block(const unsigned (&k)[8], unsigned long long ctr, unsigned (&o)[16]) {
+    unsigned x[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u, k[0], k[1], k[2], k[3],
+                      k[4], k[5], k[6], k[7], (unsigned)ctr, (unsigned)(ctr >> 32), 0u, 0u};
+    unsigned s[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = x[i];
+    auto qr = [&](int a, int b, int c, int d) {
+        x[a] += x[b]; x[d] = rotl32(x[d] ^ x[a], 16);
+        x[c] += x[d]; x[b] = rotl32(x[b] ^ x[c], 12);
+        x[a] += x[b]; x[d] = rotl32(x[d] ^ x[a], 8);
+        x[c] += x[d]; x[b] = rotl32(x[b] ^ x[c], 7);
+    };
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        qr(0, 4, 8, 12); qr(1, 5, 9, 13); qr(2, 6, 10, 14); qr(3, 7, 11, 15);
+        qr(0, 5, 10, 15); qr(1, 6, 11, 12); qr(2, 7, 8, 13); qr(3, 4, 9, 14);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = x[i] + s[i];
+}
+
+template <int T>
+__global__ void __launch_bounds__(256) dropout_kernel(const unsigned* key, double keep, double scale, long long n,
+                                                      void* out) {
+    const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (8 * b >= n) return;
+    unsigned k[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k[i] = key[i];   // the key's 32 bytes as little-endian words
+    unsigned w[16];
+    chacha20_block(k, (unsigned long long)b, w);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const long long e = 8 * b + j;
+        if (e >= n) break;
+        const unsigned long long u64 = (unsigned long long)w[2 * j] | ((unsigned long long)w[2 * j + 1] << 32);
+        const double u = (double)(u64 >> 11) / 9007199254740992.0;
+        store_f64<T>(out, e, u < keep ? scale : 0.0);
+    }
+}
 }  // namespace
 
 int convert_type(const char* name) {
@@ -147,6 +197,23 @@ hipError_t convert_launch(const void* src, int from, void* dst, int to, long lon
         case 5: return launch_from<5>(to, src, dst, n, flag, s);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t dropout_launch(const void* key, double rate, int type, long long n, void* dst, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const double keep = 1.0 - rate, scale = 1.0 / (1.0 - rate);
+    const long long blocks = (n + 7) / 8;
+    const dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
+    const unsigned* k = (const unsigned*)key;
+    switch (type) {
+        case 0: dropout_kernel<0><<<grid, block, 0, s>>>(k, keep, scale, n, dst); break;
+        case 1: dropout_kernel<1><<<grid, block, 0, s>>>(k, keep, scale, n, dst); break;
+        case 2: dropout_kernel<2><<<grid, block, 0, s>>>(k, keep, scale, n, dst); break;
+        case 4: dropout_kernel<4><<<grid, block, 0, s>>>(k, keep, scale, n, dst); break;
+        case 5: dropout_kernel<5><<<grid, block, 0, s>>>(k, keep, scale, n, dst); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 }  // namespace presk

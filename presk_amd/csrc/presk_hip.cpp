@@ -386,13 +386,15 @@ int presk_hip_time(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int
 }  // extern "C"
 
 struct presk_hip_batch {
-    // a kernel launch, or (k null) an edge conversion
+    // a kernel launch, or (k null) an edge conversion, or (k null, rate >= 0)
+    // a dropout mask: bufs {key, dst}, type in `to`
     struct Item {
         const presk_hip_kernel* k;
         std::vector<void*> bufs;
         int64_t lo, hi;
         int from = -1, to = -1;
         int64_t n = 0;
+        double rate = -1.0;
     };
     std::vector<Item> items;
     hipGraph_t graph = nullptr;
@@ -406,6 +408,11 @@ struct presk_hip_batch {
     }
     int run_each(hipStream_t s) const {
         for (const Item& it : items) {
+            if (!it.k && it.rate >= 0.0) {
+                hipError_t e = dropout_launch(it.bufs[0], it.rate, it.to, it.n, it.bufs[1], s);
+                if (e != hipSuccess) return hip_fail(e, "dropout mask");
+                continue;
+            }
             if (!it.k) {
                 hipError_t e = convert_launch(it.bufs[0], it.from, it.bufs[1], it.to, it.n, (unsigned*)it.bufs[2], s);
                 if (e != hipSuccess) return hip_fail(e, "edge conversion");
@@ -442,6 +449,29 @@ int presk_hip_convert(const void* src, const char* from, void* dst, const char* 
     if (n < 0 || (n > 0 && (!src || !dst))) return fail(PRESK_HIP_ERR, "E10001: bad conversion arguments");
     hipError_t e = convert_launch(src, f, dst, t, n, flag, (hipStream_t)stream);
     return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "edge conversion");
+}
+
+int presk_hip_dropout_mask(const void* key, double rate, const char* type, int64_t n, void* dst, void* stream) {
+    const int t = convert_type(type);
+    if (t < 0) return fail(PRESK_HIP_ERR, "E10001: a dropout mask of type `" + std::string(type ? type : "") + "`");
+    if (!(rate >= 0.0 && rate < 1.0)) return fail(PRESK_HIP_ERR, "E7001: dropout: the rate " + std::to_string(rate) + " is not in [0, 1)");
+    if (n < 0 || (n > 0 && (!key || !dst)) || (uintptr_t)key % 4) return fail(PRESK_HIP_ERR, "E10001: bad dropout arguments");
+    hipError_t e = dropout_launch(key, rate, t, n, dst, (hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "dropout mask");
+}
+
+int presk_hip_batch_add_dropout(presk_hip_batch* b, const void* key, double rate, const char* type, int64_t n, void* dst) {
+    if (!b) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    const int t = convert_type(type);
+    if (t < 0 || !(rate >= 0.0 && rate < 1.0) || n < 0 || (n > 0 && (!key || !dst)) || (uintptr_t)key % 4)
+        return fail(PRESK_HIP_ERR, "E10001: bad dropout arguments");
+    b->drop_graph();
+    presk_hip_batch::Item it{nullptr, {const_cast<void*>(key), dst}, 0, 0};
+    it.to = t;
+    it.n = n;
+    it.rate = rate;
+    b->items.push_back(it);
+    return PRESK_HIP_OK;
 }
 
 int presk_hip_batch_add_convert(presk_hip_batch* b, const void* src, const char* from, void* dst, const char* to,

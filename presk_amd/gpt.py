@@ -218,6 +218,17 @@ class Builder:
     def cross_entropy_vjp(self, logits, y, ct, name=None):
         return self._prim(lambda dt: L.cross_entropy_vjp([self.op(logits), self.op(y), self.op(ct)], dt), [logits, y, ct], name)
 
+    def dropout_mask(self, x, slot: int, rate: float, name=None):
+        """`DropoutMask(rate, key, x)`: a mask of x's shape and the site's
+        type, drawn from key `slot` of the program's key table."""
+        name = self._name(name)
+        n = 1
+        for a in self.axes[x]:
+            n *= a.len
+        self.p.add_mask(name, slot, rate, self._dt(name), n)
+        self.axes[name], self.kind[name] = list(self.axes[x]), "real"
+        return name
+
     def slice(self, x, axis, lo, hi, name=None):
         return self._prim(lambda dt: L.slice_(axis, lo, hi, [self.op(x)], dt), [x], name)
 
@@ -327,14 +338,34 @@ def _layernorm_vjp_in(b: Builder, saved, dy, tag):
     return dx, dg, db
 
 
-def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realize=None) -> tuple:
+def site_keys(s: GptShape, step_key: bytes) -> list:
+    """The keys of the program's dropout sites in slot order, derived from the
+    step's key as 05_gpt.psk splits it: (ke, kb) = split_key(k) in GPT.apply
+    (ke the embedding's); each block of the fold then splits the carried key
+    three times, (katt, k1), (kres, k2), (kff, k3), and carries k3 on."""
+    from . import keys
+    ke, kb = keys.split(step_key, 2)
+    out = [ke]
+    for _ in range(s.L):
+        katt, k1 = keys.split(kb, 2)
+        kres, k2 = keys.split(k1, 2)
+        kff, kb = keys.split(k2, 2)
+        out += [katt, kres, kff]
+    return out
+
+
+def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realize=None, dropout: float = 0.0,
+          step_key: bytes | None = None) -> tuple:
     """The program of config 3 (`train=False`: loss only) or config 4.
     Returns (program, builder, names) with names["loss"] and, for training,
     names["grads"][param] = buffer of its gradient.  `realize`: a
     Realization giving each site its storage type (else `dtype` everywhere);
     parameters are held at rest in its `params` types (else f32) and every
-    kernel reads its inputs converted at its edge."""
-    from . import hip
+    kernel reads its inputs converted at its edge.  `dropout`: the rate of
+    the program's dropout sites (the course's 0.2) with training masks drawn
+    from `step_key` (Key::from_seed(0) by default); 0 leaves them out (x * 1,
+    the configs' reading)."""
+    from . import hip, keys
     tag = dtype if realize is None else "mixed"
     p = Program(f"gpt-{'step' if train else 'forward'}-{tag}", mode=hip.FAST if mode is None else mode)
     b = Builder(p, dtype, realize)
@@ -351,12 +382,23 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
     b.input("scale", A())       # sqrt(HD : R), the attention scores' divisor
     b.input("two", A())         # real(2) of pow(2)'s and sqrt's adjoints
     b.input("one", A())         # the loss's cotangent
+    drop = dropout > 0.0
+    if drop:
+        p.set_keys(site_keys(s, step_key if step_key is not None else keys.from_seed(0)))
     mask = b.causal_mask(s.T, "mask")
     pos_ids = b.positions(s.T, "pos_ids")
     with b.func("Embedding.apply"):
         te = b.embed("tok", "ids", name="te")
         pe = b.embed("pos", pos_ids, name="pe")
         x = b.binary("add", te, pe, name="h0")
+    m_emb = None
+    if drop:
+        # dropout(0.2, ke, h0) = h0 * mask; h0 also gives the mask its shape,
+        # so it reaches memory and the mul is a kernel of its own
+        with b.func("MiniGPT.apply"):
+            m_emb = b.dropout_mask(x, 0, dropout, name="m.emb")
+            x0 = x
+            x = b.binary("mul", x0, m_emb, name="h0d")
     saved = []
     H, HD = s.H, s.HD
     lbl_q = ["batch", "heads", "seq", "hd"]
@@ -375,19 +417,35 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
             sc = b.ein(qh, kh, lbl_q, lbl_k, lbl_s, name=pr + "scores")
             sc2 = b.binary("div", sc, "scale", name=pr + "scaled")
             a = b.masked_softmax(sc2, mask, "seq2", name=pr + "probs")
-            o = b.ein(a, vh, lbl_s, lbl_k, lbl_q, name=pr + "o")
+            ad, ma = a, None
+            if drop:
+                ma = b.dropout_mask(a, 1 + 3 * l, dropout, name=pr + "m.att")
+                ad = b.binary("mul", a, ma, name=pr + "probs_d")
+            o = b.ein(ad, vh, lbl_s, lbl_k, lbl_q, name=pr + "o")
             om = b.merge_heads(o, H, HD, name=pr + "om")
             ao = b.dot(om, pr + "wo", pr + "wo.b", name=pr + "ao")
+        mr = mf = None
         with b.func("Block.apply"):
-            h = b.binary("add", x, ao, name=pr + "h")
+            if drop:
+                # x + dropout(kres, ao): {ao * m, x + .} one group (ao also
+                # shapes the mask, so it reaches memory)
+                mr = b.dropout_mask(ao, 2 + 3 * l, dropout, name=pr + "m.res")
+                h = b.fused([("mul", [("in", 0), ("in", 1)]), ("add", [("in", 2), ("step", 0)])], [ao, mr, x], x, name=pr + "h")
+            else:
+                h = b.binary("add", x, ao, name=pr + "h")
         xn2, ln2 = _layernorm(b, h, pr + "ln2.g", pr + "ln2.b", train, f"b{l}.ln2")
         with b.func("MLP.apply"):
             u = b.dot(xn2, pr + "up", pr + "up.b", name=pr + "u")
             g = b.unary("gelu", u, name=pr + "g")
             dn = b.dot(g, pr + "down", pr + "down.b", name=pr + "dn")
         with b.func("Block.apply"):
-            xo = b.binary("add", h, dn, name=pr + "xo")
-        saved.append(dict(x=x, xn1=xn1, ln1=ln1, qh=qh, kh=kh, vh=vh, a=a, om=om, h=h, xn2=xn2, ln2=ln2, u=u, g=g))
+            if drop:
+                mf = b.dropout_mask(dn, 3 + 3 * l, dropout, name=pr + "m.ff")
+                xo = b.fused([("mul", [("in", 0), ("in", 1)]), ("add", [("in", 2), ("step", 0)])], [dn, mf, h], h, name=pr + "xo")
+            else:
+                xo = b.binary("add", h, dn, name=pr + "xo")
+        saved.append(dict(x=x, xn1=xn1, ln1=ln1, qh=qh, kh=kh, vh=vh, a=a, ad=ad, ma=ma, mr=mr, mf=mf, om=om, h=h,
+                          xn2=xn2, ln2=ln2, u=u, g=g))
         x = xo
     xf, lnf = _layernorm(b, x, "lnf.g", "lnf.b", train, "lnf")
     logits = b.dot(xf, "head", name="logits")
@@ -406,8 +464,8 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
     dx, G["lnf.g"], G["lnf.b"] = _layernorm_vjp(b, lnf, dxf, "lnf")
     for l in reversed(range(s.L)):
         pr, sv = f"b{l}.", saved[l]
-        # xo = h + dn
-        ddn = dx
+        # xo = h + dn (* mf): dn's cotangent is dx (* mf, mul's rule)
+        ddn = dx if sv["mf"] is None else b.binary("mul", dx, sv["mf"])
         with b.func("MLP.apply.vjp"):
             dg_ = b.dot_vjp_l(ddn, pr + "down")
             G[pr + "down"] = b.dot_vjp_r(sv["g"], ddn, name="d." + pr + "down")
@@ -419,15 +477,18 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
         dh_ln, G[pr + "ln2.g"], G[pr + "ln2.b"] = _layernorm_vjp(b, sv["ln2"], dxn2, f"b{l}.ln2")
         with b.func("Block.apply.vjp"):
             dh = b.binary("add", dx, dh_ln)
-        # h = x + ao
-        dao = dh
+        # h = x + ao (* mr)
+        dao = dh if sv["mr"] is None else b.binary("mul", dh, sv["mr"])
         with b.func("SelfAttention.apply.vjp"):
             dom = b.dot_vjp_l(dao, pr + "wo")
             G[pr + "wo"] = b.dot_vjp_r(sv["om"], dao, name="d." + pr + "wo")
             G[pr + "wo.b"] = b.sum_to(dao, pr + "wo.b", name="d." + pr + "wo.b")
             do = b.split_heads(dom, H, HD)
             da = b.ein(do, sv["vh"], lbl_q, lbl_k, lbl_s, like=sv["a"])
-            dvh = b.ein(do, sv["a"], lbl_q, lbl_s, lbl_k, like=sv["vh"])
+            dvh = b.ein(do, sv["ad"], lbl_q, lbl_s, lbl_k, like=sv["vh"])
+            # the dropped weights ad = a * ma: a's cotangent da * ma
+            if sv["ma"] is not None:
+                da = b.binary("mul", da, sv["ma"])
             # softmax: a * (da - broadcast(sum(da * a)))
             t = b.binary("mul", da, sv["a"])
             ssum = b.sum(t, "seq2")
@@ -447,7 +508,10 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
         dx_ln, G[pr + "ln1.g"], G[pr + "ln1.b"] = _layernorm_vjp(b, sv["ln1"], dxn1, f"b{l}.ln1")
         with b.func("Block.apply.vjp"):
             dx = b.binary("add", dh, dx_ln)
-    # h0 = te + pe: te's cotangent dx; pe's sum_to over the batch
+    # h0 = te + pe (* m.emb): te's cotangent dx (* m.emb); pe's sum_to over the batch
+    if m_emb is not None:
+        with b.func("MiniGPT.apply.vjp"):
+            dx = b.binary("mul", dx, m_emb)
     with b.func("Embedding.apply.vjp"):
         G["tok"] = b.embed_vjp("tok", "ids", dx, name="d.tok")
         dpe = b.sum_to(dx, pe)

@@ -79,6 +79,12 @@ class Program:
         # the prepared sequence: ("launch", Launch) and, where a kernel reads a
         # buffer of another storage type, ("convert", src, from, dst, to, n)
         self.steps: list = []
+        # training dropout masks (name, key slot, rate, storage type, count),
+        # drawn on the device from a table of 32-byte keys (set_keys) before
+        # the launches: a mask depends on its key alone
+        self.masks: list = []
+        self.keys: list = []
+        self._keytab = None
 
     def add(self, low: L.Lowered, ins: list, out: str) -> str:
         """Appends one launch of `low` reading buffers `ins`, writing `out`."""
@@ -101,6 +107,32 @@ class Program:
     def declare(self, name: str, ty: str, count: int):
         return self.bufs.alloc(name, ty, count)
 
+    def add_mask(self, name: str, slot: int, rate: float, ty: str, count: int) -> str:
+        """A dropout mask `name` (DropoutMask with training on) drawn from key
+        `slot` of the key table."""
+        self.masks.append((name, slot, float(rate), ty, int(count)))
+        return name
+
+    def set_keys(self, keys: list):
+        """The key table: one 32-byte key per slot.  Copied to the device by
+        prepare(), and at once when the program is already prepared (a
+        recorded graph reads the table at each replay)."""
+        self.keys = [bytes(k) for k in keys]
+        if self._keytab is not None:
+            self._upload_keys()
+
+    def _upload_keys(self):
+        if not self.keys:
+            return
+        if self._keytab is None or self._keytab.nbytes < 32 * len(self.keys):
+            self._keytab = hip.DeviceBuffer(32 * len(self.keys))
+        self._keytab.upload(np.frombuffer(b"".join(self.keys), np.uint8))
+
+    def _key_ptr(self, slot: int) -> int:
+        if self._keytab is None or slot >= len(self.keys):
+            raise ValueError(f"dropout key slot {slot}: no key table (set_keys)")
+        return self._keytab.ptr + 32 * slot
+
     def prepare(self):
         """Allocates every output and builds each launch's pointer table.  A
         kernel that reads a real buffer of another storage type reads it
@@ -110,6 +142,11 @@ class Program:
         values."""
         self.steps = []
         converted = {}
+        if self.masks:
+            self._upload_keys()
+        for name, slot, rate, ty, count in self.masks:
+            self.bufs.alloc(name, ty, count)
+            self.steps.append(("dropout", name, slot, rate, ty, count))
         for ln in self.launches:
             c = ln.compiled
             ty = ln.low.dtype if ln.low.out_kind == "real" else "i64"
@@ -134,6 +171,11 @@ class Program:
         self._flag.zero()
         return self
 
+    def _dropout(self, step, stream=None):
+        _, name, slot, rate, ty, count = step
+        hip.check(hip.lib().presk_hip_dropout_mask(self._key_ptr(slot), rate, ty.encode(), count,
+                                                   self.bufs.dev[name].ptr, stream))
+
     def _convert(self, step, stream=None):
         _, src, frm, dst, to, n = step
         hip.check(hip.lib().presk_hip_convert(self.bufs.dev[src].ptr, frm.encode(), self.bufs.dev[dst].ptr, to.encode(),
@@ -148,6 +190,11 @@ class Program:
         hip.check(lib.presk_hip_batch_create(ctypes.byref(b)))
         self._batch = b
         for st in self.steps:
+            if st[0] == "dropout":
+                _, name, slot, rate, ty, count = st
+                hip.check(lib.presk_hip_batch_add_dropout(b, self._key_ptr(slot), rate, ty.encode(), count,
+                                                          self.bufs.dev[name].ptr))
+                continue
             if st[0] == "convert":
                 _, src, frm, dst, to, n = st
                 hip.check(lib.presk_hip_batch_add_convert(b, self.bufs.dev[src].ptr, frm.encode(), self.bufs.dev[dst].ptr,
@@ -176,6 +223,9 @@ class Program:
             hip.check(lib.presk_hip_batch_run(self._batch, stream))
             return
         for st in self.steps:
+            if st[0] == "dropout":
+                self._dropout(st, stream)
+                continue
             if st[0] == "convert":
                 self._convert(st, stream)
                 continue

@@ -45,6 +45,19 @@ def convert(arr: np.ndarray, frm: str, to: str, n: int):
     return (dst if to == "e8m15" else dst.view(_NP[to])), bool(flag)
 
 
+def dropout_mask(key: bytes, rate: float, ty: str, n: int) -> np.ndarray:
+    """The host's training mask (oracle's po_dropout_mask) in storage form."""
+    import ctypes
+    import os
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(cexec.__file__), "liboracle.so"))
+    f = lib.po_dropout_mask
+    f.argtypes = [ctypes.c_void_p, ctypes.c_double, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]
+    out = np.zeros(max(n, 1) * _WIDTH[ty], np.uint8)
+    f((ctypes.c_uint8 * 32)(*key), rate, _CODES[ty], n, out.ctypes.data)
+    out = out[: n * _WIDTH[ty]]
+    return out if ty == "e8m15" else out.view(_NP[ty])
+
+
 def run(p, host: dict, threads: int = 1, native: bool = False) -> dict:
     """Executes every launch in order, a kernel reading a buffer of another
     storage type reading it converted at its edge (host.rs:793-829); returns
@@ -53,6 +66,10 @@ def run(p, host: dict, threads: int = 1, native: bool = False) -> dict:
     compile_all(p, native=native)
     env = storage_of(host, p)
     types = {}
+    # the training dropout masks, from the program's key table (oracle/rng.c)
+    for name, slot, rate, ty, count in p.masks:
+        env[name] = dropout_mask(p.keys[slot], rate, ty, count)
+        types[name] = ty
     for ln in p.launches:
         for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
             if name in env and name not in types:

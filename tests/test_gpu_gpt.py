@@ -68,3 +68,42 @@ def test_tiny_gpt_step_fast_band(oracle_tiny, dt):
         scale = max(np.max(np.abs(ref)), floor)
         err = np.max(np.abs(got - ref)) / scale
         assert err < (1e-4 if dt == "f32" else 6e-2), (name, err)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_tiny_gpt_step_with_dropout_exact_bits(dt):
+    """the course's dropout 0.2: the masks drawn on the device from the step
+    key's site keys, and every buffer of the step, equal the oracle's"""
+    from presk_amd import keys
+    s = gpt.TINY
+    k = keys.child(keys.from_seed(5), 2)
+    p, b, names = gpt.build(s, dt, train=True, mode=hip.EXACT, dropout=0.2, step_key=k)
+    host = gpt.host_inputs(s)
+    device_run(p, host)
+    q, _, _ = gpt.build(s, dt, train=True, mode=hip.EXACT, dropout=0.2, step_key=k)
+    env = cpu_program.run(q, host)
+    bad = [n for n in [m[0] for m in p.masks] + [ln.out for ln in p.launches]
+           if p.bufs.download(n).tobytes() != env[n].tobytes()]
+    assert not bad, f"{len(bad)} buffers differ, first: {bad[:5]}"
+
+
+def test_dropout_step_graph_takes_each_steps_key():
+    """recorded once as a graph; the host writes the next step's site keys to
+    the device and the replay draws that step's masks"""
+    from presk_amd import keys
+    s = gpt.TINY
+    run_key = keys.from_seed(9)
+    p, b, names = gpt.build(s, "f32", train=True, mode=hip.EXACT, dropout=0.2, step_key=keys.child(run_key, 0))
+    host = gpt.host_inputs(s)
+    p.compile()
+    configs.load_inputs(p, host)
+    p.prepare()
+    p.record(graph=True)
+    for step in (0, 1):
+        p.set_keys(gpt.site_keys(s, keys.child(run_key, step)))
+        p.run()
+        hip.sync()
+        q, _, _ = gpt.build(s, "f32", train=True, mode=hip.EXACT, dropout=0.2, step_key=keys.child(run_key, step))
+        env = cpu_program.run(q, host)
+        for name in [m[0] for m in p.masks] + [names["loss"]]:
+            assert p.bufs.download(name).tobytes() == env[name].tobytes(), (step, name)
