@@ -15,10 +15,15 @@
 // added in increasing split order by a second kernel (deterministic).
 //
 // Workgroup: 256 threads (4 waves as 2x2), tile (2*WM*16) x (2*WN*16), each
-// wave WM x WN MFMA tiles of 16x16.  Operands are staged through LDS
-// k-contiguous, double-buffered (one barrier per k-block); an operand whose
-// contiguous axis is m or n is transposed in registers on its way into LDS
-// (8-byte LDS writes, consecutive lanes along k).
+// wave WM x WN MFMA tiles of 16x16.  Operands are staged through LDS,
+// double-buffered (one barrier per k-block), each as it lies in memory: a
+// k-contiguous operand as [row][k], an m- or n-contiguous one as [k][row]
+// (16-byte writes either way).  MFMA fragments hold consecutive k of one
+// row: read directly from [row][k]; from [k][row] by gfx950's transposing
+// LDS read (ds_read_b64_tr_b16: in each 16-lane group, lane i receives
+// element i % 4 of the 8-byte chunks lanes i/4 + 4j read, so lanes reading
+// k-rows kb + L/4 at columns 4*(L % 4) hand lane i four consecutive k of its
+// column) for 16-bit types, by plain reads for f32 (one k a lane).
 #include <hip/hip_runtime.h>
 
 #include "devfmt.hpp"
@@ -70,13 +75,14 @@ struct Loader {
     typedef typename St<ST>::S S;
     typedef typename St<ST>::V V;
     static constexpr int BK = St<ST>::BK, VEC = St<ST>::VEC, LD = BK + St<ST>::PAD;
-    // KCONTIG: BK/VEC threads per row -> ROWS/(NT/(BK/VEC)) rounds of one vector.
-    // else: VEC rows x 4 k per thread block; (BK/4) k-quads x (ROWS/VEC) row
-    // blocks over NT threads -> rounds.
+    // KCONTIG: the tile is [ROWS][LD], BK/VEC threads per row -> ROWS/(NT/(BK/VEC))
+    // rounds of one vector.  else: the tile is [BK][LDR], ROWS/VEC vectors per
+    // k-row, BK k-rows over NT threads -> rounds.
     static constexpr int TPR = BK / VEC, RPR = NT / TPR, ROUNDS_K = ROWS / RPR;
-    static constexpr int KQ = BK / 4, RB = ROWS / VEC, ROUNDS_T = (KQ * RB + NT - 1) / NT;
-    static constexpr bool PARTIAL_T = (KQ * RB) % NT != 0;  // the last round leaves threads idle
-    static constexpr int NV = KCONTIG ? ROUNDS_K : 4 * ROUNDS_T;
+    static constexpr int LDR = ROWS + 16, VPR = ROWS / VEC, ROUNDS_T = (BK * VPR + NT - 1) / NT;
+    static constexpr bool PARTIAL_T = (BK * VPR) % NT != 0;  // the last round leaves threads idle
+    static constexpr int NV = KCONTIG ? ROUNDS_K : ROUNDS_T;
+    static constexpr int SIZE = KCONTIG ? ROWS * LD : BK * LDR;   // elements of one tile
     V r[NV];
     bool kin[NV];   // the vector's k lies below K; applied when it is stored, so
                     // that no use of the loaded registers waits for the loads
@@ -105,17 +111,13 @@ struct Loader {
         } else {
 #pragma unroll
             for (int q = 0; q < ROUNDS_T; ++q) {
-                const int u = PARTIAL_T && t + q * NT >= KQ * RB ? KQ * RB - 1 : t + q * NT;
-                int row = row0 + (u / KQ) * VEC;
+                const int u = PARTIAL_T && t + q * NT >= BK * VPR ? BK * VPR - 1 : t + q * NT;
+                int row = row0 + (u % VPR) * VEC;
                 row = row + VEC <= rows ? row : rows - VEC;
-                const int kq = k0 + (u % KQ) * 4;
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) {
-                    const int k = kq + kk;
-                    const bool in = k < K;
-                    r[q * 4 + kk] = *(const V*)(p + (long long)(in ? k : K - 1) * ks + row);
-                    kin[q * 4 + kk] = in;
-                }
+                const int k = k0 + u / VPR;
+                const bool in = k < K;
+                r[q] = *(const V*)(p + (long long)(in ? k : K - 1) * ks + row);
+                kin[q] = in;
             }
         }
     }
@@ -138,15 +140,11 @@ struct Loader {
         } else {
 #pragma unroll
             for (int q = 0; q < ROUNDS_T; ++q) {
-                const int u = PARTIAL_T && t + q * NT >= KQ * RB ? KQ * RB - 1 : t + q * NT;
-                const int row = row0 + (u / KQ) * VEC, kq = k0 + (u % KQ) * 4;
-                for (int kk = 0; kk < 4; ++kk) {
-                    for (int j = 0; j < VEC; ++j) {
-                        const int k = kq + kk;
-                        r[q * 4 + kk][j] = (k < K && row + j < rows) ? p[(long long)k * ks + (long long)(row + j) * rs] : (S)0;
-                    }
-                    kin[q * 4 + kk] = true;
-                }
+                const int u = PARTIAL_T && t + q * NT >= BK * VPR ? BK * VPR - 1 : t + q * NT;
+                const int row = row0 + (u % VPR) * VEC, k = k0 + u / VPR;
+                for (int j = 0; j < VEC; ++j)
+                    r[q][j] = (k < K && row + j < rows) ? p[(long long)k * ks + (long long)(row + j) * rs] : (S)0;
+                kin[q] = true;
             }
         }
     }
@@ -161,33 +159,38 @@ struct Loader {
 #pragma unroll
             for (int q = 0; q < ROUNDS_T; ++q) {
                 const int u = t + q * NT;
-                if (PARTIAL_T && u >= KQ * RB) break;  // an idle thread of the last round
-                const int row = (u / KQ) * VEC, kq = (u % KQ) * 4;
-                V z[4];
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) z[kk] = kin[q * 4 + kk] ? r[q * 4 + kk] : V{};
-#pragma unroll
-                for (int j = 0; j < VEC; ++j) {
-                    if (VEC == 8) {
-                        u16x4 w;
-                        w[0] = (unsigned short)z[0][j];
-                        w[1] = (unsigned short)z[1][j];
-                        w[2] = (unsigned short)z[2][j];
-                        w[3] = (unsigned short)z[3][j];
-                        *(u16x4*)(tile + (row + j) * LD + kq) = w;
-                    } else {
-                        f32x4 w;
-                        w[0] = (float)z[0][j];
-                        w[1] = (float)z[1][j];
-                        w[2] = (float)z[2][j];
-                        w[3] = (float)z[3][j];
-                        *(f32x4*)(tile + (row + j) * LD + kq) = w;
-                    }
-                }
+                if (PARTIAL_T && u >= BK * VPR) break;  // an idle thread of the last round
+                *(V*)(tile + (u / VPR) * LDR + (u % VPR) * VEC) = kin[q] ? r[q] : V{};
             }
         }
     }
 };
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// One MFMA operand fragment: k = kk + (lane >> 4) * KPL .. + KPL of row
+// base + (lane & 15), from a tile laid out [row][k] (KC) or [k][row].
+template <int ST, bool KC, int LDX>
+__device__ __forceinline__ typename St<ST>::Frag frag(const typename St<ST>::S* xs, int base, int kk, int lane) {
+    typedef typename St<ST>::Frag Frag;
+    if constexpr (KC) {
+        return *(const Frag*)&xs[(base + (lane & 15)) * LDX + kk + (lane >> 4) * St<ST>::KPL];
+    } else if constexpr (ST == kF32) {
+        return xs[(kk + (lane >> 4)) * LDX + base + (lane & 15)];
+    } else {
+        // two transposing reads of 4 k each: lane L of a 16-lane group reads
+        // k-row kb + L/4 at columns 4*(L % 4); lane i then holds k kb..kb+3
+        // of column base + i
+        const int L = lane & 15, r = kk + 8 * (lane >> 4) + (L >> 2), c = base + 4 * (L & 3);
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(xs + r * LDX + c));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(xs + (r + 4) * LDX + c));
+        Frag f;
+        f[0] = (unsigned short)lo[0]; f[1] = (unsigned short)lo[1]; f[2] = (unsigned short)lo[2]; f[3] = (unsigned short)lo[3];
+        f[4] = (unsigned short)hi[0]; f[5] = (unsigned short)hi[1]; f[6] = (unsigned short)hi[2]; f[7] = (unsigned short)hi[3];
+        return f;
+    }
+}
 
 template <int ST>
 __device__ __forceinline__ f32x4 mfma(typename St<ST>::Frag a, typename St<ST>::Frag b, f32x4 acc);
@@ -263,11 +266,15 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     constexpr int BM = 2 * WM * 16, BN = 2 * WN * 16;
     // LDS: the double-buffered operand tiles, reused by the epilogue for the
     // tile's f32 sums
+    typedef Loader<ST, AK, BM> LA;
+    typedef Loader<ST, BK_, BN> LB;
+    constexpr int ASZ = LA::SIZE, BSZ = LB::SIZE;
+    constexpr int LDA = AK ? LD : LA::LDR, LDB = BK_ ? LD : LB::LDR;
     constexpr int CLD = BN + 4;
-    constexpr int OPER = 2 * (BM + BN) * LD * (int)sizeof(S), CTILE = BM * CLD * 4;
+    constexpr int OPER = 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = BM * CLD * 4;
     __shared__ __attribute__((aligned(16))) char smem[OPER > CTILE ? OPER : CTILE];
     S* const As0 = (S*)smem;
-    S* const Bs0 = As0 + 2 * BM * LD;
+    S* const Bs0 = As0 + 2 * ASZ;
 
     // Work order.  The grid is one line of (split, batch, tile) items.  The
     // hardware deals workgroups to the 8 XCDs round robin (id mod 8).  Without
@@ -313,9 +320,10 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
         for (int j = 0; j < WN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // One k-block ahead: block kt+1 is loaded into registers while block kt
-    // is multiplied out of one LDS buffer, then stored to the other.
-    Loader<ST, AK, BM> la;
-    Loader<ST, BK_, BN> lb;
+    // is multiplied out of one LDS buffer, then stored to the other.  (Two
+    // blocks ahead, a second register set, measured no faster.)
+    LA la;
+    LB lb;
     const int nk = (kend - kbeg + BK - 1) / BK;
     auto fetch = [&](int k0) {
         if (SAFE) {
@@ -332,27 +340,26 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
         lb.store(Bs0);
     }
     __syncthreads();
-    const int frow = lane & 15, fk = (lane >> 4) * KPL;
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < nk) fetch(kbeg + (kt + 1) * BK);
-        const S* as = As0 + cur * BM * LD;
-        const S* bs = Bs0 + cur * BN * LD;
+        const S* as = As0 + cur * ASZ;
+        const S* bs = Bs0 + cur * BSZ;
 #pragma unroll
         for (int kk = 0; kk < BK; kk += KSTEP) {
             Frag a[WM], b[WN];
 #pragma unroll
-            for (int i = 0; i < WM; ++i) a[i] = *(const Frag*)&as[(wm + i * 16 + frow) * LD + kk + fk];
+            for (int i = 0; i < WM; ++i) a[i] = frag<ST, AK, LDA>(as, wm + i * 16, kk, lane);
 #pragma unroll
-            for (int j = 0; j < WN; ++j) b[j] = *(const Frag*)&bs[(wn + j * 16 + frow) * LD + kk + fk];
+            for (int j = 0; j < WN; ++j) b[j] = frag<ST, BK_, LDB>(bs, wn + j * 16, kk, lane);
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
                 for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
         }
         if (kt + 1 < nk) {
-            la.store(As0 + (cur ^ 1) * BM * LD);
-            lb.store(Bs0 + (cur ^ 1) * BN * LD);
+            la.store(As0 + (cur ^ 1) * ASZ);
+            lb.store(Bs0 + (cur ^ 1) * BSZ);
         }
         __syncthreads();
     }
