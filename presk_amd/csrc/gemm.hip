@@ -23,7 +23,10 @@
 // LDS read (ds_read_b64_tr_b16: in each 16-lane group, lane i receives
 // element i % 4 of the 8-byte chunks lanes i/4 + 4j read, so lanes reading
 // k-rows kb + L/4 at columns 4*(L % 4) hand lane i four consecutive k of its
-// column) for 16-bit types, by plain reads for f32 (one k a lane).
+// column) for 16-bit types, by plain reads for f32 (one k a lane).  f32
+// operands of whole k-blocks and aligned vectors skip the registers: each
+// lane's 16 bytes go from global memory straight into an XOR-swizzled LDS
+// tile (global_load_lds_dwordx4), the same products in the same order.
 #include <hip/hip_runtime.h>
 
 #include "devfmt.hpp"
@@ -166,6 +169,63 @@ struct Loader {
     }
 };
 
+// f32 operand tiles loaded straight into LDS (global_load_lds_dwordx4: lane
+// i of a wave's load writes bytes [16 i, 16 i + 16) of the wave's 1 KB LDS
+// segment, from any global address it names), so that no register, wait or
+// LDS write stands between the loads and the products.  No padding: 16-byte
+// chunks are placed by an XOR swizzle that keeps the fragment reads free of
+// bank conflicts (per 32 lanes, 32 distinct banks):
+//   k-contiguous, [row][32 k]: chunk (r, kc) at slot r*8 + (kc ^ (r & 7))
+//   m/n-contiguous, [k][ROWS]: chunk (k, cc) at slot k*(ROWS/4) + (cc ^ 4*(k & 1))
+// Rows past the operand read its last row (their results are never stored).
+// Nothing zeroes a k past K, so the launcher takes this path only when every
+// k-block is whole (K % 32 == 0) and the operands hold aligned 16-byte
+// vectors along their loaded axis.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+template <bool KCONTIG, int ROWS>
+struct DLoader {
+    static constexpr int BK = 32, CPR = ROWS / 4;     // CPR: chunks per k-row of [k][ROWS]
+    static constexpr int ROUNDS = ROWS * 8 / NT;      // chunks per thread
+    static constexpr int SIZE = ROWS * BK;            // floats of one tile
+    static_assert(ROWS * 8 % NT == 0, "whole rounds");
+    __device__ __forceinline__ void load(const float* __restrict__ p, int rows, int rs, int ks, int row0, int k0,
+                                         float* tile) const {
+        const int t = threadIdx.x, wbase = t & ~63;
+#pragma unroll
+        for (int q = 0; q < ROUNDS; ++q) {
+            const int slot = q * NT + t;
+            const float* src;
+            if (KCONTIG) {
+                const int r = slot >> 3, kc = (slot & 7) ^ (r & 7);
+                int row = row0 + r;
+                row = row < rows ? row : rows - 1;
+                src = p + (long long)row * rs + k0 + kc * 4;
+            } else {
+                const int k = slot / CPR, cc = (slot % CPR) ^ ((k & 1) * 4);
+                int row = row0 + cc * 4;
+                row = row + 4 <= rows ? row : rows - 4;
+                src = p + (long long)(k0 + k) * ks + row;
+            }
+            // the wave's segment starts at its first slot; lane i fills slot + i
+            __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(tile + (q * NT + wbase) * 4), 16, 0, 0);
+        }
+    }
+};
+
+// f32 fragment (k = kk + (lane >> 4) of row base + (lane & 15)) from a swizzled tile
+template <bool KC, int ROWS>
+__device__ __forceinline__ float frag_dl(const float* xs, int base, int kk, int lane) {
+    if constexpr (KC) {
+        const int r = base + (lane & 15);
+        return xs[r * 32 + (((kk >> 2) ^ (r & 7)) << 2) + (lane >> 4)];
+    } else {
+        const int k = kk + (lane >> 4), c = base + (lane & 15);
+        return xs[k * ROWS + (((c >> 2) ^ ((k & 1) * 4)) << 2) + (c & 3)];
+    }
+}
+
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 // One MFMA operand fragment: k = kk + (lane >> 4) * KPL .. + KPL of row
@@ -258,8 +318,9 @@ __device__ __forceinline__ float load_bias(const void* p, long long off) {
     return pk_f16_to_f32(((const unsigned short*)p)[off]);
 }
 
-template <int ST, bool AK, bool BK_, int WM, int WN, bool SAFE>
+template <int ST, bool AK, bool BK_, int WM, int WN, bool SAFE, bool DL>
 __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
+    static_assert(!DL || (ST == kF32 && !SAFE), "direct loads: f32 with whole vectors");
     typedef typename St<ST>::S S;
     typedef typename St<ST>::Frag Frag;
     constexpr int BK = St<ST>::BK, LD = BK + St<ST>::PAD, KSTEP = St<ST>::KSTEP, KPL = St<ST>::KPL;
@@ -268,7 +329,9 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     // tile's f32 sums
     typedef Loader<ST, AK, BM> LA;
     typedef Loader<ST, BK_, BN> LB;
-    constexpr int ASZ = LA::SIZE, BSZ = LB::SIZE;
+    typedef DLoader<AK, BM> DA;
+    typedef DLoader<BK_, BN> DB;
+    constexpr int ASZ = DL ? DA::SIZE : LA::SIZE, BSZ = DL ? DB::SIZE : LB::SIZE;
     constexpr int LDA = AK ? LD : LA::LDR, LDB = BK_ ? LD : LB::LDR;
     constexpr int CLD = BN + 4;
     constexpr int OPER = 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = BM * CLD * 4;
@@ -319,49 +382,84 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < WN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // One k-block ahead: block kt+1 is loaded into registers while block kt
-    // is multiplied out of one LDS buffer, then stored to the other.  (Two
-    // blocks ahead, a second register set, measured no faster.)
-    LA la;
-    LB lb;
     const int nk = (kend - kbeg + BK - 1) / BK;
-    auto fetch = [&](int k0) {
-        if (SAFE) {
-            la.load_checked(A, M, kend, sa_m, sa_k, (int)m0, k0);
-            lb.load_checked(B, N, kend, sb_n, sb_k, (int)n0, k0);
-        } else {
-            la.load(A, M, kend, sa_m, sa_k, (int)m0, k0);
-            lb.load(B, N, kend, sb_n, sb_k, (int)n0, k0);
+    if constexpr (DL) {
+        // One k-block ahead: block kt+1 streams into one LDS buffer while
+        // block kt is multiplied out of the other; a block ends with this
+        // wave's loads complete, then a barrier for every wave's.
+        const DA da{};
+        const DB db{};
+        auto fetch = [&](int k0, int buf) {
+            da.load((const float*)A, M, sa_m, sa_k, (int)m0, k0, (float*)As0 + buf * ASZ);
+            db.load((const float*)B, N, sb_n, sb_k, (int)n0, k0, (float*)Bs0 + buf * BSZ);
+        };
+        if (nk > 0) fetch(kbeg, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+            const int cur = kt & 1;
+            if (kt + 1 < nk) fetch(kbeg + (kt + 1) * BK, cur ^ 1);
+            const float* as = (const float*)As0 + cur * ASZ;
+            const float* bs = (const float*)Bs0 + cur * BSZ;
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += KSTEP) {
+                Frag a[WM], b[WN];
+#pragma unroll
+                for (int i = 0; i < WM; ++i) a[i] = frag_dl<AK, BM>(as, wm + i * 16, kk, lane);
+#pragma unroll
+                for (int j = 0; j < WN; ++j) b[j] = frag_dl<BK_, BN>(bs, wn + j * 16, kk, lane);
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
         }
-    };
-    if (nk > 0) {
-        fetch(kbeg);
-        la.store(As0);
-        lb.store(Bs0);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) fetch(kbeg + (kt + 1) * BK);
-        const S* as = As0 + cur * ASZ;
-        const S* bs = Bs0 + cur * BSZ;
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += KSTEP) {
-            Frag a[WM], b[WN];
-#pragma unroll
-            for (int i = 0; i < WM; ++i) a[i] = frag<ST, AK, LDA>(as, wm + i * 16, kk, lane);
-#pragma unroll
-            for (int j = 0; j < WN; ++j) b[j] = frag<ST, BK_, LDB>(bs, wn + j * 16, kk, lane);
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
-        }
-        if (kt + 1 < nk) {
-            la.store(As0 + (cur ^ 1) * ASZ);
-            lb.store(Bs0 + (cur ^ 1) * BSZ);
+    } else {
+        // One k-block ahead: block kt+1 is loaded into registers while block kt
+        // is multiplied out of one LDS buffer, then stored to the other.  (Two
+        // blocks ahead, a second register set, measured no faster.)
+        LA la;
+        LB lb;
+        auto fetch = [&](int k0) {
+            if (SAFE) {
+                la.load_checked(A, M, kend, sa_m, sa_k, (int)m0, k0);
+                lb.load_checked(B, N, kend, sb_n, sb_k, (int)n0, k0);
+            } else {
+                la.load(A, M, kend, sa_m, sa_k, (int)m0, k0);
+                lb.load(B, N, kend, sb_n, sb_k, (int)n0, k0);
+            }
+        };
+        if (nk > 0) {
+            fetch(kbeg);
+            la.store(As0);
+            lb.store(Bs0);
         }
         __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+            const int cur = kt & 1;
+            if (kt + 1 < nk) fetch(kbeg + (kt + 1) * BK);
+            const S* as = As0 + cur * ASZ;
+            const S* bs = Bs0 + cur * BSZ;
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += KSTEP) {
+                Frag a[WM], b[WN];
+#pragma unroll
+                for (int i = 0; i < WM; ++i) a[i] = frag<ST, AK, LDA>(as, wm + i * 16, kk, lane);
+#pragma unroll
+                for (int j = 0; j < WN; ++j) b[j] = frag<ST, BK_, LDB>(bs, wn + j * 16, kk, lane);
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
+            }
+            if (kt + 1 < nk) {
+                la.store(As0 + (cur ^ 1) * ASZ);
+                lb.store(Bs0 + (cur ^ 1) * BSZ);
+            }
+            __syncthreads();
+        }
     }
 
     // The tile's sums go through LDS (lane holds column lane & 15, rows
@@ -461,16 +559,16 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
 
-template <int ST, int WM, int WN, bool SAFE>
+template <int ST, int WM, int WN, bool SAFE, bool DL = false>
 hipError_t launch_shape(const GemmArgs& g, hipStream_t stream) {
     const long long items = (long long)g.tiles_m * g.tiles_n * g.batch * g.splits;
     if (items <= 0) return hipSuccess;
     if (items > 0x7fffffffLL) return hipErrorInvalidValue;
     dim3 grid((unsigned)items, 1, 1);
-    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
-    else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
-    else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
-    else gemm_kernel<ST, false, false, WM, WN, SAFE><<<grid, NT, 0, stream>>>(g);
+    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
+    else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
+    else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
+    else gemm_kernel<ST, false, false, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
     return hipGetLastError();
 }
 
@@ -480,9 +578,18 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     // contiguous, else the rows) to hold whole aligned vectors
     const bool fast = g.a_vec && g.b_vec;
     hipError_t e;
-    if (g.bn == 96) e = fast ? launch_shape<ST, 4, 3, false>(g, stream) : launch_shape<ST, 4, 3, true>(g, stream);
-    else if (g.bn == 64) e = fast ? launch_shape<ST, 4, 2, false>(g, stream) : launch_shape<ST, 4, 2, true>(g, stream);
-    else e = fast ? launch_shape<ST, 4, 4, false>(g, stream) : launch_shape<ST, 4, 4, true>(g, stream);
+    if (ST == kF32 && fast && g.K % St<kF32>::BK == 0) {
+        // whole k-blocks of whole vectors: the f32 tiles load straight into LDS
+        if (g.bn == 96) e = launch_shape<ST, 4, 3, false, ST == kF32>(g, stream);
+        else if (g.bn == 64) e = launch_shape<ST, 4, 2, false, ST == kF32>(g, stream);
+        else e = launch_shape<ST, 4, 4, false, ST == kF32>(g, stream);
+    } else if (g.bn == 96) {
+        e = fast ? launch_shape<ST, 4, 3, false>(g, stream) : launch_shape<ST, 4, 3, true>(g, stream);
+    } else if (g.bn == 64) {
+        e = fast ? launch_shape<ST, 4, 2, false>(g, stream) : launch_shape<ST, 4, 2, true>(g, stream);
+    } else {
+        e = fast ? launch_shape<ST, 4, 4, false>(g, stream) : launch_shape<ST, 4, 4, true>(g, stream);
+    }
     if (e != hipSuccess || g.splits <= 1) return e;
     const long long n = g.M * g.N;
     split_reduce_kernel<ST><<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(g);

@@ -50,30 +50,41 @@ __global__ void __launch_bounds__(64) colsum_chunks(ColSumArgs a) {
     a.work[ch * a.cols + col] = part;
 }
 
-// the chunk sums added in chunk order from zero, then one store: four waves
-// stage SEG chunk sums of 64 columns in LDS, lane c of wave 0 adds them in order
-constexpr int SEG = 128;
+// the chunk sums added in chunk order from zero, then one store: sixteen
+// waves stage SEG chunk sums of 64 columns in LDS (SEG/16 loads a lane, all
+// in flight), lane c of wave 0 adds them in order, reading LDS 32 at a time
+// so the chain of adds waits on one LDS round trip per 32
+constexpr int SEG = 256, TW = 16, BATCH = 32;
 
 template <int ST>
-__global__ void __launch_bounds__(256) colsum_total(ColSumArgs a) {
-    __shared__ float part[SEG][65];
+__global__ void __launch_bounds__(TW * 64) colsum_total(ColSumArgs a) {
+    __shared__ float part[SEG][64];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long long col = (long long)blockIdx.x * 64 + lane;
     const bool live = col < a.cols;
     float acc = 0.f;
     for (long long c0 = 0; c0 < a.nchunks; c0 += SEG) {
         const int n = (int)(a.nchunks - c0 < SEG ? a.nchunks - c0 : SEG);
-        float v[SEG / 4];
+        float v[SEG / TW];
 #pragma unroll
-        for (int i = 0; i < SEG / 4; ++i) {
-            const int c = i * 4 + w;
+        for (int i = 0; i < SEG / TW; ++i) {
+            const int c = i * TW + w;
             v[i] = live && c < n ? a.work[(c0 + c) * a.cols + col] : 0.f;
         }
 #pragma unroll
-        for (int i = 0; i < SEG / 4; ++i) part[i * 4 + w][lane] = v[i];
+        for (int i = 0; i < SEG / TW; ++i) part[i * TW + w][lane] = v[i];
         __syncthreads();
-        if (w == 0)
-            for (int c = 0; c < n; ++c) acc = acc + part[c][lane];
+        if (w == 0) {
+            int c = 0;
+            for (; c + BATCH <= n; c += BATCH) {
+                float t[BATCH];
+#pragma unroll
+                for (int i = 0; i < BATCH; ++i) t[i] = part[c + i][lane];
+#pragma unroll
+                for (int i = 0; i < BATCH; ++i) acc = acc + t[i];
+            }
+            for (; c < n; ++c) acc = acc + part[c][lane];
+        }
         __syncthreads();
     }
     if (w != 0 || !live) return;
@@ -104,9 +115,9 @@ hipError_t colsum_launch(const ColSumArgs& a, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     switch (a.storage) {
-        case 0: colsum_total<0><<<bx, 256, 0, stream>>>(a); break;
-        case 1: colsum_total<1><<<bx, 256, 0, stream>>>(a); break;
-        case 2: colsum_total<2><<<bx, 256, 0, stream>>>(a); break;
+        case 0: colsum_total<0><<<bx, TW * 64, 0, stream>>>(a); break;
+        case 1: colsum_total<1><<<bx, TW * 64, 0, stream>>>(a); break;
+        case 2: colsum_total<2><<<bx, TW * 64, 0, stream>>>(a); break;
     }
     return hipGetLastError();
 }

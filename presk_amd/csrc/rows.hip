@@ -775,6 +775,10 @@ hipError_t launch_walk(const RowArgs& a, hipStream_t stream) {
     }
 }
 
+// softmax rows that fit in registers but are many and of whole 64-column
+// chunks take the streamed kernel as well (aligned buffers permitting)
+bool streams_short(const RowArgs& a) { return a.n % SCW == 0 && a.rows >= 8192; }
+
 // the long-row walk serves these nests when their rows do not fit in registers
 constexpr bool walks(int op) {
     return op == kRowMean || op == kRowSum || op == kSumToRows || op == kSoftmax3 || op == kSoftmax2 ||
@@ -809,6 +813,12 @@ hipError_t launch_op(const RowArgs& a, hipStream_t stream) {
     if constexpr (walks(OP)) {
         if (!res) return launch_walk<OP>(a, stream);
     }
+    if constexpr (OP == kSoftmax3 || OP == kSoftmax2 || OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2) {
+        // short rows of whole 64-column chunks on aligned buffers stream too:
+        // 16-byte loads and the mask as bits beat the register-resident rows
+        if (streams_short(a) && (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.out % 16 == 0)
+            return launch_walk<OP>(a, stream);
+    }
     if (a.rows >= 8192)
         return res ? launch_r<OP, 16, true>(a, stream) : launch_r<OP, 16, false>(a, stream);
     return res ? launch_r<OP, 4, true>(a, stream) : launch_r<OP, 4, false>(a, stream);
@@ -819,7 +829,8 @@ hipError_t launch_op(const RowArgs& a, hipStream_t stream) {
 long long rows_mask_words(long long n) { return mask_words(n); }
 
 bool rows_need_mask_bits(const RowArgs& a) {
-    return (a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2) && a.rows > 0 && a.n > NRES * CW;
+    return (a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2) && a.rows > 0 &&
+           (a.n > NRES * CW || streams_short(a));
 }
 
 hipError_t rows_launch(const RowArgs& a, hipStream_t stream) {

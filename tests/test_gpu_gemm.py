@@ -33,6 +33,11 @@ def cases():
         out.append((f"dot+add-{dt}", L.dot([x, w, O(A(136))], dt, epilogue=(True, d.out_axes)), None))
         out.append((f"dot_vjp_l-{dt}", L.dot_vjp_l([O(A(("batch", 2), ("seq", 130), 200)), O(A(72, 200))], dt), None))
         out.append((f"dot_vjp_r-split-{dt}", L.dot_vjp_r([O(A(("batch", 4), ("seq", 600), 96)), O(A(("batch", 4), ("seq", 600), 80))], dt), None))
+        # whole k-blocks (f32 tiles then load straight into LDS): both operands
+        # k-contiguous with rows past a tile, and an m-contiguous operand of
+        # 100 rows whose last vectors are clamped
+        out.append((f"dot_vjp_l-k192-{dt}", L.dot_vjp_l([O(A(("batch", 2), ("seq", 130), 192)), O(A(72, 192))], dt), None))
+        out.append((f"dot_vjp_r-m100-{dt}", L.dot_vjp_r([O(A(("batch", 4), ("seq", 600), 100)), O(A(("batch", 4), ("seq", 600), 76))], dt), None))
         q = O(A(("batch", 2), ("heads", 3), ("seq", 40), ("hd", 64)))
         kk = O(A(("batch", 2), ("heads", 3), ("seq2", 40), ("hd", 64)))
         s = O(A(("batch", 2), ("heads", 3), ("seq", 40), ("seq2", 40)))

@@ -34,8 +34,10 @@ def chunked_colsum_text(rows, cols, dtype, chunk=64):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("shape", [(4, 300, 40), (64, 256, 384)])
+@pytest.mark.parametrize("shape", [(4, 300, 40), (64, 256, 384), (3, 5700, 70)])
 def test_fast_sum_to_is_chunked_order(dt, shape):
+    """one segment of chunk sums (19, 256 chunks) and two (268: a part
+    chunk, a part column block, a second segment shorter than a batch)"""
     B, T, D = shape
     x = O(A(("batch", B), ("seq", T), ("model", D)))
     low = L.sum_to([x, O(A(("model", D)))], dt)
@@ -157,13 +159,15 @@ def _same_bits_nan_as_nan(got, want, dt):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("T", [40, 300])
+@pytest.mark.parametrize("T", [40, 256, 300])
 def test_rows_class_nan_and_empty_rows(dt, T):
     """the masked max's corner cases: a NaN first allowed element (the max is
     NaN), a NaN later allowed element and a NaN disallowed one (both passed
     over), -inf first, and a row the mask allows nowhere (all zeros); rows
-    that stay in registers (40) and rows the long-row walk streams (300)"""
-    B, H = 2, 3
+    that stay in registers (40), short rows of whole 64-column chunks that
+    are many enough to stream (256, 8192 rows) and rows the long-row walk
+    streams (300)"""
+    B, H = 2, (16 if T == 256 else 3)
     s = O(A(("batch", B), ("heads", H), ("seq", T), ("seq2", T)))
     mask = O(A(("seq", T), ("seq2", T)), "idx")
     ex = hip.HipExec(0, mode=hip.EXACT)
