@@ -136,6 +136,23 @@ int presk_hip_time(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int
 int presk_hip_convert(const void *src, const char *from, void *dst, const char *to, int64_t n, uint32_t *flag,
                       void *stream);
 
+/* One leaf of a `.psk.d` file decoded on the device, replacing the reader's
+ * per-element Enc::decode (crates/presk-data/src/lib.rs:205-219, called from
+ * `decode`, lib.rs:816-843) followed by Buf::of into the storage type.  `src`
+ * holds the leaf's n elements as the file stores them (copied to device
+ * memory); `enc` is the header's code: 0 f64, 1 f32, 2 bf16, 3 a format given
+ * by its parameters, whose six header bytes `desc` points to (host memory;
+ * Enc::of_description, lib.rs:143-166).  Each element is the exact f64 its
+ * code denotes (Float::decode, crates/presk-format/src/lib.rs:460-476), stored
+ * as type `to` stores an f64 (as presk_hip_convert does, overflow guard
+ * included).  A description that is no format fails with E9002. */
+int presk_hip_pskd_decode(const void *src, int enc, const uint8_t *desc, int64_t n, void *dst, const char *to,
+                          uint32_t *flag, void *stream);
+/* An `idx[bound]` leaf: n elements of the smallest unsigned integer holding
+ * bound-1 (idx_width, crates/presk-data/src/lib.rs:289-296), little-endian,
+ * widened to i64 at dst. */
+int presk_hip_pskd_decode_idx(const void *src, uint64_t bound, int64_t n, int64_t *dst, void *stream);
+
 /* A recorded launch sequence: a function body's kernels in the order the
  * host's call loop issues them (crates/presk-kernel/src/host.rs:887-1030 runs
  * each `let` of the body as one or more launches through `KernelExec::run`).

@@ -85,3 +85,83 @@ uint32_t po_convert(void *dst, int to, const void *src, int from, size_t n)
     }
     return o;
 }
+
+/* ---- .psk.d leaves (crates/presk-data/src/lib.rs:205-219, Enc::decode) ----
+ * A code of a float format given by its parameters is the f64 it denotes
+ * (crates/presk-format/src/lib.rs:460-476, Float::decode): sign, exponent
+ * field biased by 1 - emin, p - 1 trailing bits; the top field holds the
+ * infinities and NaNs (IEEE) or only the NaN of the top trailing code (NaN
+ * only); field 0 the subnormals or, without them, zero.  exp2 is exact
+ * (lib.rs:170-176).  Pinned by tests/test_oracle_pskd.py: binary16 against
+ * numpy over every code, the reference's own E4M3 codes of 480, -0.375, 2^-9
+ * and -0 (crates/presk-data/tests/data.rs:235-236), E2M1's eight magnitudes
+ * from its definition, bf16 and f32 against their bit layouts. */
+static double po_exp2i(int k)
+{
+    uint64_t b = k >= -1022 ? (uint64_t)(k + 1023) << 52 : 1ull << (k + 1074);
+    double x;
+    memcpy(&x, &b, 8);
+    return x;
+}
+
+double po_format_decode(uint64_t code, int p, int emin, int emax, int subnormals, int specials)
+{
+    const int t = p - 1;
+    const uint64_t ncodes = (uint64_t)(emax - emin + 2) + (specials == 0 ? 1 : 0);
+    int ebits = 0;
+    while ((1ull << ebits) < ncodes) ebits++;
+    const int bits = 1 + ebits + t;
+    const int negative = (int)((code >> (bits - 1)) & 1);
+    const uint64_t top = (1ull << ebits) - 1, tmask = (1ull << t) - 1;
+    const uint64_t field = (code >> t) & top, trailing = code & tmask;
+    double v;
+    uint64_t nan = 0x7ff8000000000000ull;
+    if (specials == 0 && field == top) {
+        if (trailing == 0) v = INFINITY;
+        else memcpy(&v, &nan, 8);
+    } else if (specials == 1 && field == top && trailing == tmask) {
+        memcpy(&v, &nan, 8);
+    } else if (field == 0) {
+        v = subnormals ? (double)trailing * po_exp2i(emin - t) : 0.0;
+    } else {
+        v = (double)((1ull << t) | trailing) * po_exp2i((int)field - (1 - emin) - t);
+    }
+    if (negative) {
+        uint64_t b;
+        memcpy(&b, &v, 8);
+        b ^= 0x8000000000000000ull;
+        memcpy(&v, &b, 8);
+    }
+    return v;
+}
+
+/* n elements of a real leaf: enc 0 f64, 1 f32, 2 bf16 (the conversion from
+ * that type), 3 codes of `width` bytes of the format (p, emin, emax,
+ * subnormals, specials); stored as `to` stores an f64.  Returns the guard. */
+uint32_t po_pskd_decode(void *dst, int to, const void *src, int enc, int width, int p, int emin, int emax,
+                        int subnormals, int specials, size_t n)
+{
+    if (enc != 3) return po_convert(dst, to, src, enc, n);
+    const unsigned char *b = (const unsigned char *)src;
+    uint32_t o = 0;
+    for (size_t i = 0; i < n; i++) {
+        uint64_t code = 0;
+        for (int k = 0; k < width; k++) code |= (uint64_t)b[i * width + k] << (8 * k);
+        const double x = po_format_decode(code, p, emin, emax, subnormals, specials);
+        if (to == 4) o |= (uint32_t)oc_overflows_f16(x);
+        if (to == 5) o |= (uint32_t)oc_overflows_e8m15(x);
+        store_f64(dst, to, i, x);
+    }
+    return o;
+}
+
+/* n elements of an idx leaf of `width` bytes, little-endian, as i64 */
+void po_pskd_idx(int64_t *dst, const void *src, int width, size_t n)
+{
+    const unsigned char *b = (const unsigned char *)src;
+    for (size_t i = 0; i < n; i++) {
+        uint64_t v = 0;
+        for (int k = 0; k < width; k++) v |= (uint64_t)b[i * width + k] << (8 * k);
+        dst[i] = (int64_t)v;
+    }
+}

@@ -124,6 +124,55 @@ hipError_t launch_from(int to, const void* src, void* dst, long long n, unsigned
 size_t width(int t) { return t == 0 ? 8 : t == 1 ? 4 : (t == 2 || t == 4) ? 2 : t == 5 ? 3 : 0; }
 
 
+// ---- .psk.d leaves (crates/presk-data/src/lib.rs:205-219, Enc::decode) ------
+// A real leaf's elements are codes of its encoding: f64, f32 and bf16 are the
+// conversions above; a format given by its parameters (encoding 3) is decoded
+// to the f64 it denotes (crates/presk-format/src/lib.rs:460-476,
+// Float::decode), exactly, then stored as Buf::of stores an f64.  Codes are
+// `width` bytes, little-endian; bits above the format's are ignored.
+__device__ __forceinline__ double exp2i(int k) {
+    return k >= -1022 ? from_bits64((unsigned long long)(k + 1023) << 52) : from_bits64(1ull << (k + 1074));
+}
+
+__device__ __forceinline__ double format_decode(unsigned long long code, const PskFormat& f) {
+    const int t = f.p - 1;
+    const bool negative = (code >> (f.bits - 1)) & 1ull;
+    const unsigned long long top = (1ull << f.ebits) - 1, tmask = (1ull << t) - 1;
+    const unsigned long long field = (code >> t) & top, trailing = code & tmask;
+    double v;
+    if (f.specials == 0 && field == top) v = trailing == 0 ? __builtin_inf() : from_bits64(0x7ff8000000000000ull);
+    else if (f.specials == 1 && field == top && trailing == tmask) v = from_bits64(0x7ff8000000000000ull);
+    else if (field == 0) v = f.subnormals ? (double)trailing * exp2i(f.emin - t) : 0.0;
+    else v = (double)((1ull << t) | trailing) * exp2i((int)field - (1 - f.emin) - t);
+    // negation flips the sign bit, a NaN's included
+    return negative ? from_bits64(bits64(v) ^ 0x8000000000000000ull) : v;
+}
+
+template <int T>
+__global__ void __launch_bounds__(256) format_decode_kernel(const unsigned char* src, PskFormat f, long long n, void* dst,
+                                                            unsigned* flag) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    unsigned long long code = 0;
+    for (int b = 0; b < f.width; ++b) code |= (unsigned long long)src[i * f.width + b] << (8 * b);
+    const double x = format_decode(code, f);
+    if (T == 4 || T == 5) {
+        const double a = x < 0 ? -x : x;
+        const double threshold = T == 4 ? 65520.0 : 0x1.ffffp127;
+        if (a == a && a != __builtin_inf() && a >= threshold && flag) atomicOr(flag, 1u);
+    }
+    store_f64<T>(dst, i, x);
+}
+
+// an idx[N] leaf: the smallest unsigned integer holding N-1, widened to i64
+__global__ void __launch_bounds__(256) idx_widen_kernel(const unsigned char* src, int width, long long n, long long* dst) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    unsigned long long v = 0;
+    for (int b = 0; b < width; ++b) v |= (unsigned long long)src[i * width + b] << (8 * b);
+    dst[i] = (long long)v;
+}
+
 // ---- dropout masks (crates/presk-kernel/src/host.rs:1893-1926) ----------------
 // Element e is 1/(1-rate) where the key's e-th uniform draw is below 1-rate,
 // else 0, stored as Buf::of stores it (store_f64).  The draw is rand_chacha's
@@ -197,6 +246,31 @@ hipError_t convert_launch(const void* src, int from, void* dst, int to, long lon
         case 5: return launch_from<5>(to, src, dst, n, flag, s);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t pskd_decode_launch(const void* src, int enc, const PskFormat& f, long long n, void* dst, int to, unsigned* flag,
+                              hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (enc == 0 || enc == 1 || enc == 2) return convert_launch(src, enc, dst, to, n, flag, s);
+    if (enc != 3 || (n + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    const unsigned char* b = (const unsigned char*)src;
+    switch (to) {
+        case 0: format_decode_kernel<0><<<grid, 256, 0, s>>>(b, f, n, dst, flag); break;
+        case 1: format_decode_kernel<1><<<grid, 256, 0, s>>>(b, f, n, dst, flag); break;
+        case 2: format_decode_kernel<2><<<grid, 256, 0, s>>>(b, f, n, dst, flag); break;
+        case 4: format_decode_kernel<4><<<grid, 256, 0, s>>>(b, f, n, dst, flag); break;
+        case 5: format_decode_kernel<5><<<grid, 256, 0, s>>>(b, f, n, dst, flag); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t pskd_idx_launch(const void* src, int width, long long n, long long* dst, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if ((n + 255) / 256 > 0x7fffffffLL || !(width == 1 || width == 2 || width == 4 || width == 8)) return hipErrorInvalidValue;
+    idx_widen_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>((const unsigned char*)src, width, n, dst);
+    return hipGetLastError();
 }
 
 hipError_t dropout_launch(const void* key, double rate, int type, long long n, void* dst, hipStream_t s) {

@@ -542,6 +542,68 @@ int presk_hip_fill_normal(void* dst, const char* type, int64_t n, uint64_t seed,
     return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "fill");
 }
 
+}  // extern "C"
+
+namespace {
+
+// A version 3 header's six bytes as a format (crates/presk-data/src/lib.rs:143-166,
+// Enc::of_description), refused unless it is one (presk-format lib.rs:220-240,
+// Float::check); "" when it is, else why not.
+std::string psk_format(const uint8_t* d, PskFormat* f) {
+    const unsigned flags = d[5];
+    const int specials = (int)(flags >> 1 & 3), overflow = (int)(flags >> 3 & 3);
+    if (specials > 2) return "special values " + std::to_string(specials);
+    if (overflow > 2) return "overflow " + std::to_string(overflow);
+    if (flags >> 7) return "flags " + std::to_string(flags);
+    f->p = d[0];
+    f->emin = (int16_t)(d[1] | d[2] << 8);
+    f->emax = (int16_t)(d[3] | d[4] << 8);
+    f->subnormals = flags & 1;
+    f->specials = specials;
+    const bool default_nan = flags & 64;
+    if (f->p < 2 || f->p > 53) return "a float format has 2 to 53 bits of significand, not " + std::to_string(f->p);
+    if (f->emin > f->emax || f->emin < -1022 || f->emax > 1023) return "the exponent range is not inside f64's";
+    const unsigned long long codes = (unsigned long long)(f->emax - f->emin + 2) + (specials == 0 ? 1 : 0);
+    if (codes & (codes - 1)) return "the exponent range does not fill an exponent field";
+    if (default_nan && specials == 2) return "a format with no NaN gives no default NaN";
+    // (specials, overflow): IEEE any; NaN only -> NaN or saturation; none -> saturation
+    if ((specials == 1 && overflow == 0) || (specials == 2 && overflow != 2)) return "an overflow its special values do not allow";
+    f->ebits = __builtin_ctzll(codes);
+    f->bits = 1 + f->ebits + f->p - 1;
+    f->width = (f->bits + 7) / 8;
+    return "";
+}
+
+}  // namespace
+
+extern "C" {
+
+int presk_hip_pskd_decode(const void* src, int enc, const uint8_t* desc, int64_t n, void* dst, const char* to, uint32_t* flag,
+                          void* stream) {
+    const int t = convert_type(to);
+    if (t < 0) return fail(PRESK_HIP_ERR, "E10001: a .psk.d leaf decoded into `" + std::string(to ? to : "") + "`, not a storage type");
+    if (n < 0 || (n > 0 && (!src || !dst))) return fail(PRESK_HIP_ERR, "E10001: bad decode arguments");
+    PskFormat f{};
+    if (enc == 3) {
+        if (!desc) return fail(PRESK_HIP_ERR, "E10001: encoding 3 needs its format's description");
+        const std::string why = psk_format(desc, &f);
+        if (!why.empty()) return fail(PRESK_HIP_ERR, "E9002: a format the encoding does not describe (" + why + ")");
+    } else if (enc < 0 || enc > 2) {
+        return fail(PRESK_HIP_ERR, "E9002: unknown encoding " + std::to_string(enc));
+    }
+    hipError_t e = pskd_decode_launch(src, enc, f, n, dst, t, flag, (hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, ".psk.d decode");
+}
+
+int presk_hip_pskd_decode_idx(const void* src, uint64_t bound, int64_t n, int64_t* dst, void* stream) {
+    if (bound == 0) return fail(PRESK_HIP_ERR, "E9001: an `idx[0]` has no values");
+    if (n < 0 || (n > 0 && (!src || !dst))) return fail(PRESK_HIP_ERR, "E10001: bad decode arguments");
+    const uint64_t top = bound - 1;
+    const int width = top <= 0xffu ? 1 : top <= 0xffffu ? 2 : top <= 0xffffffffu ? 4 : 8;
+    hipError_t e = pskd_idx_launch(src, width, n, (long long*)dst, (hipStream_t)stream);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, ".psk.d decode");
+}
+
 int presk_hip_scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
     hipError_t e = scalar_digest(fn, lo, hi, digest);
     return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "scalar digest");

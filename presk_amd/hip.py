@@ -26,7 +26,8 @@ SYMBOLS = ["presk_hip_init", "presk_hip_last_error", "presk_hip_compile", "presk
            "presk_hip_sync", "presk_hip_stream_create", "presk_hip_stream_destroy", "presk_hip_time",
            "presk_hip_scalar_digest", "presk_hip_batch_create", "presk_hip_batch_add", "presk_hip_batch_graph",
            "presk_hip_batch_run", "presk_hip_batch_release", "presk_hip_convert", "presk_hip_batch_add_convert",
-           "presk_hip_fill_normal", "presk_hip_dropout_mask", "presk_hip_batch_add_dropout"]
+           "presk_hip_fill_normal", "presk_hip_dropout_mask", "presk_hip_batch_add_dropout",
+           "presk_hip_pskd_decode", "presk_hip_pskd_decode_idx"]
 
 
 class HipError(RuntimeError):
@@ -83,6 +84,8 @@ def lib():
         L.presk_hip_batch_release.restype = None
         L.presk_hip_convert.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_char_p, i64, vp, vp]
         L.presk_hip_fill_normal.argtypes = [vp, ctypes.c_char_p, i64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]
+        L.presk_hip_pskd_decode.argtypes = [vp, ctypes.c_int, vp, i64, vp, ctypes.c_char_p, vp, vp]
+        L.presk_hip_pskd_decode_idx.argtypes = [vp, ctypes.c_uint64, i64, vp, vp]
         L.presk_hip_dropout_mask.argtypes = [vp, ctypes.c_double, ctypes.c_char_p, i64, vp, vp]
         L.presk_hip_batch_add_dropout.argtypes = [vp, vp, ctypes.c_double, ctypes.c_char_p, i64, vp]
         L.presk_hip_batch_add_convert.argtypes = [vp, vp, ctypes.c_char_p, vp, ctypes.c_char_p, i64, vp]

@@ -56,9 +56,9 @@ def child(key: bytes, t: int) -> bytes:
     return stream(seed, 32)
 
 
-def from_seed(seed: int) -> bytes:
-    """Key::from_seed: the first 32 stream bytes of rand_core's seed_from_u64,
-    whose seed is eight PCG32 outputs (XSH RR), each little-endian."""
+def seed_key(seed: int) -> bytes:
+    """The key of rand_core's seed_from_u64 for ChaCha20Rng: eight PCG32
+    outputs (XSH RR), each little-endian."""
     mul, inc = 6364136223846793005, 11634580027462260723
     state = seed & 0xFFFFFFFFFFFFFFFF
     words = []
@@ -67,4 +67,9 @@ def from_seed(seed: int) -> bytes:
         xs = (((state >> 18) ^ state) >> 27) & _M32
         rot = state >> 59
         words.append(((xs >> rot) | (xs << ((32 - rot) & 31))) & _M32)
-    return stream(struct.pack("<8I", *words), 32)
+    return struct.pack("<8I", *words)
+
+
+def from_seed(seed: int) -> bytes:
+    """Key::from_seed: the first 32 stream bytes of seed_from_u64's generator."""
+    return stream(seed_key(seed), 32)
