@@ -139,6 +139,9 @@ def main():
     ap.add_argument("--eager", action="store_true", help="issue the launches one by one instead of one HIP graph")
     ap.add_argument("--dominant-only", type=int, default=0, metavar="N",
                     help="after the timing pass, run the dominant launch alone N times and exit (for rocprofv3 --pmc)")
+    ap.add_argument("--dominant-match", default=None, metavar="TEXT",
+                    help="take the dominant launch among those whose key contains TEXT (counter runs distort "
+                         "the timings the choice is made on)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain copy-like nest (neg over 64 Mi f32) 3 times and exit: the counters' calibration")
     ap.add_argument("--cpu-rows", type=int, default=None)
@@ -190,7 +193,8 @@ def main():
     # the dominant kernel: the launch with the largest time, timed alone with
     # HIP events on its stream
     times = p.kernel_times(reps=max(args.steps, 10))
-    ln, ms = max(times, key=lambda t: t[1])
+    pool = [t for t in times if args.dominant_match is None or args.dominant_match in launch_key(t[0])] or times
+    ln, ms = max(pool, key=lambda t: t[1])
     c = ln.compiled
     key = launch_key(ln)
     if args.dominant_only:
