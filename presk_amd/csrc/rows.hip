@@ -729,6 +729,164 @@ __global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
     if (ovf && a.flag) atomicOr(a.flag, 1u);
 }
 
+// Rows of NC whole 64-column chunks (n = 64 NC, NC <= 4): the streamed
+// kernel's three passes over the group's values kept in registers (64 a
+// lane at NC = 4), so x is read once and each exponential computed once;
+// the same max, the same walk of the tile for z, the same quotient.
+template <int OP, int ST, int NC>
+__global__ void __launch_bounds__(64) softmax_short_kernel(RowArgs a) {
+    constexpr bool MASKED = OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2;
+    constexpr bool TWO = OP == kSoftmax2 || OP == kMaskedSoftmax2;
+    using G = SGeo<ST>;
+    constexpr int VEC = G::VEC, LPR = G::LPR, RPI = G::RPI, NQ = G::NQ;
+    constexpr int n = NC * SCW;
+    typedef unsigned U4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) float tile[SR * STS];
+    const int lane = threadIdx.x;
+    const long long row0 = (long long)blockIdx.x * SR;
+    const int nr = (int)(a.rows - row0 < SR ? a.rows - row0 : SR);
+    constexpr long long MW = mask_words(n);
+    const int lc = (lane % LPR) * VEC;
+    bool ovf = false;
+    int myrow[NQ];
+    const unsigned* mrow[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int r = q * RPI + lane / LPR;
+        myrow[q] = r < nr ? r : nr - 1;
+        mrow[q] = MASKED ? a.mbits + ((row0 + myrow[q]) % a.mask_rows) * MW : nullptr;
+    }
+    // the whole group, once
+    float v[NC][NQ][VEC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const U4 w = *(const U4*)((const char*)a.x + ((row0 + myrow[q]) * n + c * SCW + lc) * (ST == 0 ? 4 : 2));
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) {
+                if (ST == 0) v[c][q][u] = __uint_as_float(w[u]);
+                else {
+                    const unsigned short h = (unsigned short)(w[u / 2] >> (16 * (u & 1)));
+                    v[c][q][u] = ST == 1 ? pk_bf16_to_f32(h) : pk_f16_to_f32(h);
+                }
+            }
+        }
+    auto bits = [&](int q, int c) -> unsigned {
+        constexpr unsigned live = (1u << VEC) - 1u;
+        if (!MASKED) return live;
+        const int col = c * SCW + lc;
+        return (mrow[q][col >> 5] >> (col & 31)) & live;
+    };
+
+    // 1. the max (as the streamed kernel: lane partials joined over the row)
+    const int BIG = 0x7fffffff;
+    float mq[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        float m = -__builtin_inff();
+        int f = BIG;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const unsigned al = bits(q, c);
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) {
+                const bool ok = ((al >> u) & 1u) != 0;
+                m = ok && v[c][q][u] > m ? v[c][q][u] : m;
+                f = ok && f == BIG ? c * SCW + lc + u : f;
+            }
+        }
+        for (int off = LPR / 2; off > 0; off >>= 1) {
+            const float o = __shfl_xor(m, off, 64);
+            const int g = __shfl_xor(f, off, 64);
+            m = o > m ? o : m;
+            f = g < f ? g : f;
+        }
+        const float first = f == BIG ? 0.f : ld<ST>(a.x, (row0 + myrow[q]) * n + f);
+        mq[q] = f == BIG ? 0.f : first != first ? first : m;
+    }
+
+    // 2. the exponentials, in place; z by lane i walking row i through the tile
+    float z = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            exps<VEC>(v[c][q], mq[q], bits(q, c));
+            float* t = &tile[(q * RPI + lane / LPR) * STS + lc];
+#pragma unroll
+            for (int u = 0; u < VEC; u += 4) *(float4*)&t[u] = float4{v[c][q][u], v[c][q][u + 1], v[c][q][u + 2], v[c][q][u + 3]};
+        }
+        __syncthreads();
+        if (lane < nr) {
+            const float* t = &tile[lane * STS];
+#pragma unroll
+            for (int j = 0; j < SCW; j += 4) {
+                const float4 e = *(const float4*)&t[j];
+                z = z + e.x;
+                z = z + e.y;
+                z = z + e.z;
+                z = z + e.w;
+            }
+        }
+        __syncthreads();
+    }
+    float zq[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) zq[q] = __shfl(z, q * RPI + lane / LPR, 64);
+
+    // 3. the outputs, 16 bytes a lane
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int row = q * RPI + lane / LPR;
+            if (row >= nr) continue;
+            const unsigned al = bits(q, c);
+            float f[VEC];
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) {
+                const bool ok = ((al >> u) & 1u) != 0;
+                const float e = v[c][q][u];
+                float o;
+                if (TWO) {
+                    if (ST == 2) ovf |= pk_overflows_f16(e);
+                    o = stored<ST>(e) / zq[q];
+                } else {
+                    o = e / zq[q];
+                }
+                f[u] = ok ? o : 0.f;
+            }
+            U4 o;
+            if (ST == 0) {
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) o[u] = __float_as_uint(f[u]);
+            } else {
+                o = U4{0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) {
+                    if (ST == 2) ovf |= pk_overflows_f16(f[u]);
+                    const unsigned h = ST == 1 ? pk_f32_to_bf16(f[u]) : pk_f32_to_f16(f[u]);
+                    o[u / 2] |= h << (16 * (u & 1));
+                }
+            }
+            *(U4*)((char*)a.out + ((row0 + row) * n + c * SCW + lc) * (ST == 0 ? 4 : 2)) = o;
+        }
+    if (ovf && a.flag) atomicOr(a.flag, 1u);
+}
+
+template <int OP, int NC>
+hipError_t launch_short(const RowArgs& a, hipStream_t stream) {
+    const unsigned grid = (unsigned)((a.rows + SR - 1) / SR);
+    switch (a.storage) {
+        case 0: softmax_short_kernel<OP, 0, NC><<<grid, 64, 0, stream>>>(a); break;
+        case 1: softmax_short_kernel<OP, 1, NC><<<grid, 64, 0, stream>>>(a); break;
+        case 2: softmax_short_kernel<OP, 2, NC><<<grid, 64, 0, stream>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int OP, int R, bool RES>
 hipError_t launch_r(const RowArgs& a, hipStream_t stream);
 
@@ -740,6 +898,14 @@ hipError_t launch_stream(const RowArgs& a, hipStream_t stream) {
     const int esz = a.storage == 0 ? 4 : 2;
     if (a.n % SCW != 0 || (uintptr_t)a.x % 16 != 0 || (uintptr_t)a.out % 16 != 0 || (a.n * esz) % 16 != 0)
         return launch_r<OP, 16, false>(a, stream);
+    // rows of at most four chunks: kept in registers
+    switch (a.n / SCW) {
+        case 1: return launch_short<OP, 1>(a, stream);
+        case 2: return launch_short<OP, 2>(a, stream);
+        case 3: return launch_short<OP, 3>(a, stream);
+        case 4: return launch_short<OP, 4>(a, stream);
+        default: break;
+    }
     const unsigned grid = (unsigned)((a.rows + SR - 1) / SR);
     switch (a.storage) {
         case 0: softmax_stream_kernel<OP, 0><<<grid, 64, 0, stream>>>(a); break;

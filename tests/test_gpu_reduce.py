@@ -293,3 +293,36 @@ def test_long_row_walk_attention_shape(dt):
         assert c.kind == "rows", c.kind
         got = out.download(want.dtype, want.size)
         _same_bits_nan_as_nan(got.reshape(-1), want.reshape(-1), dt)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("T", [64, 128, 192])
+def test_short_rows_kept_in_registers(dt, T):
+    """softmax rows of one, two and three 64-column chunks, at least 8 192 of
+    them (the register-kept form): masked 3- and 2-pass and unmasked, a NaN,
+    a row the mask allows nowhere, bit-exact against the oracle"""
+    H = -(-8192 // T)
+    s = O(A(("batch", 1), ("heads", H), ("seq", T), ("seq2", T)))
+    mask = O(A(("seq", T), ("seq2", T)), "idx")
+    ex = hip.HipExec(0, mode=hip.EXACT)
+    from oracle import kernel_text as kt
+    for low in (L.masked_softmax("seq2", [s, mask], dt), L.masked_softmax("seq2", [s, mask], dt, two_passes=True),
+                L.softmax("seq2", [s], dt)):
+        print(f"[short softmax] {dt} T={T} {low.name}", flush=True)
+        ins = zoo.inputs(low, seed=23, scale=3.0)
+        x = fmt.decode(ins[0], dt).reshape(H, T, T).copy()
+        x[1, 3, 5] = np.nan
+        ins[0] = fmt.encode(x.astype(np.float32), dt)
+        if len(ins) == 2:
+            m = np.tril(np.ones((T, T), np.int64))
+            m[7, :] = 0
+            ins[1] = m.ravel()
+        want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes, threads=8)
+        k = kt.parse_kernel(low.text)
+        nbytes = k.output.numel * hip.STORAGE_BYTES[dt]
+        out = hip.DeviceBuffer(nbytes)
+        out.upload(np.full(nbytes, 0xFF, np.uint8))
+        c = ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+        assert c.kind == "rows", c.kind
+        got = out.download(want.dtype, want.size).reshape(want.shape)
+        _same_bits_nan_as_nan(got, want, dt)
