@@ -159,14 +159,15 @@ def _same_bits_nan_as_nan(got, want, dt):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("T", [40, 256, 300])
+@pytest.mark.parametrize("T", [40, 256, 300, 320])
 def test_rows_class_nan_and_empty_rows(dt, T):
     """the masked max's corner cases: a NaN first allowed element (the max is
     NaN), a NaN later allowed element and a NaN disallowed one (both passed
     over), -inf first, and a row the mask allows nowhere (all zeros); rows
     that stay in registers (40), short rows of whole 64-column chunks that
-    are many enough to stream (256, 8192 rows) and rows the long-row walk
-    streams (300)"""
+    are many enough to stream (256, 8192 rows), rows the long-row walk
+    streams through the general row kernel (300, not whole 16-byte vectors)
+    and through the streamed kernel (320)"""
     B, H = 2, (16 if T == 256 else 3)
     s = O(A(("batch", B), ("heads", H), ("seq", T), ("seq2", T)))
     mask = O(A(("seq", T), ("seq2", T)), "idx")
