@@ -27,11 +27,13 @@ DATA = {"gpt-step": "synthetic (seeded ids and targets uniform over the vocabula
                  "presk_hip_fill_normal)"}
 
 
-def workload(name: str, dtype: str, rows=None, realize=None, dropout=0.0):
+def workload(name: str, dtype: str, rows=None, realize=None, dropout=0.0, adamw=False):
     """(program, host inputs, tokens per step, contraction flops, config record)
     of a workload; `rows` shrinks it for the CPU sample; `realize` (`@FILE`)
     gives the GPT's sites their storage types (a mixed realization).  The
-    Llama forward's inputs are made on the device (`host` None)."""
+    Llama forward's inputs are made on the device (`host` None).  `adamw`:
+    the training step followed by its optimizer step (adamw.step at step
+    200 of 1000, 05_gpt.psk's hyperparameters)."""
     from presk_amd import configs, gpt, llama
     from presk_amd.realize import Realization
 
@@ -58,13 +60,16 @@ def workload(name: str, dtype: str, rows=None, realize=None, dropout=0.0):
     train = name == "gpt-step"
     s = gpt.COURSE if rows is None else gpt.GptShape(B=max(rows // gpt.COURSE.T, 1))
     r = Realization.parse(realize) if realize else None
-    p, b, names = gpt.build(s, dtype, train=train, realize=r, dropout=dropout if train else 0.0)
+    opt = bool(adamw and train)
+    p, b, names = gpt.build(s, dtype, train=train, realize=r, dropout=dropout if train else 0.0, optimizer=opt)
     host = gpt.host_inputs(s)
+    if opt:
+        host.update(gpt.optimizer_inputs(s, 200, 1000))
     cfg = {"workload": ("config 4: course GPT training step (loss value and gradient of every parameter)" if train
                         else "config 3: course GPT forward and loss"),
            "L": s.L, "d_model": s.D, "heads": s.H, "vocab": s.V, "batch": s.B, "seq": s.T,
            "storage": dtype if r is None else f"mixed ({realize})", "compute": "f32", "launches": len(p.launches),
-           "dropout": dropout if train else 0.0}
+           "dropout": dropout if train else 0.0, "optimizer": "adamw" if opt else None}
     return p, host, s.B * s.T, gpt.contraction_flops(s, train), cfg
 
 
@@ -106,13 +111,13 @@ def copy_probe():
     print(json.dumps({"copy_probe": low.name, "bytes_read": 4 * n, "bytes_written": 4 * n, "runs": 3}), flush=True)
 
 
-def cpu_baseline(name: str, dtype: str, rows: int, threads: int, realize=None, dropout=0.0):
+def cpu_baseline(name: str, dtype: str, rows: int, threads: int, realize=None, dropout=0.0, adamw=False):
     """The oracle (the kernel interpreter's semantics in C, -O3 -march=native,
     the outermost parallel loop split over OpenMP threads as the native
     executor splits it) on a bounded sample of the workload's rows."""
     from tests import cpu_program
 
-    p, host, tokens, _, _ = workload(name, dtype, rows, realize, dropout)
+    p, host, tokens, _, _ = workload(name, dtype, rows, realize, dropout, adamw)
     cpu_program.compile_all(p, native=True, workers=threads)
     best = None
     for _ in range(1 if name.startswith("gpt") else 2):
@@ -132,6 +137,8 @@ def main():
     ap.add_argument("--dtype", default=None)
     ap.add_argument("--realize", default=None, metavar="@FILE",
                     help="a realization file (the reference's schema) for the GPT workloads: storage type per site")
+    ap.add_argument("--adamw", action="store_true",
+                    help="config 4 with its optimizer step (adamw.step, f32): the training run's whole step")
     ap.add_argument("--dropout", type=float, default=0.0,
                     help="the training step's dropout rate (the course's 0.2): masks drawn on the device, a new "
                          "step key each step")
@@ -157,7 +164,7 @@ def main():
         copy_probe()
         return
     dtype = args.dtype or ("bf16" if args.workload in ("mlp", "llama") else "f32")
-    p, host, tokens, flops, cfg = workload(args.workload, dtype, realize=args.realize, dropout=args.dropout)
+    p, host, tokens, flops, cfg = workload(args.workload, dtype, realize=args.realize, dropout=args.dropout, adamw=args.adamw)
     # a training run's keys: step i draws from Key::child(run key, i); the site
     # keys are derived before the timed region, uploaded (608 bytes) each step
     step_keys = []
@@ -243,7 +250,7 @@ def main():
     if not args.no_cpu:
         threads = min(os.cpu_count() or 1, 16)
         rows = args.cpu_rows or {"mlp": 4096, "linear": 1024, "gpt-step": 2048, "gpt-forward": 4096}[args.workload]
-        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads, args.realize, args.dropout)
+        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads, args.realize, args.dropout, args.adamw)
         rec["cpu_baseline"] = {"value": round(v, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
                                "sample": f"{n} of {tokens} tokens (rows) of the same workload: the oracle's C restatement of "
                                          f"the same default-layout nests (-O3 -march=native, -ffp-contract=off, sequential "

@@ -505,7 +505,8 @@ struct ColSumPlan : ClassPlan {
 std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
     const int st = k.dtype == Ty::F32 ? 0 : k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : -1;
     if (st < 0 || k.inputs.empty() || k.inputs[0].ty != k.dtype || k.output.ty != k.dtype) return nullptr;
-    if ((k.name == "sum_all" || k.name == "mean_all") && k.inputs.size() == 1 && k.output.dims.empty()) {
+    const bool squares = k.name == "sum_squares";
+    if ((k.name == "sum_all" || k.name == "mean_all" || squares) && k.inputs.size() == 1 && k.output.dims.empty()) {
         // every element, as one column
         auto p = std::make_unique<ColSumPlan>();
         p->n_in = 1;
@@ -516,6 +517,7 @@ std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
         p->a.nchunks = (p->a.rows + p->a.chunk - 1) / p->a.chunk;
         if (p->a.nchunks > 65535) return nullptr;
         p->a.div = k.name == "mean_all" ? (float)(double)p->a.rows : 0.f;
+        p->a.square = squares ? 1 : 0;
         p->a.storage = st;
         p->guarded = k.guarded();
         return p;

@@ -1,7 +1,8 @@
 // Column reductions in a declared chunked order (FAST mode): `sum_to` of a
 // tensor onto its trailing axes (a bias's gradient, lower.rs:1670-1680),
-// out[c] = sum_r x[r][c]; and `sum_all`/`mean_all` (lower.rs:1221-1233) as
-// the one column of all elements, the mean dividing the total once.
+// out[c] = sum_r x[r][c]; and `sum_all`/`mean_all` (lower.rs:1221-1233) and
+// `sum_squares` (lower.rs:1693-1703, the terms x * x) as the one column of
+// all elements, the mean dividing the total once.
 //
 // The interpreter's order adds the R rows one after another into the output
 // (a running sum of R dependent additions per column: latency-bound with one
@@ -28,7 +29,13 @@ __device__ __forceinline__ float ld(const void* p, long long i) {
 }
 
 // one lane per (chunk, column): the chunk's rows summed in order, all of a
-// full chunk's loads in flight before the first add
+// full chunk's loads in flight before the first add; a term is x, or x * x
+// rounded once (`sum_squares`: Product then Accum, lower.rs:1693-1703)
+template <int ST>
+__device__ __forceinline__ float term(float x, bool square) {
+    return square ? x * x : x;
+}
+
 template <int ST>
 __global__ void __launch_bounds__(64) colsum_chunks(ColSumArgs a) {
     const long long col = (long long)blockIdx.x * 64 + threadIdx.x;
@@ -41,11 +48,11 @@ __global__ void __launch_bounds__(64) colsum_chunks(ColSumArgs a) {
 #pragma unroll
         for (int i = 0; i < 64; ++i) v[i] = ld<ST>(a.x, (r0 + i) * a.cols + col);
 #pragma unroll
-        for (int i = 0; i < 64; ++i) part = part + v[i];
+        for (int i = 0; i < 64; ++i) part = part + term<ST>(v[i], a.square);
     } else {
         long long r1 = r0 + a.chunk;
         if (r1 > a.rows) r1 = a.rows;
-        for (long long r = r0; r < r1; ++r) part = part + ld<ST>(a.x, r * a.cols + col);
+        for (long long r = r0; r < r1; ++r) part = part + term<ST>(ld<ST>(a.x, r * a.cols + col), a.square);
     }
     a.work[ch * a.cols + col] = part;
 }

@@ -13,6 +13,7 @@ struct ColSumArgs {
     long long rows, cols, chunk, nchunks;
     float div;            // mean: the total divided by this (the nest's f32 count), else 0
     int storage;          // 0 f32, 1 bf16, 2 f16
+    int square;           // 1: each term is x * x (rounded), `sum_squares`
 };
 
 hipError_t colsum_launch(const ColSumArgs& a, hipStream_t stream);

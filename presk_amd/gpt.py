@@ -355,7 +355,7 @@ def site_keys(s: GptShape, step_key: bytes) -> list:
 
 
 def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realize=None, dropout: float = 0.0,
-          step_key: bytes | None = None) -> tuple:
+          step_key: bytes | None = None, optimizer: bool = False) -> tuple:
     """The program of config 3 (`train=False`: loss only) or config 4.
     Returns (program, builder, names) with names["loss"] and, for training,
     names["grads"][param] = buffer of its gradient.  `realize`: a
@@ -516,7 +516,119 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
         G["tok"] = b.embed_vjp("tok", "ids", dx, name="d.tok")
         dpe = b.sum_to(dx, pe)
         G["pos"] = b.embed_vjp("pos", pos_ids, dpe, name="d.pos")
+    if optimizer:
+        # the training run's step: `value_vjp` then `adamw.step` (crates/presk-train/src/step.rs)
+        if dtype != "f32" or realize is not None:
+            raise ValueError("E7005: the optimizer step is built for f32 storage (a narrower one rounds each "
+                             "unfused let, which its fused chains do not)")
+        names["adamw"] = adamw(b, s, G)
     return p, b, names
+
+
+# ---- the optimizer step (adamw.step) ------------------------------------------------
+
+# 05_gpt.psk's `optimizer adamw` (examples/corpus/nlp/05_gpt.psk:112-117); eps
+# takes its default (crates/presk-core/src/lower/optim.rs:58)
+ADAMW = {"lr": "3e-4", "beta1": "0.9", "beta2": "0.95", "eps": "1e-8", "weight_decay": "0.1", "grad_clip": "1.0",
+         "warmup": 100}
+# the literals the step reads, as the host makes them: f64 text, then one
+# rounding into the storage type (`Real` of an f64, host.rs's `scalar`)
+_OPT_LITS = {"opt.one": "1", "opt.b1": "beta1", "opt.b2": "beta2", "opt.eps": "eps", "opt.wd": "weight_decay",
+             "opt.clip": "grad_clip", "opt.tiny": "1e-6", "opt.lr": "lr", "opt.w": "warmup", "opt.half": "0.5"}
+# at most this many scalars a kernel sums (a kernel reads at most 24 buffers)
+_SUM_CHUNK = 21
+
+
+def optimizer_inputs(s: GptShape, t: int, total: int, hyper: dict = ADAMW) -> dict:
+    """The step's host inputs: the moments at zero (adamw.init), the literals,
+    pi (PrimOp::Pi, f64 pi rounded once), and the step counters t and total
+    (`Real` of a nat)."""
+    out = {}
+    for name, axes in param_shapes(s).items():
+        n = 1
+        for a in axes:
+            n *= a.len
+        out["m." + name] = np.zeros(n, np.float32)
+        out["v." + name] = np.zeros(n, np.float32)
+    for k, v in _OPT_LITS.items():
+        out[k] = np.array([float(hyper.get(v, v))], np.float32)
+    out["opt.pi"] = np.array([math.pi], np.float32)
+    out["opt.t"] = np.array([float(t)], np.float32)
+    out["opt.total"] = np.array([float(total)], np.float32)
+    return out
+
+
+def _min1(b: Builder, x, name):
+    """min(1, x) = 1 - relu(1 - x) (optim.rs's `min1`)."""
+    return b.fused([("sub", [("in", 0), ("in", 1)]), ("relu", [("step", 0)]), ("sub", [("in", 0), ("step", 1)])],
+                   ["opt.one", x], "opt.one", name=name)
+
+
+def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
+    """adamw.step (crates/presk-core/src/lower/optim.rs:171-237) over the
+    parameters and their gradients, as the host runs it: every tree
+    operation leaf by leaf (host.rs:1732-1787), the scalars as 0-dim
+    kernels, SumSquares as one `sum_squares` nest a leaf added in f64 on the
+    host in leaf order (host.rs:1571-1587) -- here f64 kernels over the
+    leaves' f32 scalars, read through the f32 -> f64 edge conversion, whose
+    result is read back through the f64 -> f32 one (`scalar`'s rounding).
+    Each leaf's m', v' and theta' are one fused chain each: in f32 storage a
+    chain's f32 intermediates are the values the unfused lets store.
+    Returns {param: (theta', m', v')}."""
+    names = list(param_shapes(s))
+    for k in list(_OPT_LITS) + ["opt.pi", "opt.t", "opt.total"]:
+        b.input(k, A())
+    for n in names:
+        b.input("m." + n, b.axes[n])
+        b.input("v." + n, b.axes[n])
+    out = {}
+    with b.func("adamw.step"):
+        # clipping to the global norm: g * min(1, c / (sqrt(sum g^2) + 1e-6))
+        ss = [b._prim(lambda dt, g=grads[n]: L.sum_squares([b.op(g)], dt), [grads[n]], f"opt.ss.{n}") for n in names]
+        acc = None
+        for i in range(0, len(ss), _SUM_CHUNK):
+            part = ss[i:i + _SUM_CHUNK]
+            ins = ([acc] if acc else []) + part
+            steps = [("add", [("in", 0), ("in", 1)])] + [("add", [("step", k), ("in", k + 2)]) for k in range(len(ins) - 2)]
+            name = f"opt.n2.{i // _SUM_CHUNK}"
+            acc = b._out(L.fused(steps, [b.op(x) for x in ins], [], "f64"), ins, name)
+        norm = b.fused([("sqrt", [("in", 0)]), ("add", [("step", 0), ("in", 1)]), ("div", [("in", 2), ("step", 1)])],
+                       [acc, "opt.tiny", "opt.clip"], "opt.one", name="opt.coef")
+        factor = _min1(b, norm, "opt.factor")
+        omb = b.fused([("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b1"], "opt.one", name="opt.omb1")
+        omb2 = b.fused([("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b2"], "opt.one", name="opt.omb2")
+        # bias corrections 1 - beta^t = 1 - exp(t * ln beta)
+        bc = [b.fused([("log", [("in", 1)]), ("mul", [("in", 2), ("step", 0)]), ("exp", [("step", 1)]),
+                       ("sub", [("in", 0), ("step", 2)])], ["opt.one", beta, "opt.t"], "opt.one", name=f"opt.bc{i + 1}")
+              for i, beta in enumerate(("opt.b1", "opt.b2"))]
+    with b.func("adamw.lr"):
+        # cosine(warmup = w): lr * min(1, t/w) * (1 + cos(pi * min(1, relu((t - w) / (relu(total - w - 1) + 1))))) / 2
+        q = b.fused([("div", [("in", 0), ("in", 1)])], ["opt.t", "opt.w"], "opt.one", name="opt.q")
+        warm = _min1(b, q, "opt.warm")
+        r = b.fused([("sub", [("in", 0), ("in", 2)]), ("sub", [("in", 1), ("in", 2)]), ("sub", [("step", 1), ("in", 3)]),
+                     ("relu", [("step", 2)]), ("add", [("step", 3), ("in", 3)]), ("div", [("step", 0), ("step", 4)]),
+                     ("relu", [("step", 5)])], ["opt.t", "opt.total", "opt.w", "opt.one"], "opt.one", name="opt.r")
+        prog = _min1(b, r, "opt.p")
+        lr = b.fused([("mul", [("in", 0), ("in", 1)]), ("cos", [("step", 0)]), ("add", [("in", 2), ("step", 1)]),
+                      ("mul", [("step", 2), ("in", 3)]), ("mul", [("in", 4), ("step", 3)]), ("mul", [("in", 5), ("step", 4)])],
+                     ["opt.pi", prog, "opt.one", "opt.half", warm, "opt.lr"], "opt.one", name="opt.lr_t")
+    with b.func("adamw.step"):
+        for n in names:
+            g, m, v = grads[n], "m." + n, "v." + n
+            # m' = m b1 + (g factor)(1 - b1)
+            m2 = b.fused([("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("in", 4)]),
+                          ("add", [("step", 1), ("step", 2)])], [g, factor, m, "opt.b1", omb], n, name=f"opt.m2.{n}")
+            # v' = v b2 + (g factor)^2 (1 - b2)
+            v2 = b.fused([("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("step", 0)]),
+                          ("mul", [("step", 2), ("in", 4)]), ("add", [("step", 1), ("step", 3)])],
+                         [g, factor, v, "opt.b2", omb2], n, name=f"opt.v2.{n}")
+            # theta' = theta - lr (m'/bc1 / (sqrt(v'/bc2) + eps) + lambda theta)
+            th = b.fused([("div", [("in", 1), ("in", 2)]), ("div", [("in", 3), ("in", 4)]), ("sqrt", [("step", 1)]),
+                          ("add", [("step", 2), ("in", 5)]), ("div", [("step", 0), ("step", 3)]), ("mul", [("in", 0), ("in", 6)]),
+                          ("add", [("step", 4), ("step", 5)]), ("mul", [("step", 6), ("in", 7)]), ("sub", [("in", 0), ("step", 7)])],
+                         [n, m2, bc[0], v2, bc[1], "opt.eps", "opt.wd", lr], n, name=f"opt.theta.{n}")
+            out[n] = (th, m2, v2)
+    return out
 
 
 def host_inputs(s: GptShape, seed: int = 2) -> dict:

@@ -105,3 +105,55 @@ def test_tiny_gpt_step_with_dropout_matches_autograd():
         want = want_grads[name]
         err = np.max(np.abs(got - want)) / max(np.max(np.abs(want)), floor)
         assert err < 1e-4, (name, err)
+
+
+def adamw_f64(theta, g_all, m, v, t, total, h=gpt.ADAMW):
+    """AdamW as optim.rs:1-25 states it (PyTorch's, clip_grad_norm_ included)
+    in float64, from given gradients: clip to the global norm c, moments,
+    bias corrections 1 - beta^t, decoupled weight decay, cosine schedule
+    with warm-up w over `total` steps, t counted from 1."""
+    c, b1, b2 = float(h["grad_clip"]), float(h["beta1"]), float(h["beta2"])
+    eps, wd, lr0, w = float(h["eps"]), float(h["weight_decay"]), float(h["lr"]), float(h["warmup"])
+    norm = math.sqrt(sum(float(np.sum(np.square(g, dtype=np.float64))) for g in g_all.values()))
+    factor = min(1.0, c / (norm + 1e-6))
+    p = min(1.0, max(0.0, (t - w) / max(total - w, 1.0)))
+    lr = lr0 * min(1.0, t / w) * 0.5 * (1 + math.cos(math.pi * p))
+    out = {}
+    for k, th in theta.items():
+        g = g_all[k] * factor
+        m2 = b1 * m[k] + (1 - b1) * g
+        v2 = b2 * v[k] + (1 - b2) * g * g
+        upd = (m2 / (1 - b1 ** t)) / (np.sqrt(v2 / (1 - b2 ** t)) + eps) + wd * th
+        out[k] = (th - lr * upd, m2, v2)
+    return out, lr, factor
+
+
+def test_tiny_adamw_step_matches_float64():
+    """The program's adamw.step (gpt.adamw) run by the oracle, after a step
+    from nonzero moments, against AdamW in float64 from the program's own
+    f32 gradients: theta', m' and v' within f32 rounding."""
+    s = gpt.TINY
+    t, total = 150, 400
+    p, b, names = gpt.build(s, "f32", train=True, optimizer=True)
+    host = gpt.host_inputs(s)
+    host.update(gpt.optimizer_inputs(s, t, total))
+    rng = np.random.default_rng(4)
+    for k in gpt.param_shapes(s):                      # a later step: moments not at zero
+        host["m." + k] = (rng.standard_normal(host["m." + k].size) * 1e-3).astype(np.float32)
+        host["v." + k] = (rng.random(host["v." + k].size) * 1e-6).astype(np.float32)
+    env = cpu_program.run(p, host)
+    shapes = gpt.param_shapes(s)
+    dec = lambda name: fmt.decode(env[name], "f32").astype(np.float64)
+    grads = {k: dec(names["grads"][k]).ravel() for k in shapes}
+    theta = {k: np.asarray(host[k], np.float64).ravel() for k in shapes}
+    m = {k: host["m." + k].astype(np.float64) for k in shapes}
+    v = {k: host["v." + k].astype(np.float64) for k in shapes}
+    want, lr, factor = adamw_f64(theta, grads, m, v, t, total)
+    assert 0 < lr < 3e-4 and 0 < factor <= 1
+    for k in shapes:
+        th2, m2, v2 = (dec(x).ravel() for x in names["adamw"][k])
+        wt, wm, wv = want[k]
+        assert np.max(np.abs(m2 - wm)) <= 1e-6 * max(np.max(np.abs(wm)), 1e-30), k
+        assert np.max(np.abs(v2 - wv)) <= 1e-6 * max(np.max(np.abs(wv)), 1e-30), k
+        # theta' = theta - lr * update: the update within f32 rounding of itself, plus theta's own rounding
+        assert np.max(np.abs((th2 - theta[k]) - (wt - theta[k]))) <= 1e-5 * lr + 2 ** -23 * np.max(np.abs(theta[k])), k

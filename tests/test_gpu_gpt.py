@@ -107,3 +107,28 @@ def test_dropout_step_graph_takes_each_steps_key():
         env = cpu_program.run(q, host)
         for name in [m[0] for m in p.masks] + [names["loss"]]:
             assert p.bufs.download(name).tobytes() == env[name].tobytes(), (step, name)
+
+
+def test_tiny_gpt_step_with_adamw_exact_bits():
+    """the training run's step with its optimizer (adamw.step, f32): the
+    clipped global norm summed in f64 through the edge conversions, the
+    schedule and bias corrections as 0-dim kernels, every leaf's moments
+    and parameters -- every buffer equal to the oracle's, replayed as a
+    graph too"""
+    s = gpt.TINY
+    p, b, names = gpt.build(s, "f32", train=True, mode=hip.EXACT, optimizer=True)
+    host = gpt.host_inputs(s)
+    host.update(gpt.optimizer_inputs(s, 150, 400))
+    device_run(p, host)
+    q, _, _ = gpt.build(s, "f32", train=True, mode=hip.EXACT, optimizer=True)
+    env = cpu_program.run(q, host)
+    outs = [ln.out for ln in p.launches]
+    bad = [n for n in outs if p.bufs.download(n).tobytes() != env[n].tobytes()]
+    assert not bad, f"{len(bad)} buffers differ, first: {bad[:5]}"
+    assert any(ln.low.dtype == "f64" for ln in p.launches)       # the f64 sums ran
+    p.record(graph=True)
+    p.run()
+    hip.sync()
+    for k, (th, m2, v2) in names["adamw"].items():
+        for n in (th, m2, v2):
+            assert p.bufs.download(n).tobytes() == env[n].tobytes(), (k, n)

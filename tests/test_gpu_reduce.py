@@ -197,16 +197,19 @@ def test_rows_class_nan_and_empty_rows(dt, T):
         _same_bits_nan_as_nan(got, want, dt)
 
 
-def chunked_total_text(n, dtype, mean, chunk=64):
+def chunked_total_text(n, dtype, mean, chunk=64, squares=False):
     """out = chunked sum of x[0..n) (chunks of 64 from zero, then the chunk sums
-    in order from zero), divided by n for the mean: the declared order."""
+    in order from zero), divided by n for the mean: the declared order; with
+    `squares` the terms are x * x (sum_squares)."""
     full, rem = divmod(n, chunk)
     lines = [f"kernel total (%0 : {dtype}[{n}]) -> %1 : {dtype}[] {{", "  s0 = 0"]
+    term = (lambda i: f"(%0[{i}] * %0[{i}])") if squares else (lambda i: f"%0[{i}]")
     if full:
         lines += [f"  for i1 in 0..{full} {{", "    s1 = 0", f"    for i2 in 0..{chunk} {{",
-                  f"      s1 = (s1 + %0[((i1 * {chunk}) + i2)])", "    }", "    s0 = (s0 + s1)", "  }"]
+                  f"      s1 = (s1 + {term(f'((i1 * {chunk}) + i2)')})", "    }", "    s0 = (s0 + s1)", "  }"]
     if rem:
-        lines += ["  s1 = 0", f"  for i2 in 0..{rem} {{", f"    s1 = (s1 + %0[(i2 + {full * chunk})])", "  }", "  s0 = (s0 + s1)"]
+        lines += ["  s1 = 0", f"  for i2 in 0..{rem} {{", f"    s1 = (s1 + {term(f'(i2 + {full * chunk})')})", "  }",
+                  "  s0 = (s0 + s1)"]
     lines += [f"  %1[] = (s0 / {n})" if mean else "  %1[] = s0", "}"]
     return "\n".join(lines) + "\n"
 
@@ -327,3 +330,27 @@ def test_short_rows_kept_in_registers(dt, T):
         assert c.kind == "rows", c.kind
         got = out.download(want.dtype, want.size).reshape(want.shape)
         _same_bits_nan_as_nan(got, want, dt)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("mode", [hip.FAST, hip.EXACT])
+@pytest.mark.parametrize("n", [1500, 590_000])
+def test_sum_squares(dt, mode, n):
+    """sum_squares (the optimizer's clipping, lower.rs:1693-1703): FAST in the
+    chunked(64) order with the terms x * x (colsum class: a part chunk, and
+    9 219 chunks over two segments of the final chain), EXACT in index order;
+    bit-exact against the oracle's run of the order as a nest"""
+    x = O(A(("model", n)))
+    low = L.sum_squares([x], dt)
+    ex = hip.HipExec(0, mode=mode)
+    ins = zoo.inputs(low, seed=31, scale=0.2)          # a total binary16 holds (590 000 x 0.04)
+    c = ex.compiled(low.text, dt, low.lanes)
+    if mode == hip.FAST:
+        assert c.kind == "colsum", c.kind
+        want, _ = cexec.run(chunked_total_text(n, dt, False, squares=True), dt, ins, lanes=1)
+    else:
+        want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes)
+    nb = hip.STORAGE_BYTES[dt]
+    out = hip.DeviceBuffer(nb)
+    ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
+    assert out.download(np.uint8, nb).tobytes() == want.view(np.uint8).tobytes()
