@@ -539,12 +539,34 @@ _OPT_LITS = {"opt.one": "1", "opt.b1": "beta1", "opt.b2": "beta2", "opt.eps": "e
 _SUM_CHUNK = 21
 
 
+# Block's leaves in its record's order: attn's wq, wk, wv, wo (w, b each),
+# ff's up and down, ln1 and ln2 (gamma, beta) (05_gpt.psk:44-71)
+_BLOCK_LEAVES = ["wq", "wq.b", "wk", "wk.b", "wv", "wv.b", "wo", "wo.b", "up", "up.b", "down", "down.b",
+                 "ln1.g", "ln1.b", "ln2.g", "ln2.b"]
+
+
+def opt_leaves(s: GptShape) -> dict:
+    """The leaves adamw.step walks, in order: `params GPT`'s fields as
+    declared (tok, pos, blocks, lnf, head; 05_gpt.psk:80-85; the interpreter
+    keeps a record's fields as an ordered list, value.rs:278), the blocks'
+    leaves stacked along a leading layer axis (`stack{L}(Block)`,
+    StackParams, crates/presk-core/src/ir.rs:297).  name -> (axes, the
+    per-layer parameters it stacks, or None)."""
+    ps = param_shapes(s)
+    out = {"tok": (ps["tok"], None), "pos": (ps["pos"], None)}
+    for r in _BLOCK_LEAVES:
+        out["blocks." + r] = ([L.Axis("layer", s.L)] + ps["b0." + r], [f"b{l}.{r}" for l in range(s.L)])
+    for n in ("lnf.g", "lnf.b", "head"):
+        out[n] = (ps[n], None)
+    return out
+
+
 def optimizer_inputs(s: GptShape, t: int, total: int, hyper: dict = ADAMW) -> dict:
-    """The step's host inputs: the moments at zero (adamw.init), the literals,
-    pi (PrimOp::Pi, f64 pi rounded once), and the step counters t and total
-    (`Real` of a nat)."""
+    """The step's host inputs: the moments of every leaf at zero
+    (adamw.init), the literals, pi (PrimOp::Pi, f64 pi rounded once), and the
+    step counters t and total (`Real` of a nat)."""
     out = {}
-    for name, axes in param_shapes(s).items():
+    for name, (axes, _) in opt_leaves(s).items():
         n = 1
         for a in axes:
             n *= a.len
@@ -574,8 +596,23 @@ def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
     result is read back through the f64 -> f32 one (`scalar`'s rounding).
     Each leaf's m', v' and theta' are one fused chain each: in f32 storage a
     chain's f32 intermediates are the values the unfused lets store.
-    Returns {param: (theta', m', v')}."""
-    names = list(param_shapes(s))
+    The leaves are `opt_leaves`: a stacked leaf's parameters and gradients
+    are its layers' buffers, held one after another in one buffer
+    (Program.stack), as StackParams lays them out.
+    Returns {leaf: (theta', m', v')}."""
+    leaves = opt_leaves(s)
+    names = list(leaves)
+    grads = dict(grads)
+    for n, (axes, members) in leaves.items():
+        if members is None:
+            continue
+        count = 1
+        for a in axes[1:]:
+            count *= a.len
+        b.p.stack(n, members, "f32", count)
+        b.p.stack("d." + n, [grads[m] for m in members], "f32", count)
+        b.input(n, axes)
+        grads[n] = b.input("d." + n, axes)
     for k in list(_OPT_LITS) + ["opt.pi", "opt.t", "opt.total"]:
         b.input(k, A())
     for n in names:

@@ -152,6 +152,20 @@ class DeviceBuffer:
             pass
 
 
+class DeviceView(DeviceBuffer):
+    """Bytes [offset, offset + nbytes) of another buffer, which it keeps alive
+    and does not free."""
+
+    def __init__(self, parent: DeviceBuffer, offset: int, nbytes: int):
+        if offset < 0 or offset + nbytes > parent.nbytes:
+            raise ValueError(f"view [{offset}, {offset + nbytes}) outside a buffer of {parent.nbytes} bytes")
+        self.parent, self.nbytes = parent, int(nbytes)
+        self.ptr = parent.ptr + int(offset)
+
+    def free(self):
+        self.ptr = None
+
+
 class Compiled:
     """A compiled kernel (`KernelFn`)."""
 

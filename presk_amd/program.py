@@ -33,6 +33,9 @@ class Buffers:
     def __init__(self):
         self.dev: dict = {}
         self.meta: dict = {}
+        # name -> (parent, first element, parent's type, parent's count): a
+        # buffer held inside another (a layer's slice of a stacked leaf)
+        self.views: dict = {}
 
     def alloc(self, name: str, ty: str, count: int) -> hip.DeviceBuffer:
         if name in self.dev:
@@ -40,6 +43,15 @@ class Buffers:
             if (ty0, c0) != (ty, count):
                 raise ValueError(f"buffer {name} redeclared as {ty}[{count}] (was {ty0}[{c0}])")
             return self.dev[name]
+        if name in self.views:
+            parent, first, pty, pcount = self.views[name]
+            if ty != pty or first + count > pcount:
+                raise ValueError(f"buffer {name} ({ty}[{count}]) does not fit {parent} ({pty}[{pcount}]) at {first}")
+            whole = self.alloc(parent, pty, pcount)
+            b = hip.DeviceView(whole, first * BYTES[ty], count * BYTES[ty])
+            self.dev[name] = b
+            self.meta[name] = (ty, count)
+            return b
         b = hip.DeviceBuffer(max(count, 1) * BYTES[ty])
         self.dev[name] = b
         self.meta[name] = (ty, count)
@@ -106,6 +118,15 @@ class Program:
 
     def declare(self, name: str, ty: str, count: int):
         return self.bufs.alloc(name, ty, count)
+
+    def stack(self, parent: str, members: list, ty: str, count: int):
+        """Holds buffers `members` (each `count` elements of `ty`) one after
+        another in `parent` (`ty`[len(members) * count]): member i is the
+        parent's slice i along a new leading axis, with no copy."""
+        for i, m in enumerate(members):
+            if m in self.bufs.dev or m in self.bufs.views:
+                raise ValueError(f"buffer {m} is already allocated or held in a stack")
+            self.bufs.views[m] = (parent, i * count, ty, len(members) * count)
 
     def add_mask(self, name: str, slot: int, rate: float, ty: str, count: int) -> str:
         """A dropout mask `name` (DropoutMask with training on) drawn from key

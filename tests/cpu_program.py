@@ -74,10 +74,19 @@ def run(p, host: dict, threads: int = 1, native: bool = False) -> dict:
         for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
             if name in env and name not in types:
                 types[name] = p.input_types.get(name, ty) if ty != "i64" else ty
+    # a stacked buffer (Program.stack): its members one after another, read
+    # only after every member is written
+    stacks = {}
+    for m, (parent, first, _, _) in p.bufs.views.items():
+        stacks.setdefault(parent, []).append((first, m))
     flag = False
     for ln in p.launches:
         ins = []
         for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
+            if name not in env and name in stacks:
+                members = [m for _, m in sorted(stacks[name])]
+                env[name] = np.concatenate([np.asarray(env[m]).ravel() for m in members])
+                types[name] = types[members[0]]
             a = env[name]
             if types[name] not in ("i64", ln.low.dtype):
                 a, f = convert(a, types[name], ln.low.dtype, max(count, 1))

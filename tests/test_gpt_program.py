@@ -137,20 +137,26 @@ def test_tiny_adamw_step_matches_float64():
     p, b, names = gpt.build(s, "f32", train=True, optimizer=True)
     host = gpt.host_inputs(s)
     host.update(gpt.optimizer_inputs(s, t, total))
+    leaves = gpt.opt_leaves(s)
+    assert len(leaves) == 21 and sum(1 for _, mem in leaves.values() if mem) == 16
     rng = np.random.default_rng(4)
-    for k in gpt.param_shapes(s):                      # a later step: moments not at zero
+    for k in leaves:                                   # a later step: moments not at zero
         host["m." + k] = (rng.standard_normal(host["m." + k].size) * 1e-3).astype(np.float32)
         host["v." + k] = (rng.random(host["v." + k].size) * 1e-6).astype(np.float32)
     env = cpu_program.run(p, host)
-    shapes = gpt.param_shapes(s)
     dec = lambda name: fmt.decode(env[name], "f32").astype(np.float64)
-    grads = {k: dec(names["grads"][k]).ravel() for k in shapes}
-    theta = {k: np.asarray(host[k], np.float64).ravel() for k in shapes}
-    m = {k: host["m." + k].astype(np.float64) for k in shapes}
-    v = {k: host["v." + k].astype(np.float64) for k in shapes}
+
+    def stacked(get, k):
+        # a stacked leaf is its layers' values one after another
+        mem = leaves[k][1]
+        return np.concatenate([get(x) for x in mem]) if mem else get(k)
+    grads = {k: stacked(lambda x: dec(names["grads"][x]).ravel(), k) for k in leaves}
+    theta = {k: stacked(lambda x: np.asarray(host[x], np.float64).ravel(), k) for k in leaves}
+    m = {k: host["m." + k].astype(np.float64) for k in leaves}
+    v = {k: host["v." + k].astype(np.float64) for k in leaves}
     want, lr, factor = adamw_f64(theta, grads, m, v, t, total)
     assert 0 < lr < 3e-4 and 0 < factor <= 1
-    for k in shapes:
+    for k in leaves:
         th2, m2, v2 = (dec(x).ravel() for x in names["adamw"][k])
         wt, wm, wv = want[k]
         assert np.max(np.abs(m2 - wm)) <= 1e-6 * max(np.max(np.abs(wm)), 1e-30), k

@@ -113,13 +113,17 @@ def test_tiny_gpt_step_with_adamw_exact_bits():
     """the training run's step with its optimizer (adamw.step, f32): the
     clipped global norm summed in f64 through the edge conversions, the
     schedule and bias corrections as 0-dim kernels, every leaf's moments
-    and parameters -- every buffer equal to the oracle's, replayed as a
-    graph too"""
+    and parameters (the blocks' leaves stacked over the layers) -- every
+    buffer equal to the oracle's, replayed as a graph too"""
     s = gpt.TINY
     p, b, names = gpt.build(s, "f32", train=True, mode=hip.EXACT, optimizer=True)
     host = gpt.host_inputs(s)
     host.update(gpt.optimizer_inputs(s, 150, 400))
     device_run(p, host)
+    # the blocks' parameters and gradients sit in their stacked leaves, no copy
+    for l in range(s.L):
+        assert p.bufs.dev[f"b{l}.wq"].ptr == p.bufs.dev["blocks.wq"].ptr + 4 * l * s.D * s.D
+        assert p.bufs.dev[names["grads"][f"b{l}.up.b"]].ptr == p.bufs.dev["d.blocks.up.b"].ptr + 4 * l * 4 * s.D
     q, _, _ = gpt.build(s, "f32", train=True, mode=hip.EXACT, optimizer=True)
     env = cpu_program.run(q, host)
     outs = [ln.out for ln in p.launches]
