@@ -1,0 +1,60 @@
+"""Program.stack: buffers held one after another inside a stacked buffer
+(the layers' slices of a `stack{L}` leaf), checked on the host."""
+import pytest
+
+from presk_amd import gpt, hip
+from presk_amd.program import Buffers, Program
+
+
+class _Parent:
+    """A stand-in allocation: a base address and a size, nothing on a device."""
+    def __init__(self, ptr, nbytes):
+        self.ptr, self.nbytes = ptr, nbytes
+
+
+def test_view_offsets_and_bounds():
+    p = _Parent(4096, 64)
+    v = hip.DeviceView(p, 16, 48)
+    assert v.ptr == 4096 + 16 and v.nbytes == 48
+    v.free()                                   # a view frees nothing
+    assert p.ptr == 4096
+    with pytest.raises(ValueError):
+        hip.DeviceView(p, 32, 48)
+    with pytest.raises(ValueError):
+        hip.DeviceView(p, -4, 8)
+
+
+def test_stack_records_each_member_at_its_slice():
+    q = Program("t")
+    q.stack("w", ["w0", "w1", "w2"], "f32", 10)
+    assert q.bufs.views == {"w0": ("w", 0, "f32", 30), "w1": ("w", 10, "f32", 30), "w2": ("w", 20, "f32", 30)}
+    with pytest.raises(ValueError):
+        q.stack("w2x", ["w1"], "f32", 10)         # a buffer sits in one stack
+
+
+def test_member_of_another_type_or_size_is_refused():
+    b = Buffers()
+    b.dev["w"], b.meta["w"] = _Parent(0, 120), ("f32", 30)
+    b.views["w1"] = ("w", 10, "f32", 30)
+    with pytest.raises(ValueError):
+        b.alloc("w1", "bf16", 10)
+    with pytest.raises(ValueError):
+        b.views["w3"] = ("w", 25, "f32", 30)
+        b.alloc("w3", "f32", 10)
+    v = b.alloc("w1", "f32", 10)
+    assert v.ptr == 40 and b.meta["w1"] == ("f32", 10)
+
+
+def test_optimizer_leaves_stack_every_layer():
+    s = gpt.TINY
+    p, b, names = gpt.build(s, "f32", train=True, optimizer=True)
+    leaves = gpt.opt_leaves(s)
+    assert list(leaves)[:3] == ["tok", "pos", "blocks.wq"] and list(leaves)[-1] == "head"
+    for n, (axes, members) in leaves.items():
+        if members:
+            assert axes[0].len == s.L and len(members) == s.L
+            for l, m in enumerate(members):
+                parent, first, ty, total = p.bufs.views[m]
+                assert parent == n and ty == "f32" and first * s.L == l * total
+                assert p.bufs.views[names["grads"][m]][0] == "d." + n
+    assert set(names["adamw"]) == set(leaves)
