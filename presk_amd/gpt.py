@@ -539,24 +539,26 @@ _OPT_LITS = {"opt.one": "1", "opt.b1": "beta1", "opt.b2": "beta2", "opt.eps": "e
 _SUM_CHUNK = 21
 
 
-# Block's leaves in its record's order: attn's wq, wk, wv, wo (w, b each),
-# ff's up and down, ln1 and ln2 (gamma, beta) (05_gpt.psk:44-71)
+# Block's leaves in its tree's order: Block has no params of its own; its
+# uses attn (wq, wk, wv, wo: Linear's params w, b), ff (up, down), ln1 and
+# ln2 (LayerNorm's params gamma, beta) (05_gpt.psk:28-71)
 _BLOCK_LEAVES = ["wq", "wq.b", "wk", "wk.b", "wv", "wv.b", "wo", "wo.b", "up", "up.b", "down", "down.b",
                  "ln1.g", "ln1.b", "ln2.g", "ln2.b"]
 
 
 def opt_leaves(s: GptShape) -> dict:
-    """The leaves adamw.step walks, in order: `params GPT`'s fields as
-    declared (tok, pos, blocks, lnf, head; 05_gpt.psk:80-85; the interpreter
-    keeps a record's fields as an ordered list, value.rs:278), the blocks'
-    leaves stacked along a leading layer axis (`stack{L}(Block)`,
-    StackParams, crates/presk-core/src/ir.rs:297).  name -> (axes, the
-    per-layer parameters it stacks, or None)."""
+    """The leaves adamw.step walks, in order: the tree `params GPT` denotes,
+    a module's own params first and then its uses, each in declaration order
+    (crates/presk-types/src/elab/mod.rs:191-203): tok, pos, head, then
+    blocks, then lnf (05_gpt.psk:80-85); the blocks' leaves stacked along a
+    leading layer axis (`stack{L}(Block)`, ParamsTree::Stacked,
+    crates/presk-types/src/ty.rs:131-136).  name -> (axes, the per-layer
+    parameters it stacks, or None)."""
     ps = param_shapes(s)
-    out = {"tok": (ps["tok"], None), "pos": (ps["pos"], None)}
+    out = {n: (ps[n], None) for n in ("tok", "pos", "head")}
     for r in _BLOCK_LEAVES:
         out["blocks." + r] = ([L.Axis("layer", s.L)] + ps["b0." + r], [f"b{l}.{r}" for l in range(s.L)])
-    for n in ("lnf.g", "lnf.b", "head"):
+    for n in ("lnf.g", "lnf.b"):
         out[n] = (ps[n], None)
     return out
 

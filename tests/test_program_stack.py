@@ -49,7 +49,9 @@ def test_optimizer_leaves_stack_every_layer():
     s = gpt.TINY
     p, b, names = gpt.build(s, "f32", train=True, optimizer=True)
     leaves = gpt.opt_leaves(s)
-    assert list(leaves)[:3] == ["tok", "pos", "blocks.wq"] and list(leaves)[-1] == "head"
+    # a module's params, then its uses (crates/presk-types/src/elab/mod.rs:191-203)
+    assert list(leaves)[:5] == ["tok", "pos", "head", "blocks.wq", "blocks.wq.b"]
+    assert list(leaves)[-4:] == ["blocks.ln2.g", "blocks.ln2.b", "lnf.g", "lnf.b"]
     for n, (axes, members) in leaves.items():
         if members:
             assert axes[0].len == s.L and len(members) == s.L
