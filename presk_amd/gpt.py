@@ -376,6 +376,17 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
             p.input_types[name] = "f32"
     for name, axes in param_shapes(s).items():
         b.input(name, axes)
+    # each block parameter's layers held in one stacked buffer, as `params GPT`
+    # stores them (a reference checkpoint's leaf decodes straight into it)
+    for n, (axes, members) in opt_leaves(s).items():
+        if members is None:
+            continue
+        tys = {p.input_types.get(m, dtype if realize is None else None) for m in members}
+        if len(tys) == 1 and None not in tys:
+            count = 1
+            for a in axes[1:]:
+                count *= a.len
+            p.stack(n, members, tys.pop(), count)
     b.input("ids", A(("batch", s.B), ("seq", s.T)), "idx")
     b.input("y", A(("batch", s.B), ("seq", s.T)), "idx")
     b.input("eps", A())
@@ -563,6 +574,40 @@ def opt_leaves(s: GptShape) -> dict:
     return out
 
 
+# a leaf of Block as `params GPT` names it -> its name here
+_BLOCK_PATHS = {"wq": "attn.wq.w", "wq.b": "attn.wq.b", "wk": "attn.wk.w", "wk.b": "attn.wk.b",
+                "wv": "attn.wv.w", "wv.b": "attn.wv.b", "wo": "attn.wo.w", "wo.b": "attn.wo.b",
+                "up": "ff.up.w", "up.b": "ff.up.b", "down": "ff.down.w", "down.b": "ff.down.b",
+                "ln1.g": "ln1.γ", "ln1.b": "ln1.β", "ln2.g": "ln2.γ", "ln2.b": "ln2.β"}
+
+
+def params_layout(s: GptShape):
+    """(layout, rename) of a `params GPT` file: the tree in its leaf order
+    (opt_leaves), Block's leaves stacked, and the program buffer of each
+    leaf's dotted path (`blocks.attn.wq.w` -> the stacked `blocks.wq`)."""
+    from .pskd import Layout, Leaf
+
+    def rec(pairs):
+        return Layout.record([(k, v) for k, v in pairs])
+    leaves = opt_leaves(s)
+    shape = lambda n: tuple(a.len for a in leaves[n][0])
+    tree = {}
+    for r, path in _BLOCK_PATHS.items():
+        node = tree
+        parts = path.split(".")
+        for q in parts[:-1]:
+            node = node.setdefault(q, {})
+        node[parts[-1]] = Leaf(shape("blocks." + r))
+
+    def build(node):
+        return rec([(k, build(v) if isinstance(v, dict) else v) for k, v in node.items()])
+    layout = rec([("tok", Leaf(shape("tok"))), ("pos", Leaf(shape("pos"))), ("head", Leaf(shape("head"))),
+                  ("blocks", build(tree)), ("lnf", rec([("γ", Leaf(shape("lnf.g"))), ("β", Leaf(shape("lnf.b")))]))])
+    rename = {"blocks." + path: "blocks." + r for r, path in _BLOCK_PATHS.items()}
+    rename.update({"lnf.γ": "lnf.g", "lnf.β": "lnf.b"})
+    return layout, rename
+
+
 def optimizer_inputs(s: GptShape, t: int, total: int, hyper: dict = ADAMW) -> dict:
     """The step's host inputs: the moments of every leaf at zero
     (adamw.init), the literals, pi (PrimOp::Pi, f64 pi rounded once), and the
@@ -611,7 +656,8 @@ def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
         count = 1
         for a in axes[1:]:
             count *= a.len
-        b.p.stack(n, members, "f32", count)
+        if b.p.bufs.views.get(members[0], ("",))[0] != n:
+            raise ValueError(f"E7005: the layers of `{n}` are not held in one buffer")
         b.p.stack("d." + n, [grads[m] for m in members], "f32", count)
         b.input(n, axes)
         grads[n] = b.input("d." + n, axes)

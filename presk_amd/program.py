@@ -57,6 +57,13 @@ class Buffers:
         self.meta[name] = (ty, count)
         return b
 
+    def stacked(self, name: str):
+        """(type, count) of `name` when it is the buffer members are held in."""
+        for parent, _, ty, count in self.views.values():
+            if parent == name:
+                return ty, count
+        return None
+
     def upload(self, name: str, storage: np.ndarray):
         self.dev[name].upload(storage)
 

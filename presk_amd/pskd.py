@@ -237,6 +237,17 @@ class Layout:
             return [self.leaf]
         return [x for it in self.items for x in it.leaves()]
 
+    def paths(self, prefix: str = "") -> list:
+        """Each leaf's dotted path in leaf order: a record's field names, a
+        tuple's positions (`params M`'s leaves `blocks.attn.wq.w`, …)."""
+        if self.leaf is not None:
+            return [prefix]
+        out = []
+        for i, it in enumerate(self.items):
+            key = self.names[i] if self.names is not None else str(i)
+            out += it.paths(f"{prefix}.{key}" if prefix else key)
+        return out
+
     def sample_bytes(self, encs: list | None = None) -> int:
         out = 0
         for i, l in enumerate(self.leaves()):
@@ -511,14 +522,20 @@ class Reader:
         return out
 
 
-def load_params(p, path: str, layout: Layout, stream=None):
+def load_params(p, path: str, layout: Layout, stream=None, rename=None):
     """A `params M` file's leaves decoded straight into a program's declared
-    inputs of the same names (each in the storage type it was declared in)."""
+    inputs (each in the storage type it was declared in): the buffer of a
+    leaf is its dotted path, or `rename[path]` when given (a stacked leaf
+    into the buffer its layers are held in)."""
     r = Reader(path).with_layout(layout)
     if r.header.count != 1:
         raise DataError("E9005", f"a parameter file holds one tree, not {r.header.count}")
-    names, leaves = layout.names, layout.leaves()
+    names, leaves = layout.paths(), layout.leaves()
+    if rename is not None:
+        names = [rename.get(n, n) for n in names]
     for i, (name, leaf, raw) in enumerate(zip(names, leaves, r.leaf_bytes())):
+        if name not in p.bufs.meta and p.bufs.stacked(name) is not None:
+            p.bufs.alloc(name, *p.bufs.stacked(name))
         if name not in p.bufs.meta:
             raise DataError("E9005", f"the program has no input `{name}`")
         ty, n = p.bufs.meta[name]

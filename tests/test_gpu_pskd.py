@@ -141,6 +141,43 @@ def test_params_file_into_program_buffers(lib, tmp_path):
     assert np.array_equal(prog.bufs.dev["b"].download(np.float32), np.array(b, np.float32))
 
 
+def test_reference_gpt_checkpoint_into_stacked_buffers(lib, tmp_path):
+    """A `params GPT` file in the reference's tree (Block's leaves stacked
+    over the layers, f32 and bf16 leaves) decoded into the GPT program: each
+    stacked leaf lands in the one buffer its layers' inputs are views of."""
+    from presk_amd import gpt
+    from presk_amd.program import numel
+    s = gpt.TINY
+    layout, rename = gpt.params_layout(s)
+    rng = np.random.default_rng(9)
+    encs = [pskd.ENC_BF16 if i % 3 == 1 else pskd.ENC_F32 for i in range(len(layout.leaves()))]
+    values = []
+    for l, e in zip(layout.leaves(), encs):
+        v = (rng.standard_normal(l.numel) * 0.02).astype(np.float32).astype(np.float64)
+        if e is pskd.ENC_BF16:                          # the writer takes numbers of the leaf's format only
+            u = v.astype(np.float32).view(np.uint32).astype(np.uint64)
+            u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)    # nearest even bf16
+            v = u.view(np.float32).astype(np.float64)
+        values.append(list(v))
+    path = str(tmp_path / "gpt.psk.d")
+    pskd.write(path, "params GPT", layout, [values], encs)
+    prog, _, _ = gpt.build(s, "f32", train=False)
+    for n, axes in gpt.param_shapes(s).items():          # the program's parameter inputs, declared
+        prog.declare(n, "f32", numel(axes))
+    pskd.load_params(prog, path, layout, rename=rename)
+    leaves = gpt.opt_leaves(s)
+    for i, (name, (axes, members)) in enumerate(leaves.items()):
+        want = np.array(values[i], np.float64).astype(np.float32)
+        if members is None:
+            assert np.array_equal(prog.bufs.dev[name].download(np.float32), want), name
+            continue
+        per = numel(axes[1:])
+        for l, m in enumerate(members):
+            assert prog.bufs.dev[m].ptr == prog.bufs.dev[name].ptr + 4 * l * per     # a view of the stacked leaf
+            got = prog.bufs.dev[m].download(np.float32)
+            assert np.array_equal(got, want[l * per:(l + 1) * per]), (name, l)
+
+
 def test_description_that_is_no_format_is_refused(lib):
     s = hip.DeviceBuffer(16)
     d = hip.DeviceBuffer(16)

@@ -60,3 +60,20 @@ def test_optimizer_leaves_stack_every_layer():
                 assert parent == n and ty == "f32" and first * s.L == l * total
                 assert p.bufs.views[names["grads"][m]][0] == "d." + n
     assert set(names["adamw"]) == set(leaves)
+
+
+def test_reference_checkpoint_layout_maps_onto_the_program():
+    """`params GPT`'s leaves (a module's params, then its uses; Block's
+    leaves stacked) name every stacked buffer and unstacked parameter once."""
+    s = gpt.TINY
+    layout, rename = gpt.params_layout(s)
+    paths = layout.paths()
+    assert paths[:4] == ["tok", "pos", "head", "blocks.attn.wq.w"] and paths[-2:] == ["lnf.γ", "lnf.β"]
+    names = [rename.get(x, x) for x in paths]
+    assert names == list(gpt.opt_leaves(s))
+    assert [l.shape for l in layout.leaves()][3] == (s.L, s.D, s.D)
+    p, b, _ = gpt.build(s, "f32", train=False)
+    for n, (axes, members) in gpt.opt_leaves(s).items():
+        if members:
+            assert p.bufs.stacked(n) == ("f32", s.L * (p.bufs.views[members[0]][3] // s.L))
+            assert [p.bufs.views[m][1] for m in members] == [l * p.bufs.views[members[0]][3] // s.L for l in range(s.L)]
