@@ -138,7 +138,7 @@ def main():
     ap.add_argument("--realize", default=None, metavar="@FILE",
                     help="a realization file (the reference's schema) for the GPT workloads: storage type per site")
     ap.add_argument("--adamw", action="store_true",
-                    help="config 4 with its optimizer step (adamw.step, f32): the training run's whole step")
+                    help="config 4 with its optimizer step (adamw.step): the training run's whole step")
     ap.add_argument("--dropout", type=float, default=0.0,
                     help="the training step's dropout rate (the course's 0.2): masks drawn on the device, a new "
                          "step key each step")

@@ -529,9 +529,8 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
         G["pos"] = b.embed_vjp("pos", pos_ids, dpe, name="d.pos")
     if optimizer:
         # the training run's step: `value_vjp` then `adamw.step` (crates/presk-train/src/step.rs)
-        if dtype != "f32" or realize is not None:
-            raise ValueError("E7005: the optimizer step is built for f32 storage (a narrower one rounds each "
-                             "unfused let, which its fused chains do not)")
+        if realize is not None:
+            raise ValueError("E7005: the optimizer step is built for one storage type (no mixed realization)")
         names["adamw"] = adamw(b, s, G)
     return p, b, names
 
@@ -627,10 +626,25 @@ def optimizer_inputs(s: GptShape, t: int, total: int, hyper: dict = ADAMW) -> di
     return out
 
 
+def _chain(b: Builder, steps, ins, like, name):
+    """One chain of the step's lets: a fused nest in f32 storage (its f32
+    intermediates are the values the lets store), else one nest a let, each
+    result stored -- rounded -- in the storage type, as the host runs the
+    tree operations one kernel at a time."""
+    if b.dt == "f32":
+        return b.fused(steps, ins, like, name=name)
+    vals = []
+    for k, (op, args) in enumerate(steps):
+        srcs = [ins[i] if kind == "in" else vals[i] for kind, i in args]
+        nm = name if k + 1 == len(steps) else f"{name}.{k}"
+        vals.append(b.binary(op, srcs[0], srcs[1], name=nm) if len(srcs) == 2 else b.unary(op, srcs[0], name=nm))
+    return vals[-1]
+
+
 def _min1(b: Builder, x, name):
     """min(1, x) = 1 - relu(1 - x) (optim.rs's `min1`)."""
-    return b.fused([("sub", [("in", 0), ("in", 1)]), ("relu", [("step", 0)]), ("sub", [("in", 0), ("step", 1)])],
-                   ["opt.one", x], "opt.one", name=name)
+    return _chain(b, [("sub", [("in", 0), ("in", 1)]), ("relu", [("step", 0)]), ("sub", [("in", 0), ("step", 1)])],
+                  ["opt.one", x], "opt.one", name)
 
 
 def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
@@ -641,8 +655,8 @@ def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
     host in leaf order (host.rs:1571-1587) -- here f64 kernels over the
     leaves' f32 scalars, read through the f32 -> f64 edge conversion, whose
     result is read back through the f64 -> f32 one (`scalar`'s rounding).
-    Each leaf's m', v' and theta' are one fused chain each: in f32 storage a
-    chain's f32 intermediates are the values the unfused lets store.
+    Each leaf's m', v' and theta' are one chain each (`_chain`: fused in f32
+    storage, one nest a let in a narrower one).
     The leaves are `opt_leaves`: a stacked leaf's parameters and gradients
     are its layers' buffers, held one after another in one buffer
     (Program.stack), as StackParams lays them out.
@@ -658,7 +672,7 @@ def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
             count *= a.len
         if b.p.bufs.views.get(members[0], ("",))[0] != n:
             raise ValueError(f"E7005: the layers of `{n}` are not held in one buffer")
-        b.p.stack("d." + n, [grads[m] for m in members], "f32", count)
+        b.p.stack("d." + n, [grads[m] for m in members], b.dt, count)
         b.input(n, axes)
         grads[n] = b.input("d." + n, axes)
     for k in list(_OPT_LITS) + ["opt.pi", "opt.t", "opt.total"]:
@@ -677,41 +691,41 @@ def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
             steps = [("add", [("in", 0), ("in", 1)])] + [("add", [("step", k), ("in", k + 2)]) for k in range(len(ins) - 2)]
             name = f"opt.n2.{i // _SUM_CHUNK}"
             acc = b._out(L.fused(steps, [b.op(x) for x in ins], [], "f64"), ins, name)
-        norm = b.fused([("sqrt", [("in", 0)]), ("add", [("step", 0), ("in", 1)]), ("div", [("in", 2), ("step", 1)])],
-                       [acc, "opt.tiny", "opt.clip"], "opt.one", name="opt.coef")
+        norm = _chain(b, [("sqrt", [("in", 0)]), ("add", [("step", 0), ("in", 1)]), ("div", [("in", 2), ("step", 1)])],
+                       [acc, "opt.tiny", "opt.clip"], "opt.one", "opt.coef")
         factor = _min1(b, norm, "opt.factor")
-        omb = b.fused([("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b1"], "opt.one", name="opt.omb1")
-        omb2 = b.fused([("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b2"], "opt.one", name="opt.omb2")
+        omb = _chain(b, [("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b1"], "opt.one", "opt.omb1")
+        omb2 = _chain(b, [("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b2"], "opt.one", "opt.omb2")
         # bias corrections 1 - beta^t = 1 - exp(t * ln beta)
-        bc = [b.fused([("log", [("in", 1)]), ("mul", [("in", 2), ("step", 0)]), ("exp", [("step", 1)]),
-                       ("sub", [("in", 0), ("step", 2)])], ["opt.one", beta, "opt.t"], "opt.one", name=f"opt.bc{i + 1}")
+        bc = [_chain(b, [("log", [("in", 1)]), ("mul", [("in", 2), ("step", 0)]), ("exp", [("step", 1)]),
+                       ("sub", [("in", 0), ("step", 2)])], ["opt.one", beta, "opt.t"], "opt.one", f"opt.bc{i + 1}")
               for i, beta in enumerate(("opt.b1", "opt.b2"))]
     with b.func("adamw.lr"):
         # cosine(warmup = w): lr * min(1, t/w) * (1 + cos(pi * min(1, relu((t - w) / (relu(total - w - 1) + 1))))) / 2
-        q = b.fused([("div", [("in", 0), ("in", 1)])], ["opt.t", "opt.w"], "opt.one", name="opt.q")
+        q = _chain(b, [("div", [("in", 0), ("in", 1)])], ["opt.t", "opt.w"], "opt.one", "opt.q")
         warm = _min1(b, q, "opt.warm")
-        r = b.fused([("sub", [("in", 0), ("in", 2)]), ("sub", [("in", 1), ("in", 2)]), ("sub", [("step", 1), ("in", 3)]),
+        r = _chain(b, [("sub", [("in", 0), ("in", 2)]), ("sub", [("in", 1), ("in", 2)]), ("sub", [("step", 1), ("in", 3)]),
                      ("relu", [("step", 2)]), ("add", [("step", 3), ("in", 3)]), ("div", [("step", 0), ("step", 4)]),
-                     ("relu", [("step", 5)])], ["opt.t", "opt.total", "opt.w", "opt.one"], "opt.one", name="opt.r")
+                     ("relu", [("step", 5)])], ["opt.t", "opt.total", "opt.w", "opt.one"], "opt.one", "opt.r")
         prog = _min1(b, r, "opt.p")
-        lr = b.fused([("mul", [("in", 0), ("in", 1)]), ("cos", [("step", 0)]), ("add", [("in", 2), ("step", 1)]),
+        lr = _chain(b, [("mul", [("in", 0), ("in", 1)]), ("cos", [("step", 0)]), ("add", [("in", 2), ("step", 1)]),
                       ("mul", [("step", 2), ("in", 3)]), ("mul", [("in", 4), ("step", 3)]), ("mul", [("in", 5), ("step", 4)])],
-                     ["opt.pi", prog, "opt.one", "opt.half", warm, "opt.lr"], "opt.one", name="opt.lr_t")
+                     ["opt.pi", prog, "opt.one", "opt.half", warm, "opt.lr"], "opt.one", "opt.lr_t")
     with b.func("adamw.step"):
         for n in names:
             g, m, v = grads[n], "m." + n, "v." + n
             # m' = m b1 + (g factor)(1 - b1)
-            m2 = b.fused([("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("in", 4)]),
-                          ("add", [("step", 1), ("step", 2)])], [g, factor, m, "opt.b1", omb], n, name=f"opt.m2.{n}")
+            m2 = _chain(b, [("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("in", 4)]),
+                          ("add", [("step", 1), ("step", 2)])], [g, factor, m, "opt.b1", omb], n, f"opt.m2.{n}")
             # v' = v b2 + (g factor)^2 (1 - b2)
-            v2 = b.fused([("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("step", 0)]),
+            v2 = _chain(b, [("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("step", 0)]),
                           ("mul", [("step", 2), ("in", 4)]), ("add", [("step", 1), ("step", 3)])],
-                         [g, factor, v, "opt.b2", omb2], n, name=f"opt.v2.{n}")
+                         [g, factor, v, "opt.b2", omb2], n, f"opt.v2.{n}")
             # theta' = theta - lr (m'/bc1 / (sqrt(v'/bc2) + eps) + lambda theta)
-            th = b.fused([("div", [("in", 1), ("in", 2)]), ("div", [("in", 3), ("in", 4)]), ("sqrt", [("step", 1)]),
+            th = _chain(b, [("div", [("in", 1), ("in", 2)]), ("div", [("in", 3), ("in", 4)]), ("sqrt", [("step", 1)]),
                           ("add", [("step", 2), ("in", 5)]), ("div", [("step", 0), ("step", 3)]), ("mul", [("in", 0), ("in", 6)]),
                           ("add", [("step", 4), ("step", 5)]), ("mul", [("step", 6), ("in", 7)]), ("sub", [("in", 0), ("step", 7)])],
-                         [n, m2, bc[0], v2, bc[1], "opt.eps", "opt.wd", lr], n, name=f"opt.theta.{n}")
+                         [n, m2, bc[0], v2, bc[1], "opt.eps", "opt.wd", lr], n, f"opt.theta.{n}")
             out[n] = (th, m2, v2)
     return out
 

@@ -109,22 +109,25 @@ def test_dropout_step_graph_takes_each_steps_key():
             assert p.bufs.download(name).tobytes() == env[name].tobytes(), (step, name)
 
 
-def test_tiny_gpt_step_with_adamw_exact_bits():
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_tiny_gpt_step_with_adamw_exact_bits(dt):
     """the training run's step with its optimizer (adamw.step, f32): the
     clipped global norm summed in f64 through the edge conversions, the
     schedule and bias corrections as 0-dim kernels, every leaf's moments
-    and parameters (the blocks' leaves stacked over the layers) -- every
-    buffer equal to the oracle's, replayed as a graph too"""
+    and parameters (the blocks' leaves stacked over the layers; in bf16
+    storage every let its own rounded nest) -- every buffer equal to the
+    oracle's, replayed as a graph too"""
     s = gpt.TINY
-    p, b, names = gpt.build(s, "f32", train=True, mode=hip.EXACT, optimizer=True)
+    p, b, names = gpt.build(s, dt, train=True, mode=hip.EXACT, optimizer=True)
     host = gpt.host_inputs(s)
     host.update(gpt.optimizer_inputs(s, 150, 400))
     device_run(p, host)
     # the blocks' parameters and gradients sit in their stacked leaves, no copy
     for l in range(s.L):
-        assert p.bufs.dev[f"b{l}.wq"].ptr == p.bufs.dev["blocks.wq"].ptr + 4 * l * s.D * s.D
-        assert p.bufs.dev[names["grads"][f"b{l}.up.b"]].ptr == p.bufs.dev["d.blocks.up.b"].ptr + 4 * l * 4 * s.D
-    q, _, _ = gpt.build(s, "f32", train=True, mode=hip.EXACT, optimizer=True)
+        w = 4 if dt == "f32" else 2
+        assert p.bufs.dev[f"b{l}.wq"].ptr == p.bufs.dev["blocks.wq"].ptr + w * l * s.D * s.D
+        assert p.bufs.dev[names["grads"][f"b{l}.up.b"]].ptr == p.bufs.dev["d.blocks.up.b"].ptr + w * l * 4 * s.D
+    q, _, _ = gpt.build(s, dt, train=True, mode=hip.EXACT, optimizer=True)
     env = cpu_program.run(q, host)
     outs = [ln.out for ln in p.launches]
     bad = [n for n in outs if p.bufs.download(n).tobytes() != env[n].tobytes()]
