@@ -585,26 +585,11 @@ def params_layout(s: GptShape):
     (opt_leaves), Block's leaves stacked, and the program buffer of each
     leaf's dotted path (`blocks.attn.wq.w` -> the stacked `blocks.wq`)."""
     from .pskd import Layout, Leaf
-
-    def rec(pairs):
-        return Layout.record([(k, v) for k, v in pairs])
-    leaves = opt_leaves(s)
-    shape = lambda n: tuple(a.len for a in leaves[n][0])
-    tree = {}
-    for r, path in _BLOCK_PATHS.items():
-        node = tree
-        parts = path.split(".")
-        for q in parts[:-1]:
-            node = node.setdefault(q, {})
-        node[parts[-1]] = Leaf(shape("blocks." + r))
-
-    def build(node):
-        return rec([(k, build(v) if isinstance(v, dict) else v) for k, v in node.items()])
-    layout = rec([("tok", Leaf(shape("tok"))), ("pos", Leaf(shape("pos"))), ("head", Leaf(shape("head"))),
-                  ("blocks", build(tree)), ("lnf", rec([("γ", Leaf(shape("lnf.g"))), ("β", Leaf(shape("lnf.b")))]))])
     rename = {"blocks." + path: "blocks." + r for r, path in _BLOCK_PATHS.items()}
     rename.update({"lnf.γ": "lnf.g", "lnf.β": "lnf.b"})
-    return layout, rename
+    back = {v: k for k, v in rename.items()}
+    pairs = [(back.get(n, n), Leaf(tuple(a.len for a in axes))) for n, (axes, _) in opt_leaves(s).items()]
+    return Layout.from_paths(pairs), rename
 
 
 def optimizer_inputs(s: GptShape, t: int, total: int, hyper: dict = ADAMW) -> dict:

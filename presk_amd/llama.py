@@ -229,6 +229,45 @@ def _swiglu(b: Builder, pr, x):
             return b.dot(m, pr + "ff.down", name=pr + "down")
 
 
+# a Block leaf here -> its path under `blocks` in `params Llama`: Attention's
+# params wq, wk, wv, wo; SwiGLU's uses gate, up, down (Dense's param w);
+# RMSNorm's param gamma (llama.psk:29-118)
+_BLOCK_PATHS = {"attn.wq": "attn.wq", "attn.wk": "attn.wk", "attn.wv": "attn.wv", "attn.wo": "attn.wo",
+                "ff.gate": "ff.gate.w", "ff.up": "ff.up.w", "ff.down": "ff.down.w", "n1.g": "n1.γ", "n2.g": "n2.γ"}
+
+
+def _count(axes) -> int:
+    n = 1
+    for a in axes:
+        n *= a.len
+    return n
+
+
+def leaves(s: LlamaShape) -> dict:
+    """`params Llama`'s leaves in order -- a module's params, then its uses,
+    each in declaration order (crates/presk-types/src/elab/mod.rs:191-203):
+    tok, head, blocks (`stack{L}(Block)`, each leaf with a leading layer
+    axis), norm (llama.psk:120-130).  name -> (axes, the per-layer
+    parameters a stacked leaf holds, or None)."""
+    ps = param_shapes(s)
+    out = {"tok": (ps["tok"], None), "head": (ps["head"], None)}
+    for r in _BLOCK_PATHS:
+        out["blocks." + r] = ([L.Axis("layer", s.L)] + ps["b0." + r], [f"b{l}.{r}" for l in range(s.L)])
+    out["norm.g"] = (ps["norm.g"], None)
+    return out
+
+
+def params_layout(s: LlamaShape):
+    """(layout, rename) of a `params Llama` file: its tree (Block's leaves
+    stacked) and the program buffer of each leaf's dotted path."""
+    from .pskd import Layout, Leaf
+    rename = {"blocks." + path: "blocks." + r for r, path in _BLOCK_PATHS.items()}
+    rename["norm.γ"] = "norm.g"
+    back = {v: k for k, v in rename.items()}
+    pairs = [(back.get(n, n), Leaf(tuple(a.len for a in axes))) for n, (axes, _) in leaves(s).items()]
+    return Layout.from_paths(pairs), rename
+
+
 def build(s: LlamaShape, dtype: str = "bf16", mode=None, realize=None) -> tuple:
     """The program of `Llama.apply` (the logits).  Returns (program,
     builder, names) with names["logits"]."""
@@ -241,6 +280,12 @@ def build(s: LlamaShape, dtype: str = "bf16", mode=None, realize=None) -> tuple:
             p.input_types[name] = realize.param_dtype(name)
     for name, axes in param_shapes(s).items():
         b.input(name, axes)
+    # each block parameter's layers held in one stacked buffer, as `params
+    # Llama` stores them (a checkpoint's leaf decodes straight into it)
+    for n, (axes, members) in leaves(s).items():
+        tys = {p.input_types.get(m, dtype if realize is None else None) for m in members or []}
+        if members and len(tys) == 1 and None not in tys:
+            p.stack(n, members, tys.pop(), _count(axes[1:]))
     b.input("ids", A(("batch", s.B), ("seq", s.T)), "idx")
     for name in SCALARS:
         b.input(name, A())

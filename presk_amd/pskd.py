@@ -232,6 +232,22 @@ class Layout:
     def record(fields: list) -> "Layout":
         return Layout(items=[l if isinstance(l, Layout) else Layout(l) for _, l in fields], names=[n for n, _ in fields])
 
+    @staticmethod
+    def from_paths(pairs: list) -> "Layout":
+        """The record tree of (dotted path, Leaf) pairs given in leaf order
+        (`params M`'s leaves: `blocks.attn.wq`, …)."""
+        root: dict = {}
+        for path, leaf in pairs:
+            node = root
+            parts = path.split(".")
+            for q in parts[:-1]:
+                node = node.setdefault(q, {})
+            node[parts[-1]] = leaf
+
+        def build(node):
+            return Layout.record([(k, build(v) if isinstance(v, dict) else v) for k, v in node.items()])
+        return build(root)
+
     def leaves(self) -> list:
         if self.leaf is not None:
             return [self.leaf]

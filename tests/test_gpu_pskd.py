@@ -141,14 +141,17 @@ def test_params_file_into_program_buffers(lib, tmp_path):
     assert np.array_equal(prog.bufs.dev["b"].download(np.float32), np.array(b, np.float32))
 
 
-def test_reference_gpt_checkpoint_into_stacked_buffers(lib, tmp_path):
-    """A `params GPT` file in the reference's tree (Block's leaves stacked
-    over the layers, f32 and bf16 leaves) decoded into the GPT program: each
-    stacked leaf lands in the one buffer its layers' inputs are views of."""
-    from presk_amd import gpt
+@pytest.mark.parametrize("model", ["gpt", "llama"])
+def test_reference_checkpoint_into_stacked_buffers(lib, tmp_path, model):
+    """A `params GPT` / `params Llama` file in the reference's tree (Block's
+    leaves stacked over the layers, f32 and bf16 leaves) decoded into the
+    program: each stacked leaf lands in the one buffer its layers' inputs
+    are views of."""
+    from presk_amd import gpt, llama
     from presk_amd.program import numel
-    s = gpt.TINY
-    layout, rename = gpt.params_layout(s)
+    mod = gpt if model == "gpt" else llama
+    s = mod.TINY
+    layout, rename = mod.params_layout(s)
     rng = np.random.default_rng(9)
     encs = [pskd.ENC_BF16 if i % 3 == 1 else pskd.ENC_F32 for i in range(len(layout.leaves()))]
     values = []
@@ -159,13 +162,13 @@ def test_reference_gpt_checkpoint_into_stacked_buffers(lib, tmp_path):
             u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)    # nearest even bf16
             v = u.view(np.float32).astype(np.float64)
         values.append(list(v))
-    path = str(tmp_path / "gpt.psk.d")
-    pskd.write(path, "params GPT", layout, [values], encs)
-    prog, _, _ = gpt.build(s, "f32", train=False)
-    for n, axes in gpt.param_shapes(s).items():          # the program's parameter inputs, declared
+    path = str(tmp_path / "theta.psk.d")
+    pskd.write(path, "params GPT" if model == "gpt" else "params Llama", layout, [values], encs)
+    prog = gpt.build(s, "f32", train=False)[0] if model == "gpt" else llama.build(s, "f32")[0]
+    for n, axes in mod.param_shapes(s).items():          # the program's parameter inputs, declared
         prog.declare(n, "f32", numel(axes))
     pskd.load_params(prog, path, layout, rename=rename)
-    leaves = gpt.opt_leaves(s)
+    leaves = gpt.opt_leaves(s) if model == "gpt" else llama.leaves(s)
     for i, (name, (axes, members)) in enumerate(leaves.items()):
         want = np.array(values[i], np.float64).astype(np.float32)
         if members is None:

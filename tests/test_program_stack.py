@@ -77,3 +77,18 @@ def test_reference_checkpoint_layout_maps_onto_the_program():
         if members:
             assert p.bufs.stacked(n) == ("f32", s.L * (p.bufs.views[members[0]][3] // s.L))
             assert [p.bufs.views[m][1] for m in members] == [l * p.bufs.views[members[0]][3] // s.L for l in range(s.L)]
+
+
+def test_llama_checkpoint_layout_maps_onto_the_program():
+    """`params Llama`: tok, head (its params), blocks, norm (its uses); every
+    block leaf stacked over the layers in the program."""
+    from presk_amd import llama
+    s = llama.TINY
+    layout, rename = llama.params_layout(s)
+    paths = layout.paths()
+    assert paths[:3] == ["tok", "head", "blocks.attn.wq"] and paths[-1] == "norm.γ"
+    assert [rename.get(x, x) for x in paths] == list(llama.leaves(s))
+    p, _, _ = llama.build(s, "bf16")
+    for n, (axes, members) in llama.leaves(s).items():
+        if members:
+            assert p.bufs.stacked(n)[0] == "bf16" and [p.bufs.views[m][0] for m in members] == [n] * s.L
