@@ -17,8 +17,31 @@
  *   ok_tanhf  follows presk_libm.c:1915-1998 (s_tanhf)
  *   ok_erff   follows presk_libm.c:2542-2680 (s_erff)
  *
- * Pinned by tests/test_oracle_libm.py: every f32 input, digest against the
+ * Pinned by tests/test_oracle_scalar.py: every f32 input, digest against the
  * reference's C compiled into oracle/_ref.
+ *
+ * Notices.  The method, constants and operation order restated here are
+ * those of the following sources, whose terms ask that these notices be
+ * kept with any work derived from them:
+ *
+ *   musl libc 1.1.22 -- Copyright (c) 2005-2014 Rich Felker, et al.
+ *   Permission is hereby granted, free of charge, to any person obtaining
+ *   a copy of this software and associated documentation files (the
+ *   "Software"), to deal in the Software without restriction, including
+ *   without limitation the rights to use, copy, modify, merge, publish,
+ *   distribute, sublicense, and/or sell copies of the Software, and to
+ *   permit persons to whom the Software is furnished to do so, subject to
+ *   the following conditions: The above copyright notice and this
+ *   permission notice shall be included in all copies or substantial
+ *   portions of the Software.  THE SOFTWARE IS PROVIDED "AS IS", WITHOUT
+ *   WARRANTY OF ANY KIND, EXPRESS OR IMPLIED.
+ *
+ *   fdlibm (via FreeBSD msun) -- Copyright (C) 1993 by Sun Microsystems,
+ *   Inc. All rights reserved.  Developed at SunPro, a Sun Microsystems,
+ *   Inc. business.  Permission to use, copy, modify, and distribute this
+ *   software is freely granted, provided that this notice is preserved.
+ *   (The f32 conversions of these functions are by Ian Lance Taylor,
+ *   Cygnus Support, and Bruce D. Evans, under the same terms.)
  */
 #include <stdint.h>
 #include <string.h>

@@ -21,6 +21,29 @@
 //
 // Each is checked over every f32 input on the GPU against the reference's
 // compiled C (tests/test_gpu_scalar.py, digests in tests/golden/digests.json).
+//
+// Notices.  The method, constants and operation order restated here are
+// those of the following sources, whose terms ask that these notices be
+// kept with any work derived from them:
+//
+//   musl libc 1.1.22 -- Copyright (c) 2005-2014 Rich Felker, et al.
+//   Permission is hereby granted, free of charge, to any person obtaining
+//   a copy of this software and associated documentation files (the
+//   "Software"), to deal in the Software without restriction, including
+//   without limitation the rights to use, copy, modify, merge, publish,
+//   distribute, sublicense, and/or sell copies of the Software, and to
+//   permit persons to whom the Software is furnished to do so, subject to
+//   the following conditions: The above copyright notice and this
+//   permission notice shall be included in all copies or substantial
+//   portions of the Software.  THE SOFTWARE IS PROVIDED "AS IS", WITHOUT
+//   WARRANTY OF ANY KIND, EXPRESS OR IMPLIED.
+//
+//   fdlibm (via FreeBSD msun) -- Copyright (C) 1993 by Sun Microsystems,
+//   Inc. All rights reserved.  Developed at SunPro, a Sun Microsystems,
+//   Inc. business.  Permission to use, copy, modify, and distribute this
+//   software is freely granted, provided that this notice is preserved.
+//   (The f32 conversions of these functions are by Ian Lance Taylor,
+//   Cygnus Support, and Bruce D. Evans, under the same terms.)
 #pragma once
 
 #define PK_DEV __device__ __forceinline__

@@ -647,19 +647,6 @@ def reduce_all(op, ins, dtype) -> Lowered:
     return kernel(op, dtype, ins, [], "real", bd, body)
 
 
-def sum_squares(ins, dtype) -> Lowered:
-    """lower.rs:1693-1703: every element's square added in index order from
-    zero (Accum and Product, printed + and *), one scalar out."""
-    t = ins[0]
-    bd = B()
-    v = bd.loops(dims(t.axes))
-    acc = bd.sv()
-    x = load(0, ivs(v))
-    body = [Set(acc, num(0))] + nest(v, dims(t.axes), [Set(acc, bin_("+", sv(acc), bin_("*", x, x)))])
-    body.append(Store(1, [], sv(acc)))
-    return kernel("sum_squares", dtype, ins, [], "real", bd, body)
-
-
 def reduce_axis(op, axis, ins, dtype) -> Lowered:
     """lower.rs:1239-1255 (`sum axis a`/`mean axis a`)."""
     t = ins[0]
