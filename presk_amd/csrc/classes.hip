@@ -113,13 +113,13 @@ struct GemmPlan : ClassPlan {
     bool epilogue = false;
     int n_in = 2;
     bool guarded = false;
-    int64_t split_bound = -1;  // the KernelFn split loop's bound
+    // what one iteration of the KernelFn split loop covers: a batch entry
+    // (the first batch axis), rows_per_iter rows of M, or cols_per_iter
+    // columns of N (an `ein` whose first output axis is J)
     bool split_on_batch = false;
     bool swapped = false;          // operand 1 is A (an `ein` whose operand 1 carries I)
-    bool whole_only = false;       // no partial range of the split loop (an `ein` whose first axis is J)
-    long long rows_per_iter = 0;   // M rows (or batch entries) one outer iteration covers
-    mutable float* work = nullptr;
-    mutable size_t work_floats = 0;
+    long long rows_per_iter = 0;
+    long long cols_per_iter = 0;
 
     const char* kind() const override { return "gemm"; }
     std::string order() const override {
@@ -127,8 +127,15 @@ struct GemmPlan : ClassPlan {
         if (g.splits > 1) o += "-split" + std::to_string(g.splits);
         return o;
     }
+    // split-K partials, [splits][M][N] in f32
+    size_t workspace_bytes() const override {
+        return g.splits > 1 ? (size_t)g.splits * (size_t)g.M * (size_t)g.N * sizeof(float) : 0;
+    }
 
-    hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, hipStream_t stream) const override {
+    hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const override {
+        int64_t first, count;
+        if (!range(lo, hi, &first, &count)) return hipErrorInvalidValue;
+        if (count == 0) return hipSuccess;
         GemmArgs a = g;
         a.A = bufs[swapped ? 1 : 0];
         a.B = bufs[swapped ? 0 : 1];
@@ -136,24 +143,30 @@ struct GemmPlan : ClassPlan {
         a.C = bufs[n_in];
         a.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
         const int esz = storage == kF32 ? 4 : 2;
-        if (split_bound >= 0 && !(lo == 0 && hi == split_bound)) {
-            if (lo < 0 || hi > split_bound || lo > hi) return hipErrorInvalidValue;
-            if (lo == hi) return hipSuccess;
-            if (whole_only) return hipErrorInvalidValue;
+        // a partial range: the same tiles, k-blocks and split of K as the
+        // whole call, over fewer batch entries, rows or columns -- each
+        // element is summed by the same steps, so its bits do not change
+        if (count > 0 && count < split) {
             if (split_on_batch) {
-                a.A = (const char*)a.A + lo * a.sa_b[0] * esz;
-                a.B = (const char*)a.B + lo * a.sb_b[0] * esz;
-                a.C = (char*)a.C + lo * a.sc_b[0] * esz;
-                a.batch = a.batch / a.bdim[0] * (hi - lo);
-                a.bdim[0] = hi - lo;
+                a.A = (const char*)a.A + first * a.sa_b[0] * esz;
+                a.B = (const char*)a.B + first * a.sb_b[0] * esz;
+                a.C = (char*)a.C + first * a.sc_b[0] * esz;
+                a.batch = a.batch / a.bdim[0] * count;
+                a.bdim[0] = count;
+            } else if (cols_per_iter > 0) {
+                const long long n0 = first * cols_per_iter;
+                a.B = (const char*)a.B + n0 * a.sb_n * esz;
+                a.C = (char*)a.C + n0 * esz;
+                if (a.bias && a.bias_kind == 1) a.bias = (const char*)a.bias + n0 * esz;
+                a.N = count * cols_per_iter;
+                a.tiles_n = (int)((a.N + a.bn - 1) / a.bn);
             } else {
-                const long long m0 = lo * rows_per_iter;
+                const long long m0 = first * rows_per_iter;
                 a.A = (const char*)a.A + m0 * a.sa_m * esz;
                 a.C = (char*)a.C + m0 * a.sc_m * esz;
-                a.M = (hi - lo) * rows_per_iter;
-                a.tiles_m = (int)((a.M + gemm_tile_m() - 1) / gemm_tile_m());
                 if (a.bias && a.bias_kind == 2) a.bias = (const char*)a.bias + m0 * a.N * esz;
-                if (a.splits > 1) return hipErrorInvalidValue;  // a partial range of a split-K plan
+                a.M = count * rows_per_iter;
+                a.tiles_m = (int)((a.M + gemm_tile_m() - 1) / gemm_tile_m());
             }
         }
         // the clamped 16-byte loads need whole aligned vectors along the
@@ -170,33 +183,10 @@ struct GemmPlan : ClassPlan {
         a.a_vec = aligned(a.A, a.a_kcontig, a.M, a.a_kcontig ? a.sa_m : a.sa_k, a.sa_b);
         a.b_vec = aligned(a.B, a.b_kcontig, a.N, a.b_kcontig ? a.sb_n : a.sb_k, a.sb_b);
         if (a.splits > 1) {
-            const size_t need = (size_t)a.splits * a.M * a.N;
-            if (need > work_floats) {
-                if (work) hipFree(work);
-                work = nullptr;
-                hipError_t e = hipMalloc(&work, need * sizeof(float));
-                if (e != hipSuccess) return e;
-                work_floats = need;
-            }
-            a.work = work;
+            if (!work) return hipErrorInvalidValue;
+            a.work = (float*)work;
         }
         return gemm_launch(a, stream);
-    }
-
-    hipError_t prepare() const override {
-        if (g.splits <= 1) return hipSuccess;
-        const size_t need = (size_t)g.splits * g.M * g.N;
-        if (need <= work_floats) return hipSuccess;
-        if (work) hipFree(work);
-        work = nullptr;
-        work_floats = 0;
-        hipError_t e = hipMalloc(&work, need * sizeof(float));
-        if (e == hipSuccess) work_floats = need;
-        return e;
-    }
-
-    ~GemmPlan() override {
-        if (work) hipFree(work);
     }
 };
 
@@ -282,7 +272,7 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     p->epilogue = epi;
     p->n_in = (int)k.inputs.size();
     p->guarded = k.guarded();
-    p->split_bound = parallel_outer(k);
+    p->nest = parallel_outer(k);
     if (is_dot) {
         // x[outer..., I, K] . w[K, J] -> [outer..., I, J]   (Contraction::of, lower.rs:700-711)
         if (w.dims.size() != 2 || x.dims.size() < 2 || x.dims.back() != w.dims[0]) return nullptr;
@@ -439,10 +429,10 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
             g.batch *= bd[q];
         }
         // a partial range of the split loop (the first output axis): a batch
-        // range, a row range, or (J first) not offered
+        // range, a row range, or a column range (J first)
         p->split_on_batch = first_is_batch;
         p->rows_per_iter = vo[0] == vi ? 1 : 0;
-        p->whole_only = !first_is_batch && vo[0] != vi;
+        p->cols_per_iter = !first_is_batch && vo[0] == vj ? 1 : 0;
     }
     if (epi) {
         if (g.sc_m != g.N) return nullptr;
@@ -472,6 +462,15 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     const double lim = 2147483647.0;
     if ((double)g.M * g.N > lim || (double)g.M * g.sc_m > lim || (double)g.M * g.K > lim || (double)g.K * g.N > lim ||
         (double)x.numel() > lim || (double)w.numel() > lim) return nullptr;
+    // the split loop the plan honours partial ranges of: the output's first
+    // axis, as one batch entry, rows_per_iter whole rows or one column each
+    const long long n0 = p->nest;
+    if (n0 > 0 && !o.dims.empty() && o.dims[0] == n0) {
+        if (p->split_on_batch ? g.nbatch > 0 && g.bdim[0] == n0
+                              : p->cols_per_iter > 0 ? g.N == n0 && g.bias_kind != 2
+                                                     : p->rows_per_iter > 0 && g.M == n0 * p->rows_per_iter)
+            p->split = n0;
+    }
     return p;
 }
 
@@ -479,26 +478,31 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
 struct ColSumPlan : ClassPlan {
     ColSumArgs a{};
     bool guarded = false;
-    mutable float* work = nullptr;
+    int n_in = 2;
+    long long cols_per_iter = 0;   // output columns one iteration of the split loop covers
     const char* kind() const override { return "colsum"; }
     std::string order() const override { return "chunked(" + std::to_string(a.chunk) + ")-f32"; }
-    int n_in = 2;
-    hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
+    // the chunk sums, [nchunks][cols] in f32
+    size_t workspace_bytes() const override { return sizeof(float) * (size_t)(a.nchunks * a.cols); }
+    hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const override {
+        int64_t first, count;
+        if (!range(lo, hi, &first, &count)) return hipErrorInvalidValue;
+        if (count == 0) return hipSuccess;
+        if (!work) return hipErrorInvalidValue;
         ColSumArgs x = a;
+        const int esz = a.storage == 0 ? 4 : 2;
         x.x = bufs[0];
         x.out = bufs[n_in];
         x.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
-        hipError_t e = prepare();
-        if (e != hipSuccess) return e;
-        x.work = work;
+        x.work = (float*)work;
+        if (count > 0 && count < split) {
+            // columns [c0, c0 + count * cols_per_iter) of every row
+            const long long c0 = first * cols_per_iter;
+            x.x = (const char*)x.x + c0 * esz;
+            x.out = (char*)x.out + c0 * esz;
+            x.cols = count * cols_per_iter;
+        }
         return colsum_launch(x, stream);
-    }
-    hipError_t prepare() const override {
-        if (work) return hipSuccess;
-        return hipMalloc(&work, sizeof(float) * (size_t)(a.nchunks * a.cols));
-    }
-    ~ColSumPlan() override {
-        if (work) hipFree(work);
     }
 };
 
@@ -519,7 +523,9 @@ std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
         p->a.div = k.name == "mean_all" ? (float)(double)p->a.rows : 0.f;
         p->a.square = squares ? 1 : 0;
         p->a.storage = st;
+        p->a.ld = 1;
         p->guarded = k.guarded();
+        p->nest = parallel_outer(k);
         return p;
     }
     if (k.name != "sum_to" || k.inputs.size() != 2) return nullptr;
@@ -538,7 +544,15 @@ std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
     p->a.nchunks = (p->a.rows + p->a.chunk - 1) / p->a.chunk;
     if (p->a.nchunks > 65535) return nullptr;  // one grid row per chunk
     p->a.storage = st;
+    p->a.ld = p->a.cols;
     p->guarded = k.guarded();
+    // the split loop runs over the output's first axis, each iteration a
+    // run of whole trailing columns
+    p->nest = parallel_outer(k);
+    if (p->nest > 0 && o.dims[0] == p->nest && p->a.cols % p->nest == 0) {
+        p->split = p->nest;
+        p->cols_per_iter = p->a.cols / p->nest;
+    }
     return p;
 }
 
@@ -547,26 +561,39 @@ struct RowPlan : ClassPlan {
     RowArgs a{};
     int n_in = 1;
     bool guarded = false;
-    mutable unsigned* mbits = nullptr;   // the mask as bits (long masked rows)
+    long long rows_per_iter = 0;   // rows one iteration of the split loop covers
+    bool row_out = false;          // one output element a row (a sum, a mean, a loss)
     const char* kind() const override { return "rows"; }
     std::string order() const override { return "sequential"; }
-    hipError_t prepare() const override {
-        if (mbits || !rows_need_mask_bits(a)) return hipSuccess;
-        return hipMalloc(&mbits, (size_t)a.mask_rows * rows_mask_words(a.n) * sizeof(unsigned));
+    // the mask as bits (masked softmax over long rows), [mask_rows][words]
+    size_t workspace_bytes() const override {
+        return rows_need_mask_bits(a) ? (size_t)a.mask_rows * rows_mask_words(a.n) * sizeof(unsigned) : 0;
     }
-    ~RowPlan() override {
-        if (mbits) hipFree(mbits);
-    }
-    hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
-        if (hipError_t e = prepare(); e != hipSuccess) return e;
+    hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const override {
+        int64_t first, count;
+        if (!range(lo, hi, &first, &count)) return hipErrorInvalidValue;
+        if (count == 0) return hipSuccess;
         RowArgs x = a;
-        x.mbits = mbits;
+        const int esz = a.storage == 0 ? 4 : 2;
         x.x = bufs[0];
         if (a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2) x.mask = bufs[1];
         if (a.op == kCrossEntropy || a.op == kCrossEntropyVjp) x.y = bufs[1];
         if (a.op == kCrossEntropyVjp) x.ct = bufs[2];
         x.out = bufs[n_in];
         x.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
+        if (count > 0 && count < split) {
+            // rows [r0, r0 + count * rows_per_iter): the mask row of row r is
+            // still r mod mask_rows
+            const long long r0 = first * rows_per_iter;
+            x.rows = count * rows_per_iter;
+            x.x = (const char*)x.x + r0 * a.n * esz;
+            x.out = (char*)x.out + (row_out ? r0 : r0 * a.n) * esz;
+            if (x.y) x.y = (const long long*)x.y + r0;
+            if (x.ct) x.ct = (const char*)x.ct + r0 * esz;
+            if (a.mask_rows > 0) x.mask_row0 = r0 % a.mask_rows;
+        }
+        x.mbits = rows_need_mask_bits(x) ? (unsigned*)work : nullptr;
+        if (rows_need_mask_bits(x) && !work) return hipErrorInvalidValue;
         return rows_launch(x, stream);
     }
 };
@@ -636,6 +663,15 @@ std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
         return nullptr;
     }
     if (k.output.ty != k.dtype) return nullptr;
+    // the split loop runs over x's first axis (and the output's), each
+    // iteration a run of whole rows
+    p->row_out = p->a.op == kRowMean || p->a.op == kRowSum || p->a.op == kSumToRows || p->a.op == kCrossEntropy;
+    p->nest = parallel_outer(k);
+    if (p->nest > 0 && x.dims[0] == p->nest && !k.output.dims.empty() && k.output.dims[0] == p->nest &&
+        p->a.rows % p->nest == 0) {
+        p->split = p->nest;
+        p->rows_per_iter = p->a.rows / p->nest;
+    }
     return p;
 }
 
@@ -650,7 +686,11 @@ struct ScatterPlan : ClassPlan {
     bool guarded = false;
     const char* kind() const override { return "scatter"; }
     std::string order() const override { return "sequential"; }
-    hipError_t launch(void* const* bufs, int64_t, int64_t, hipStream_t stream) const override {
+    // the nest zeroes its output before the scatter, so it has no split loop
+    // (crates/presk-kernel/src/ir.rs:336-376): only whole calls
+    hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void*, hipStream_t stream) const override {
+        int64_t first, count;
+        if (!range(lo, hi, &first, &count)) return hipErrorInvalidValue;
         ScatterArgs x = a;
         x.idx = (const long long*)bufs[1];
         x.ct = bufs[2];
@@ -674,11 +714,15 @@ std::unique_ptr<ClassPlan> classify_scatter(const Kernel& k) {
     p->a.d = table.dims[1];
     p->a.storage = st;
     p->guarded = k.guarded();
+    p->nest = parallel_outer(k);
     if (p->a.tokens > (1ll << 30) || p->a.vocab > 0x7fffffffll) return nullptr;
     return p;
 }
 
 std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode) {
+    // integer weights (their scales in the slots after the output): the
+    // generic printer's loads
+    if (k.n_quant() > 0) return nullptr;
     // FAST: column sums and totals in the declared chunked order
     if (mode == PRESK_HIP_FAST)
         if (auto p = classify_sum_to(k)) return p;

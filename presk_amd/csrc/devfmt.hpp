@@ -98,6 +98,13 @@ PK_DEV bool pk_overflows_e8m15(float x) {
 PK_DEV unsigned pk_ld24(const unsigned char* p, long long e) {
     return (unsigned)p[3 * e] | ((unsigned)p[3 * e + 1] << 8) | ((unsigned)p[3 * e + 2] << 16);
 }
+// int4 weights (crates/presk-rt/src/quant.rs:333-337): element e is the
+// nibble of byte e/2, the low one when e is even, two's complement
+PK_DEV int pk_nibble(const unsigned char* p, long long e) {
+    const unsigned b = p[e >> 1];
+    const unsigned n = (e & 1) ? b >> 4 : b & 15u;
+    return (int)(n << 28) >> 28;
+}
 PK_DEV void pk_st24(unsigned char* p, long long e, unsigned c) {
     p[3 * e] = (unsigned char)c;
     p[3 * e + 1] = (unsigned char)(c >> 8);

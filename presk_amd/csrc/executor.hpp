@@ -13,15 +13,34 @@
 namespace presk {
 
 // A hand-written kernel chosen for a nest (classes.hip).  `launch` enqueues it
-// on `stream` over the KernelFn pointer table.
+// on `stream` over the KernelFn pointer table, for the iterations [lo, hi)
+// of the nest's split loop.  `nest` is that loop's bound (`parallel_outer`,
+// -1 when the nest has none: then the whole call is (0, 0)); `split` is the
+// bound the plan honours partial ranges of: `nest`, or -1 when the plan
+// computes only whole calls.  `work` is device memory of at least
+// `workspace_bytes()` bytes (null when that is 0) that the launch may use as
+// scratch: the caller provides it and keeps it until the launch has run;
+// nothing in it needs to be zero, and a partial range needs no more than
+// the whole.
 struct ClassPlan {
     virtual ~ClassPlan() = default;
     virtual const char* kind() const = 0;
     virtual std::string order() const = 0;
-    virtual hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, hipStream_t stream) const = 0;
-    // allocate what a full-range launch would allocate on first use (its
-    // workspace), so that a recorded sequence can be captured into a graph
-    virtual hipError_t prepare() const { return hipSuccess; }
+    virtual hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const = 0;
+    virtual size_t workspace_bytes() const { return 0; }
+    int64_t nest = -1, split = -1;
+
+    // (first, count) of the split loop's iterations a launch covers, count
+    // -1 for the whole call; false when [lo, hi) is not a range the plan runs
+    bool range(int64_t lo, int64_t hi, int64_t* first, int64_t* count) const {
+        *first = 0;
+        *count = -1;
+        if (lo == 0 && (hi == nest || (nest < 0 && hi == 0))) return true;
+        if (split < 0 || lo < 0 || hi > split || lo > hi) return false;
+        *first = lo;
+        *count = hi - lo;
+        return true;
+    }
 };
 
 // The hand-written kernel for `k` under `mode` (PRESK_HIP_EXACT/FAST), or

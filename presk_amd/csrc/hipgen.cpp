@@ -65,20 +65,48 @@ struct Printer {
             case Ty::F64: return std::string(c) + "double*";
             case Ty::F32: return std::string(c) + "float*";
             case Ty::BF16: case Ty::F16: return std::string(c) + "unsigned short*";
-            case Ty::E8M15: return std::string(c) + "unsigned char*";
+            case Ty::E8M15: case Ty::Q4: return std::string(c) + "unsigned char*";
+            case Ty::Q8: return std::string(c) + "signed char*";
             case Ty::I64: return std::string(c) + "long long*";
         }
         return "";
     }
+    // the scales of a Quant input b, `ps<b>`, in the slot after the output
+    std::string sptr(int b) const { return "ps" + std::to_string(b); }
     std::string ptr_params() const {
         std::string d;
         for (int b = 0; b <= (int)k.inputs.size(); ++b) d += ", " + ptr_type(b) + " __restrict__ pb" + std::to_string(b);
+        for (int b = 0; b < (int)k.inputs.size(); ++b)
+            if (ty_quant(k.inputs[b].ty)) d += ", const float* __restrict__ " + sptr(b);
         return d;
     }
     std::string ptr_args() const {
         std::string d;
         for (int b = 0; b <= (int)k.inputs.size(); ++b) d += ", (" + ptr_type(b) + ")a.buf[" + std::to_string(b) + "]";
+        for (int b = 0; b < (int)k.inputs.size(); ++b)
+            if (ty_quant(k.inputs[b].ty)) d += ", (const float*)a.buf[" + std::to_string(k.scale_slot(b)) + "]";
         return d;
+    }
+
+    // element ix (moved `lane` along the last axis) of a Quant input as the
+    // realization denotes it: f32(q) * s, one f32 multiplication
+    // (crates/presk-rt/src/quant.rs:248-252, crates/presk-cranelift/src/
+    // lib.rs:687-720); int4's element e the nibble of byte e/2, low when e
+    // is even, sign-extended
+    std::string quant_load(int b, const std::vector<const Expr*>& ix, const std::string& lane) {
+        const BufSpec& q = k.buf(b);
+        std::string off = offset(b, ix), soff = "(0LL";
+        const auto ss = q.scale_strides();
+        for (size_t p = 0; p < ix.size() && p < ss.size(); ++p)
+            if (ss[p]) soff += " + (" + intx(ix[p]) + ")*" + std::to_string(ss[p]) + "LL";
+        soff += ")";
+        if (!lane.empty()) {
+            off += " + " + lane;
+            if (!ss.empty() && ss.back()) soff += " + (" + lane + ")*" + std::to_string(ss.back()) + "LL";
+        }
+        const std::string code = q.ty == Ty::Q8 ? "(float)" + ptr(b) + "[" + off + "]"
+                                                : "(float)pk_nibble(" + ptr(b) + ", " + off + ")";
+        return "(" + code + " * " + sptr(b) + "[" + soff + "])";
     }
 
     std::string offset(int b, const std::vector<const Expr*>& ix) {
@@ -100,7 +128,7 @@ struct Printer {
             case Ty::BF16: return "pk_bf16_to_f32(" + src + ")";
             case Ty::F16: return "pk_f16_to_f32(" + src + ")";
             case Ty::I64: return "((double)" + src + ")";
-            case Ty::E8M15: break;
+            case Ty::E8M15: case Ty::Q8: case Ty::Q4: break;
         }
         return "";
     }
@@ -120,6 +148,7 @@ struct Printer {
                     if (k.buf(e->id).ty == Ty::I64) return "((" + A + ")(double)" + r + ")";
                     return "((" + A + ")" + widen(e->id, r) + ")";
                 }
+                if (ty_quant(k.buf(e->id).ty)) return "((" + A + ")" + quant_load(e->id, e->kids, "") + ")";
                 std::string off = offset(e->id, e->kids);
                 if (k.buf(e->id).ty == Ty::I64) return "((" + A + ")(double)" + ptr(e->id) + "[" + off + "])";
                 return "((" + A + ")" + load_stored(e->id, off) + ")";
@@ -170,6 +199,7 @@ struct Printer {
                     if (k.buf(e->id).ty == Ty::I64) return r;
                     return "pk_i64((double)" + widen(e->id, r) + ")";
                 }
+                if (ty_quant(k.buf(e->id).ty)) return "pk_i64((double)((" + A + ")" + quant_load(e->id, e->kids, "") + "))";
                 std::string off = offset(e->id, e->kids);
                 if (k.buf(e->id).ty == Ty::I64) return ptr(e->id) + "[" + off + "]";
                 return "pk_i64((double)" + load_stored(e->id, off) + ")";
@@ -198,6 +228,7 @@ struct Printer {
         switch (e->kind) {
             case Expr::Vv: return "v" + std::to_string(e->id) + "[l]";
             case Expr::VLoad: {
+                if (ty_quant(k.buf(e->id).ty)) return "((" + A + ")" + quant_load(e->id, e->kids, "l") + ")";
                 std::string off = offset(e->id, e->kids) + " + l";
                 return "((" + A + ")" + load_stored(e->id, off) + ")";
             }
@@ -444,6 +475,7 @@ int elem_bytes(Ty t) {
         case Ty::F32: return 4;
         case Ty::BF16: case Ty::F16: return 2;
         case Ty::E8M15: return 3;
+        case Ty::Q8: case Ty::Q4: return 1;
     }
     return 0;
 }
@@ -453,7 +485,8 @@ const char* elem_type(Ty t) {
         case Ty::F32: return "float";
         case Ty::BF16: case Ty::F16: return "unsigned short";
         case Ty::I64: return "long long";
-        case Ty::E8M15: return "unsigned char";
+        case Ty::E8M15: case Ty::Q4: return "unsigned char";
+        case Ty::Q8: return "signed char";
     }
     return "";
 }
@@ -553,8 +586,8 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
                "); the kernel interpreter emulates those";
         return false;
     }
-    if ((int)k.inputs.size() + 1 > kMaxBufs) {
-        *err = "E10001: more than " + std::to_string(kMaxBufs - 1) + " inputs";
+    if ((int)k.inputs.size() + 1 + k.n_quant() > kMaxBufs) {
+        *err = "E10001: more than " + std::to_string(kMaxBufs) + " buffers and scales";
         return false;
     }
     Printer P(k);
@@ -711,7 +744,7 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
                 for (auto e : lds) {
                     const int b = e->id;
                     const Ty ty = k.buf(b).ty;
-                    if (b == k.out_buf() || ty == Ty::E8M15 || !in_bounds(k, b, e->kids, gb)) continue;
+                    if (b == k.out_buf() || ty == Ty::E8M15 || ty_quant(ty) || !in_bounds(k, b, e->kids, gb)) continue;
                     bool unit = !e->kids.empty();  // (a scalar buffer is the same element for every u)
                     for (size_t p = 0; p < e->kids.size(); ++p) {
                         Affine f = affine_of(e->kids[p]);

@@ -20,6 +20,8 @@ const char* ty_name(Ty t) {
         case Ty::F16: return "f16";
         case Ty::E8M15: return "e8m15";
         case Ty::I64: return "i64";
+        case Ty::Q8: return "int8";
+        case Ty::Q4: return "int4";
     }
     return "?";
 }
@@ -38,11 +40,13 @@ int ty_bytes(Ty t) {
         case Ty::F32: return 4;
         case Ty::BF16: case Ty::F16: return 2;
         case Ty::E8M15: return 3;
+        case Ty::Q8: case Ty::Q4: return 1;
     }
     return 0;
 }
 
 bool ty_real(Ty t) { return t != Ty::I64; }
+bool ty_quant(Ty t) { return t == Ty::Q8 || t == Ty::Q4; }
 bool ty_coded(Ty t) { return t == Ty::F16 || t == Ty::E8M15; }
 
 // Precision rank of a real type: a buffer of lower rank than the kernel's type
@@ -65,6 +69,38 @@ std::vector<int64_t> BufSpec::strides() const {
     std::vector<int64_t> s(dims.size(), 1);
     for (int i = (int)dims.size() - 2; i >= 0; --i) s[i] = s[i + 1] * dims[i + 1];
     return s;
+}
+
+std::vector<int64_t> BufSpec::scale_strides() const {
+    std::vector<int64_t> s(dims.size(), 0);
+    if (!ty_quant(ty)) return s;
+    int64_t acc = 1;
+    for (int a = (int)dims.size() - 1; a >= 0; --a)
+        if (!(a >= qover && a < qover + qspan)) {
+            s[a] = acc;
+            acc *= dims[a];
+        }
+    return s;
+}
+
+int64_t BufSpec::scale_count() const {
+    int64_t n = 1;
+    for (int a = 0; a < (int)dims.size(); ++a)
+        if (!(a >= qover && a < qover + qspan)) n *= dims[a];
+    return n;
+}
+
+int Kernel::scale_slot(int b) const {
+    if (b < 0 || b >= (int)inputs.size() || !ty_quant(inputs[b].ty)) return -1;
+    int slot = out_buf() + 1;
+    for (int i = 0; i < b; ++i) slot += ty_quant(inputs[i].ty) ? 1 : 0;
+    return slot;
+}
+
+int Kernel::n_quant() const {
+    int n = 0;
+    for (auto& b : inputs) n += ty_quant(b.ty) ? 1 : 0;
+    return n;
 }
 
 namespace {
@@ -340,7 +376,24 @@ BufSpec parse_spec(const std::string& s) {
     if (lb == std::string::npos || rb == std::string::npos || rb < lb) throw ParseError("bad buffer spec '" + s + "'");
     BufSpec b;
     std::string ty = s.substr(0, lb);
-    if (!ty_parse(ty, &b.ty)) throw ParseError("E7005: the buffer type '" + ty + "' (quantised or emulated) is not one the executor computes");
+    if ((ty.compare(0, 5, "int8/") == 0 || ty.compare(0, 5, "int4/") == 0) && ty.size() > 5) {
+        // `int{bits}/{over}` or `int{bits}/{over}..{end}` (ir.rs:506-507)
+        b.ty = ty[3] == '8' ? Ty::Q8 : Ty::Q4;
+        const std::string r = ty.substr(5);
+        const size_t dd = r.find("..");
+        char* e = nullptr;
+        b.qover = (int)std::strtol(r.c_str(), &e, 10);
+        if (e == r.c_str() || b.qover < 0) throw ParseError("bad quantised buffer type '" + ty + "'");
+        if (dd != std::string::npos) {
+            const int end = (int)std::strtol(r.c_str() + dd + 2, &e, 10);
+            if (end <= b.qover || *e) throw ParseError("bad quantised buffer type '" + ty + "'");
+            b.qspan = end - b.qover;
+        } else if (*e) {
+            throw ParseError("bad quantised buffer type '" + ty + "'");
+        }
+    } else if (!ty_parse(ty, &b.ty)) {
+        throw ParseError("E7005: the buffer type '" + ty + "' is not one the executor computes");
+    }
     std::string axes = s.substr(lb + 1, rb - lb - 1);
     size_t i = 0;
     while (i < axes.size()) {
@@ -449,12 +502,17 @@ std::unique_ptr<Kernel> parse_kernel(const std::string& text, const std::string&
         } else {
             int best = -1;
             for (auto& b : k->inputs)
-                if (b.ty != Ty::I64 && ty_rank(b.ty) > best) { best = ty_rank(b.ty); k->dtype = b.ty; }
+                if (b.ty != Ty::I64 && !ty_quant(b.ty) && ty_rank(b.ty) > best) { best = ty_rank(b.ty); k->dtype = b.ty; }
             if (best < 0) k->dtype = Ty::F32;
         }
         for (size_t i = 0; i <= k->inputs.size(); ++i) {
             BufSpec& b = i == k->inputs.size() ? k->output : k->inputs[i];
             if (b.ty == Ty::I64 || b.ty == k->dtype) continue;
+            if (ty_quant(b.ty)) {
+                if (i == k->inputs.size()) throw ParseError("an integer output buffer");
+                if (b.qover + b.qspan > (int)b.dims.size()) throw ParseError("a quantised buffer's scale axes past its rank");
+                continue;
+            }
             if (ty_rank(b.ty) < ty_rank(k->dtype) && i < k->inputs.size()) b.wide = true;
             else throw ParseError(std::string("buffer %") + std::to_string(i) + " of type " + ty_name(b.ty) + " in a " + ty_name(k->dtype) + " kernel");
         }
@@ -541,7 +599,12 @@ static void show_body(const std::vector<const Stmt*>& body, int depth, std::stri
 }
 
 static std::string show_spec(const BufSpec& b) {
-    std::string s = std::string(ty_name(b.ty)) + "[";
+    std::string s = ty_name(b.ty);
+    if (ty_quant(b.ty)) {
+        s += "/" + std::to_string(b.qover);
+        if (b.qspan != 1) s += ".." + std::to_string(b.qover + b.qspan);
+    }
+    s += "[";
     for (size_t i = 0; i < b.dims.size(); ++i) {
         if (i) s += ", ";
         if (!b.names[i].empty()) s += b.names[i] + ": ";

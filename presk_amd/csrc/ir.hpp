@@ -17,22 +17,32 @@
 
 namespace presk {
 
-// Storage types of a buffer (`Dtype` plus the index buffers of `BufKind::Idx`).
-enum class Ty : uint8_t { F64, F32, BF16, F16, E8M15, I64 };
+// Storage types of a buffer (`Dtype` plus the index buffers of `BufKind::Idx`
+// and the integer weights of `BufKind::Quant`, int8 one a byte and int4 two a
+// byte, the even element in the low nibble).
+enum class Ty : uint8_t { F64, F32, BF16, F16, E8M15, I64, Q8, Q4 };
 
 const char* ty_name(Ty t);
 bool ty_parse(const std::string& s, Ty* out);
-int ty_bytes(Ty t);            // bytes of one stored element (e8m15: 3)
+int ty_bytes(Ty t);            // bytes of one stored element (e8m15: 3; int4: 1, two elements a byte)
 bool ty_real(Ty t);            // everything but I64
+bool ty_quant(Ty t);           // Q8 and Q4
 bool ty_coded(Ty t);           // f16 and e8m15: a store into them is guarded
 
 struct BufSpec {
     Ty ty = Ty::F32;           // the type the text shows
     bool wide = false;         // `BufKind::Wide`: narrower than the kernel's type
+    // `BufKind::Quant { over, span }` (ir.rs:30): the scales are constant
+    // along the `qspan` axes from axis `qover`
+    int qover = 0, qspan = 1;
     std::vector<int64_t> dims;
     std::vector<std::string> names;  // "" for an unnamed axis
     int64_t numel() const;
     std::vector<int64_t> strides() const;
+    // `BufSpec::scale_strides` (ir.rs:81-95): the scale of element ix is at
+    // sum ix_a * s_a, zero along the span axes, the other axes row-major
+    std::vector<int64_t> scale_strides() const;
+    int64_t scale_count() const;   // the scales a Quant buffer's pointer holds
 };
 
 enum class Op : uint8_t { Add, Sub, Mul, Div };
@@ -73,6 +83,12 @@ struct Kernel {
     int nloops = 0, nreal = 0, nint = 0, nvec = 0;
 
     int out_buf() const { return (int)inputs.size(); }
+    // the KernelFn slot of input b's scales (a Quant input), after the output
+    // in input order (crates/presk-cranelift/src/lib.rs:1619-1624), or -1
+    int scale_slot(int b) const;
+    int n_quant() const;
+    // the slot of the overflow flag: after the scales
+    int flag_slot() const { return out_buf() + 1 + n_quant(); }
     const BufSpec& buf(int b) const { return b == out_buf() ? output : inputs[b]; }
     // `Kernel::guarded` (ir.rs:332-334): stores reals into f16 or e8m15.
     bool guarded() const { return ty_coded(dtype) && output.ty != Ty::I64; }

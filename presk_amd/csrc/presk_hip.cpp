@@ -130,7 +130,8 @@ double kernel_bytes(const Kernel& k) {
     double q = 0;
     for (size_t b = 0; b <= k.inputs.size(); ++b) {
         const BufSpec& s = k.buf((int)b);
-        q += (double)s.numel() * ty_bytes(s.ty);
+        q += s.ty == Ty::Q4 ? (double)((s.numel() + 1) / 2) : (double)s.numel() * ty_bytes(s.ty);
+        if (ty_quant(s.ty)) q += 4.0 * (double)s.scale_count();
     }
     return q;
 }
@@ -167,6 +168,11 @@ double kernel_flops(const Kernel& k) {
 
 using namespace presk;
 
+namespace {
+int load_module(const presk_hip_kernel* h);
+
+}  // namespace
+
 struct presk_hip_kernel {
     std::unique_ptr<Kernel> k;
     std::unique_ptr<ClassPlan> plan;
@@ -174,6 +180,8 @@ struct presk_hip_kernel {
     std::vector<char> code;
     mutable hipModule_t module = nullptr;
     mutable std::vector<hipFunction_t> fns;
+    // a class kernel's scratch for presk_hip_run, allocated on first use
+    mutable void* work = nullptr;
     int mode = PRESK_HIP_EXACT;
 };
 
@@ -213,6 +221,9 @@ int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, 
         if (!build_code_object(h->gen.src, &h->code, &err)) return fail(PRESK_HIP_ERR, err);
     }
     h->k = std::move(k);
+    // on a device (after presk_hip_init) the code object is loaded now
+    if (g_device >= 0)
+        if (int rc = load_module(h.get())) return rc;
     *out = h.release();
     return PRESK_HIP_OK;
 }
@@ -221,50 +232,50 @@ int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, 
 
 namespace {
 
-// What a kernel's first launch would set up: the generic kernel's module, a
-// class kernel's workspace.
-int prepare_kernel(const presk_hip_kernel* h) {
-    if (h->plan) {
-        hipError_t e = h->plan->prepare();
-        return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
-    }
-    if (!h->module) {
-        hipModule_t m = nullptr;
-        hipError_t e = hipModuleLoadData(&m, h->code.data());
-        if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
-        std::vector<hipFunction_t> fns;
-        for (auto& ph : h->gen.phases) {
-            hipFunction_t f;
-            e = hipModuleGetFunction(&f, m, ph.fn.c_str());
-            if (e != hipSuccess) {
-                hipModuleUnload(m);
-                return hip_fail(e, "hipModuleGetFunction");
-            }
-            fns.push_back(f);
+// The generic kernel's code object, loaded on the current device.
+int load_module(const presk_hip_kernel* h) {
+    if (h->plan || h->module) return PRESK_HIP_OK;
+    hipModule_t m = nullptr;
+    hipError_t e = hipModuleLoadData(&m, h->code.data());
+    if (e != hipSuccess) return hip_fail(e, "hipModuleLoadData");
+    std::vector<hipFunction_t> fns;
+    for (auto& ph : h->gen.phases) {
+        hipFunction_t f;
+        e = hipModuleGetFunction(&f, m, ph.fn.c_str());
+        if (e != hipSuccess) {
+            hipModuleUnload(m);
+            return hip_fail(e, "hipModuleGetFunction");
         }
-        h->module = m;
-        h->fns = std::move(fns);
+        fns.push_back(f);
+    }
+    h->module = m;
+    h->fns = std::move(fns);
+    return PRESK_HIP_OK;
+}
+
+// What a kernel's first launch by presk_hip_run sets up: the generic
+// kernel's module, a class kernel's workspace.
+int prepare_kernel(const presk_hip_kernel* h) {
+    if (!h->plan) return load_module(h);
+    const size_t bytes = h->plan->workspace_bytes();
+    if (bytes && !h->work) {
+        hipError_t e = hipMalloc(&h->work, bytes);
+        if (e != hipSuccess) {
+            h->work = nullptr;
+            return hip_fail(e, "hipMalloc (workspace)");
+        }
     }
     return PRESK_HIP_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int presk_hip_run(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int64_t hi, void* stream) {
-    if (!h || !bufs) return fail(PRESK_HIP_ERR, "E10001: null argument");
-    hipStream_t s = (hipStream_t)stream;
-    if (h->plan) {
-        hipError_t e = h->plan->launch(bufs, lo, hi, s);
-        return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
-    }
-    if (int rc = prepare_kernel(h)) return rc;
+// The generic kernel's phases over [lo, hi) of the split loop.
+int run_generic(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int64_t hi, hipStream_t s) {
     const Kernel& k = *h->k;
     PhaseArgs args{};
-    const int nb = (int)k.inputs.size() + 1;
+    // inputs, output, one scales pointer a Quant input, then the flag
+    const int nb = (int)k.inputs.size() + 1 + k.n_quant();
     for (int i = 0; i < nb; ++i) args.buf[i] = bufs[i];
-    args.flag = k.guarded() ? (unsigned*)bufs[nb] : nullptr;
+    args.flag = k.guarded() ? (unsigned*)bufs[k.flag_slot()] : nullptr;
     for (size_t p = 0; p < h->gen.phases.size(); ++p) {
         const Phase& ph = h->gen.phases[p];
         long long total = 1;
@@ -292,6 +303,21 @@ int presk_hip_run(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int6
     return PRESK_HIP_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
+int presk_hip_run(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int64_t hi, void* stream) {
+    if (!h || !bufs) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    hipStream_t s = (hipStream_t)stream;
+    if (int rc = prepare_kernel(h)) return rc;
+    if (h->plan) {
+        hipError_t e = h->plan->launch(bufs, lo, hi, h->work, s);
+        return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
+    }
+    return run_generic(h, bufs, lo, hi, s);
+}
+
 int presk_hip_kernel_info(const presk_hip_kernel* h, presk_hip_info* info) {
     if (!h || !info) return fail(PRESK_HIP_ERR, "E10001: null argument");
     std::memset(info, 0, sizeof *info);
@@ -299,7 +325,7 @@ int presk_hip_kernel_info(const presk_hip_kernel* h, presk_hip_info* info) {
     std::snprintf(info->order, sizeof info->order, "%s", h->plan ? h->plan->order().c_str() : "sequential");
     info->guarded = h->k->guarded();
     info->n_inputs = (int32_t)h->k->inputs.size();
-    info->split_bound = parallel_outer(*h->k);
+    info->split_bound = h->plan ? h->plan->split : parallel_outer(*h->k);
     info->flops = kernel_flops(*h->k);
     info->bytes = kernel_bytes(*h->k);
     return PRESK_HIP_OK;
@@ -315,6 +341,7 @@ int64_t presk_hip_kernel_text(const presk_hip_kernel* h, char* buf, size_t cap) 
 void presk_hip_release(presk_hip_kernel* h) {
     if (!h) return;
     if (h->module) hipModuleUnload(h->module);
+    if (h->work) hipFree(h->work);
     delete h;
 }
 
@@ -435,7 +462,7 @@ int presk_hip_batch_create(presk_hip_batch** out) {
 
 int presk_hip_batch_add(presk_hip_batch* b, const presk_hip_kernel* k, void* const* bufs, int64_t lo, int64_t hi) {
     if (!b || !k || !bufs) return fail(PRESK_HIP_ERR, "E10001: null argument");
-    const size_t n = k->k->inputs.size() + 1 + (k->k->guarded() ? 1 : 0);
+    const size_t n = k->k->flag_slot() + (k->k->guarded() ? 1 : 0);
     b->drop_graph();
     b->items.push_back({k, std::vector<void*>(bufs, bufs + n), lo, hi});
     return PRESK_HIP_OK;

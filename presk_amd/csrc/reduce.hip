@@ -46,13 +46,13 @@ __global__ void __launch_bounds__(64) colsum_chunks(ColSumArgs a) {
     if (a.chunk == 64 && r0 + 64 <= a.rows) {
         float v[64];
 #pragma unroll
-        for (int i = 0; i < 64; ++i) v[i] = ld<ST>(a.x, (r0 + i) * a.cols + col);
+        for (int i = 0; i < 64; ++i) v[i] = ld<ST>(a.x, (r0 + i) * a.ld + col);
 #pragma unroll
         for (int i = 0; i < 64; ++i) part = part + term<ST>(v[i], a.square);
     } else {
         long long r1 = r0 + a.chunk;
         if (r1 > a.rows) r1 = a.rows;
-        for (long long r = r0; r < r1; ++r) part = part + term<ST>(ld<ST>(a.x, r * a.cols + col), a.square);
+        for (long long r = r0; r < r1; ++r) part = part + term<ST>(ld<ST>(a.x, r * a.ld + col), a.square);
     }
     a.work[ch * a.cols + col] = part;
 }

@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(64) rows_kernel(RowArgs a) {
     // the mask row of each of the R rows (the mask repeats over leading axes)
     long long moff[MASKED ? R : 1];
     if (MASKED) {
-        long long mr = row0 % a.mask_rows;
+        long long mr = (row0 + a.mask_row0) % a.mask_rows;
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             moff[i] = mr * n;
@@ -567,7 +567,7 @@ __global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
     for (int q = 0; q < NQ; ++q) {
         const int r = q * RPI + lane / LPR;
         myrow[q] = r < nr ? r : nr - 1;             // clamped: a dead row's values are never used
-        mrow[q] = MASKED ? a.mbits + ((row0 + myrow[q]) % a.mask_rows) * MW : nullptr;
+        mrow[q] = MASKED ? a.mbits + ((row0 + myrow[q] + a.mask_row0) % a.mask_rows) * MW : nullptr;
     }
     // the 16-byte vectors of the chunk at c0 (columns clamped into the row)
     auto load = [&](long long c0, U4 (&w)[NQ]) {
@@ -754,7 +754,7 @@ __global__ void __launch_bounds__(64) softmax_short_kernel(RowArgs a) {
     for (int q = 0; q < NQ; ++q) {
         const int r = q * RPI + lane / LPR;
         myrow[q] = r < nr ? r : nr - 1;
-        mrow[q] = MASKED ? a.mbits + ((row0 + myrow[q]) % a.mask_rows) * MW : nullptr;
+        mrow[q] = MASKED ? a.mbits + ((row0 + myrow[q] + a.mask_row0) % a.mask_rows) * MW : nullptr;
     }
     // the whole group, once
     float v[NC][NQ][VEC];

@@ -18,6 +18,7 @@ struct RowArgs {
     void* out;
     unsigned* flag;
     long long rows, n, mask_rows;
+    long long mask_row0;  // the mask row of row 0 (a launch over a range of rows)
     float n_real;         // n as the nest's f32 constant (mean)
     int op, storage;      // RowOp; 0 f32, 1 bf16, 2 f16
     unsigned* mbits;      // masked softmax over long rows: the mask as bits, [mask_rows][mask_words(n)]
