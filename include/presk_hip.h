@@ -85,14 +85,20 @@ const char *presk_hip_last_error(void);
  * kernel's text, chooses its HIP kernel, builds it.  `dtype` is "f64", "f32",
  * "bf16", "f16" or "e8m15"; `lanes` is Kernel::lanes; `mode` is
  * PRESK_HIP_EXACT or PRESK_HIP_FAST.  Refuses (PRESK_HIP_REFUSED) a kernel
- * whose formats are not its storage type's arithmetic (ir.rs:204-259) and
- * quantised inputs, as the native backend's `prepare` does (host.rs:416-434). */
+ * whose formats are not its storage type's arithmetic (ir.rs:204-259), as
+ * the native backend's `prepare` does (host.rs:416-434).  Integer weights
+ * (`int8/<over>`, `int4/<over>..<end>`, BufKind::Quant, ir.rs:30) are
+ * computed: each load is f32(q) * scale (crates/presk-rt/src/quant.rs:248-252).
+ * After presk_hip_init, the kernel's code object is loaded here. */
 int presk_hip_compile(const char *text, const char *dtype, int lanes, int mode, presk_hip_kernel **out);
 
 /* The KernelFn call (crates/presk-cranelift/src/lib.rs:38-42): `bufs` holds
- * device pointers [inputs..., output, overflow flag iff guarded]; [lo, hi) is
- * the range of the outermost loop when Kernel::parallel_outer holds
- * (ir.rs:336-373), else it is ignored.  `stream` is a hipStream_t (NULL: the
+ * device pointers [inputs..., output, one f32 scales pointer per int8/int4
+ * input in input order, overflow flag iff guarded] (lib.rs:1609-1629);
+ * [lo, hi) is a range of the outermost loop's iterations when
+ * presk_hip_kernel_info's split_bound is not -1 (Kernel::parallel_outer,
+ * ir.rs:336-373): pieces that cover [0, split_bound) give the whole call's
+ * bytes.  When split_bound is -1 the call is (0, 0).  `stream` is a hipStream_t (NULL: the
  * null stream).  Asynchronous: the overflow flag, a device u32 the caller
  * zeroes, is read after presk_hip_sync (E7007 if set). */
 int presk_hip_run(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi, void *stream);
