@@ -103,6 +103,19 @@ int presk_hip_compile(const char *text, const char *dtype, int lanes, int mode, 
  * zeroes, is read after presk_hip_sync (E7007 if set). */
 int presk_hip_run(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi, void *stream);
 
+/* No counterpart in the reference: presk_hip_run for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The same kernels and bits as
+ * presk_hip_run; a class kernel's workspace (split-K partials, chunk sums,
+ * mask bits) is the library's fixed scratch array of 64 MiB per device,
+ * held from the library's load to the process's end, instead of memory
+ * allocated on first use.  It calls no hipMalloc, hipFree or allocating
+ * routine; a kernel compiled before presk_hip_init (no code object loaded
+ * yet) or needing more scratch than 64 MiB is refused with an E10001 error.
+ * Calls on one device share its scratch: calls that overlap on one device
+ * (on several streams, or from several threads) race. */
+int presk_hip_run_noalloc(const presk_hip_kernel *k, void *const *bufs, int64_t lo, int64_t hi, void *stream);
+
 int presk_hip_kernel_info(const presk_hip_kernel *k, presk_hip_info *info);
 void presk_hip_release(presk_hip_kernel *k);
 

@@ -171,6 +171,35 @@ using namespace presk;
 namespace {
 int load_module(const presk_hip_kernel* h);
 
+// ---- scratch memory of presk_hip_run_noalloc ------------------------------------
+// One array a device, held from the library's load to the process's end: the
+// class kernels' workspaces (split-K partials, chunk sums, mask bits) when the
+// caller cannot allocate.  In host code `scratch` names a host-side stand-in,
+// never device memory: every use goes through the address hipGetSymbolAddress
+// gives on each device (g_scratch), taken once per device with it current.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+void* g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's scratch address, looked up on its first use.
+int scratch_ptr(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(PRESK_HIP_ERR, "E10001: device " + std::to_string(dev) + " past the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress (scratch)");
+        if (!p) return fail(PRESK_HIP_ERR, "E10001: hipGetSymbolAddress gave no scratch address");
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return PRESK_HIP_OK;
+}
 }  // namespace
 
 struct presk_hip_kernel {
@@ -193,7 +222,9 @@ int presk_hip_init(int device) {
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
     g_device = device;
-    return PRESK_HIP_OK;
+    // the no-allocation entry point's scratch, looked up once per device
+    void* p = nullptr;
+    return scratch_ptr(&p);
 }
 
 int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, presk_hip_kernel** out) {
@@ -221,7 +252,8 @@ int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, 
         if (!build_code_object(h->gen.src, &h->code, &err)) return fail(PRESK_HIP_ERR, err);
     }
     h->k = std::move(k);
-    // on a device (after presk_hip_init) the code object is loaded now
+    // on a device (after presk_hip_init) the code object is loaded now, so
+    // that presk_hip_run_noalloc never loads one
     if (g_device >= 0)
         if (int rc = load_module(h.get())) return rc;
     *out = h.release();
@@ -315,6 +347,27 @@ int presk_hip_run(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int6
         hipError_t e = h->plan->launch(bufs, lo, hi, h->work, s);
         return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
     }
+    return run_generic(h, bufs, lo, hi, s);
+}
+
+int presk_hip_run_noalloc(const presk_hip_kernel* h, void* const* bufs, int64_t lo, int64_t hi, void* stream) {
+    if (!h || !bufs) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    hipStream_t s = (hipStream_t)stream;
+    if (h->plan) {
+        const size_t need = h->plan->workspace_bytes();
+        if (need > kScratchBytes)
+            return fail(PRESK_HIP_ERR, "E10001: the kernel `" + h->k->name + "` needs " + std::to_string(need) +
+                                           " bytes of scratch, more than the " + std::to_string(kScratchBytes) +
+                                           " presk_hip_run_noalloc holds; run it with presk_hip_run");
+        void* p = nullptr;
+        if (need)
+            if (int rc = scratch_ptr(&p)) return rc;
+        hipError_t e = h->plan->launch(bufs, lo, hi, p, s);
+        return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, h->plan->kind());
+    }
+    if (!h->module)
+        return fail(PRESK_HIP_ERR, "E10001: the kernel `" + h->k->name + "` has no code object loaded: compile it after "
+                                   "presk_hip_init, or run it once with presk_hip_run");
     return run_generic(h, bufs, lo, hi, s);
 }
 

@@ -21,7 +21,8 @@ OK, ERR, REFUSED, OVERFLOW = 0, -1, -2, -3
 STORAGE_BYTES = {"f64": 8, "f32": 4, "bf16": 2, "f16": 2, "e8m15": 3, "i64": 8}
 
 # Every entry point include/presk_hip.h declares.
-SYMBOLS = ["presk_hip_init", "presk_hip_last_error", "presk_hip_compile", "presk_hip_run", "presk_hip_kernel_info",
+SYMBOLS = ["presk_hip_init", "presk_hip_last_error", "presk_hip_compile", "presk_hip_run", "presk_hip_run_noalloc",
+           "presk_hip_kernel_info",
            "presk_hip_release", "presk_hip_kernel_text", "presk_hip_alloc", "presk_hip_free", "presk_hip_h2d", "presk_hip_d2h", "presk_hip_memset",
            "presk_hip_sync", "presk_hip_stream_create", "presk_hip_stream_destroy", "presk_hip_time",
            "presk_hip_scalar_digest", "presk_hip_batch_create", "presk_hip_batch_add", "presk_hip_batch_graph",
@@ -61,6 +62,7 @@ def lib():
         L.presk_hip_last_error.restype = ctypes.c_char_p
         L.presk_hip_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i32, i32, ctypes.POINTER(vp)]
         L.presk_hip_run.argtypes = [vp, ctypes.POINTER(vp), i64, i64, vp]
+        L.presk_hip_run_noalloc.argtypes = [vp, ctypes.POINTER(vp), i64, i64, vp]
         L.presk_hip_kernel_info.argtypes = [vp, ctypes.POINTER(Info)]
         L.presk_hip_kernel_text.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
         L.presk_hip_kernel_text.restype = i64

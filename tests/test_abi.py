@@ -51,3 +51,29 @@ def test_malformed_text_is_an_executor_error():
     with pytest.raises(hip.HipError) as e:
         hip.Compiled("kernel x (%0 : f32[2]) -> %1 : f32[2] {\n  for i0 in 0..2 {\n", "f32")
     assert e.value.code == "E10001"
+
+
+def test_noalloc_refuses_before_touching_the_device():
+    """presk_hip_run_noalloc's refusals are host-side: a class kernel whose
+    workspace exceeds the 64 MiB scratch (here 1 024 chunk sums of 16 400
+    columns, 67.2 MB), and a generic kernel with no code object loaded (no
+    presk_hip_init in this process).  No pointer is read."""
+    import ctypes
+
+    from presk_amd import lower as L
+    A, O = L.ax, L.Operand
+    low = L.sum_to([O(A(("batch", 65536), ("model", 16400))), O(A(("model", 16400)))], "f32")
+    c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+    assert c.kind == "colsum"
+    table = (ctypes.c_void_p * 3)(None, None, None)
+    rc = hip.lib().presk_hip_run_noalloc(c.handle, table, 0, 0, None)
+    assert rc == hip.ERR
+    msg = hip.lib().presk_hip_last_error().decode()
+    assert msg.startswith("E10001") and "67174400 bytes of scratch" in msg, msg
+    if hip._initialized is not None:
+        return   # a device is set up in this process: the code object would be loaded
+    g = L.unary("gelu", [O(A(("batch", 4), ("model", 8)))], "f32")
+    cg = hip.Compiled(g.text, "f32", g.lanes, hip.EXACT)
+    assert cg.kind == "generic"
+    rc = hip.lib().presk_hip_run_noalloc(cg.handle, (ctypes.c_void_p * 2)(None, None), 0, 4, None)
+    assert rc == hip.ERR and "no code object loaded" in hip.lib().presk_hip_last_error().decode()
