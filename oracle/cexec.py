@@ -36,6 +36,7 @@ from __future__ import annotations
 import ctypes
 import hashlib
 import os
+import re
 import subprocess
 import tempfile
 
@@ -73,15 +74,27 @@ class _Printer:
         self.A = "double" if dtype == "f64" else "float"
         self.n_in = len(k.inputs)
         self.kinds = []
+        # integer weights (BufKind::Quant): buffer -> (scales slot, k, inner)
+        self.quant = {}
         for i, b in enumerate(k.bufs):
-            if b.ty == "i64":
+            q = quant_of(b.ty)
+            if q is not None and i < self.n_in:
+                bits, over, span = q
+                self.kinds.append(f"q{bits}")
+                kk, inner = 1, 1
+                for d in b.dims[over:over + span]:
+                    kk *= d
+                for d in b.dims[over + span:]:
+                    inner *= d
+                self.quant[i] = (self.n_in + 1 + len(self.quant), kk, inner)
+            elif b.ty == "i64":
                 self.kinds.append("i64")
             elif b.ty in REAL:
                 if b.ty != dtype and WIDTH_RANK[b.ty] <= WIDTH_RANK[dtype]:
                     raise Refused(f"buffer %{i} of type {b.ty} in a {dtype} kernel")
                 self.kinds.append(b.ty)
             else:
-                raise Refused(f"buffer %{i} of type {b.ty} (quantised weights)")
+                raise Refused(f"buffer %{i} of type {b.ty}")
         out_kind = self.kinds[-1]
         if out_kind not in ("i64", dtype):
             raise Refused(f"output of type {out_kind} in a {dtype} kernel")
@@ -94,8 +107,14 @@ class _Printer:
         return "(" + (" + ".join(terms) if terms else "0") + ")"
 
     def load_stored(self, b, off):
-        """The buffer's element widened exactly to its own arithmetic type."""
+        """The buffer's element widened exactly to its own arithmetic type;
+        an integer weight's, f32(q) * s with s the scale of its channel
+        (exec.rs:653, crates/presk-rt/src/quant.rs:236-252, 295-297)."""
         kind, p = self.kinds[b], f"p{b}"
+        if kind in ("q8", "q4"):
+            _, kk, inner = self.quant[b]
+            q = f"(float){p}[{off}]" if kind == "q8" else f"(float)oc_nibble({p}, {off})"
+            return f"({q} * sc{b}[(({off}) / {kk * inner}) * {inner} + ({off}) % {inner}])"
         if kind in ("f32", "f64"):
             return f"{p}[{off}]"
         if kind == "bf16":
@@ -247,11 +266,16 @@ class _Printer:
         k = self.k
         split = parallel_outer(k)
         lines = [f"void {fname}(void *const *bufs, int64_t lo, int64_t hi) {{"]
-        ctype = {"f32": "float", "f64": "double", "bf16": "uint16_t", "f16": "uint16_t", "e8m15": "uint8_t", "i64": "int64_t"}
+        ctype = {"f32": "float", "f64": "double", "bf16": "uint16_t", "f16": "uint16_t", "e8m15": "uint8_t", "i64": "int64_t",
+                 "q8": "int8_t", "q4": "uint8_t"}
         for i, kind in enumerate(self.kinds):
             lines.append(f"    {ctype[kind]} *restrict p{i} = ({ctype[kind]} *)bufs[{i}];")
+        # the scales of the integer inputs after the output, then the flag
+        # (crates/presk-cranelift/src/lib.rs:1609-1629)
+        for b, (slot, _, _) in self.quant.items():
+            lines.append(f"    const float *restrict sc{b} = (const float *)bufs[{slot}];")
         if self.guarded:
-            lines.append(f"    uint32_t *flag = (uint32_t *)bufs[{self.n_in + 1}];")
+            lines.append(f"    uint32_t *flag = (uint32_t *)bufs[{self.n_in + 1 + len(self.quant)}];")
         lines.append("    int ovf = 0; (void)ovf; (void)lo; (void)hi;")
         for v in range(k.nloops):
             lines.append(f"    int64_t i{v} = 0; (void)i{v};")
@@ -307,6 +331,12 @@ static inline int64_t rs_i64(double x) {
     if (x >= 9223372036854775807.0) return INT64_MAX;
     if (x <= -9223372036854775808.0) return INT64_MIN;
     return (int64_t)x;
+}
+/* int4 weights, two a byte: element e the low nibble of byte e/2 when e is
+   even, else the high one, sign-extended (crates/presk-rt/src/quant.rs:333-337) */
+static inline int oc_nibble(const uint8_t *p, int64_t e) {
+    const int n = (e & 1) ? p[e >> 1] >> 4 : p[e >> 1] & 15;
+    return n >= 8 ? n - 16 : n;
 }
 static inline uint32_t ld24(const uint8_t *p, int64_t e) {
     return (uint32_t)p[3*e] | ((uint32_t)p[3*e+1] << 8) | ((uint32_t)p[3*e+2] << 16);
@@ -367,6 +397,16 @@ def compile_kernel(text: str, dtype: str, lanes: int = 1, opt: str = "-O2", nati
     return lib, k, parallel_outer(k), p.guarded
 
 
+def quant_of(ty: str):
+    """(bits, over, span) of an integer-weight buffer type `int8/1` or
+    `int4/1..3` (crates/presk-kernel/src/ir.rs:506-507), else None."""
+    m = re.fullmatch(r"int([48])/(\d+)(?:\.\.(\d+))?", ty)
+    if not m:
+        return None
+    over = int(m.group(2))
+    return int(m.group(1)), over, (int(m.group(3)) - over) if m.group(3) else 1
+
+
 def storage_array(ty: str, numel: int) -> np.ndarray:
     """A zeroed buffer of `numel` elements of storage type `ty` (e8m15: 3 bytes each)."""
     if ty == "e8m15":
@@ -383,15 +423,25 @@ def run(text: str, dtype: str, inputs: list, lanes: int = 1, threads: int = 1, o
     lib, k, split, guarded = compile_kernel(text, dtype, lanes, native=native)
     if len(inputs) != len(k.inputs):
         raise ValueError(f"{k.name}: {len(inputs)} inputs for {len(k.inputs)}")
+    scales = []
+    inputs = list(inputs)
     for i, (a, b) in enumerate(zip(inputs, k.inputs)):
-        ty = b.ty if b.ty != dtype else dtype
-        want = b.numel * (3 if ty == "e8m15" else 1)
+        q = quant_of(b.ty)
+        if q is not None:
+            # an integer input is (codes, f32 scales)
+            a, sc = a
+            inputs[i] = a
+            scales.append(np.ascontiguousarray(sc, dtype=np.float32))
+            want = b.numel if q[0] == 8 else (b.numel + 1) // 2
+        else:
+            ty = b.ty if b.ty != dtype else dtype
+            want = b.numel * (3 if ty == "e8m15" else 1)
         if a.size != want or not a.flags.c_contiguous:
             raise ValueError(f"{k.name}: input %{i} has {a.size} storage elements, {want} expected")
     if out is None:
         out = storage_array(k.output.ty, k.output.numel)
     flag = np.zeros(1, dtype=np.uint32)
-    ptrs = [a.ctypes.data for a in inputs] + [out.ctypes.data]
+    ptrs = [a.ctypes.data for a in inputs] + [out.ctypes.data] + [sc.ctypes.data for sc in scales]
     if guarded:
         ptrs.append(flag.ctypes.data)
     arr = (ctypes.c_void_p * len(ptrs))(*ptrs)

@@ -90,7 +90,11 @@ def mlp(rows=8192, d=768, hidden=3072, dtype="bf16", seed=1):
 
 
 def storage_inputs(p: Program, host: dict) -> dict:
-    """Host values -> each input's storage in its declared type (indices int64)."""
+    """Host values -> each input's storage in its declared type (indices
+    int64); an integer weight quantised from its values read in f64
+    (QTensor::quantize, crates/presk-rt/src/quant.rs:118-145), its codes
+    under its name and its f32 scales under `<name>#scales`."""
+    from . import quant as Q
     env = {}
     for ln in p.launches:
         for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
@@ -99,6 +103,11 @@ def storage_inputs(p: Program, host: dict) -> dict:
                 v = host[name]
                 if ty == "i64":
                     env[name] = np.ascontiguousarray(v, dtype=np.int64).ravel()
+                elif name in p.quant:
+                    q, over, axes = p.quant[name]
+                    qt = Q.quantize(np.asarray(v, np.float32).astype(np.float64), [a.len for a in axes],
+                                    Q.Quant(q.bits, over, q.scheme))
+                    env[name], env[name + "#scales"] = qt.data, qt.scales
                 else:
                     env[name] = encode(np.asarray(v, np.float32).reshape(-1)[:max(count, 1)], ty)
     return env
@@ -111,7 +120,10 @@ def load_inputs(p: Program, host: dict):
         for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
             specs.setdefault(name, (p.input_types.get(name, ty) if ty != "i64" else ty, count))
     for name, arr in storage_inputs(p, host).items():
-        ty, count = specs[name]
+        if name.endswith("#scales"):
+            ty, count = "f32", arr.size
+        else:
+            ty, count = specs[name]
         p.declare(name, ty, max(count, 1))
         p.bufs.upload(name, arr)
 

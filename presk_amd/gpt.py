@@ -25,6 +25,7 @@ gradient against torch autograd, tests/test_gpt_program.py).
 from __future__ import annotations
 
 import contextlib
+import dataclasses
 import math
 import re
 from dataclasses import dataclass
@@ -32,6 +33,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import lower as L
+from . import quant as Q
 from .program import Program
 
 A, O = L.ax, L.Operand
@@ -134,7 +136,23 @@ class Builder:
         return self.view(src, ax[:p] + [L.Axis(None, ax[p].len * ax[p + 1].len)] + ax[p + 2:], name)
 
     def _out(self, low, ins, name):
-        self.p.add(low, [self.base.get(i, i) for i in ins], name)
+        # an input holding integer weights is marked with its buffer kind,
+        # the run of the view's axes its scales are constant along
+        # (BufKind::of_quant, crates/presk-kernel/src/ir.rs:52-79), and its
+        # scales ride after the output
+        scales = []
+        for j, i in enumerate(ins):
+            base = self.base.get(i, i)
+            if base not in self.p.quant:
+                continue
+            q, over, axes = self.p.quant[base]
+            kind = Q.of_quant_dims(q.bits, over, [a.len for a in axes], [a.len for a in self.axes[i]])
+            if kind is None:
+                raise ValueError(f"E7005: `{low.name}` reads the integer weights `{base}` through a view that merges "
+                                 f"their quantised axis")
+            low = dataclasses.replace(low, text=Q.mark(low.text, j, kind))
+            scales.append(base + "#scales")
+        self.p.add(low, [self.base.get(i, i) for i in ins], name, scales)
         self.axes[name], self.kind[name] = list(low.out_axes), low.out_kind
         return name
 
@@ -142,6 +160,17 @@ class Builder:
         """One primitive: `make(dtype)` lowers it at the site's storage type."""
         name = self._name(name)
         return self._out(make(self._dt(name)), ins, name)
+
+    def params_of(self, leaves: dict, rename: dict, shapes: dict):
+        """The realization's `params` types and `quant` weights on the
+        program's parameter buffers, by their dotted paths (E7001 for a path
+        the program does not have)."""
+        types, quants = self.realize.resolve_params(leaves, rename)
+        for name in shapes:
+            self.p.input_types[name] = types.get(name, "f32")
+        for name, (q, over, axes) in quants.items():
+            self.p.input_types[name] = f"int{q.bits}"
+            self.p.quant[name] = (q, over, axes)
 
     # --- primitives -----------------------------------------------------------
     def binary(self, op, a, b, name=None):
@@ -370,8 +399,7 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
     p = Program(f"gpt-{'step' if train else 'forward'}-{tag}", mode=hip.FAST if mode is None else mode)
     b = Builder(p, dtype, realize)
     if realize is not None:
-        for name in param_shapes(s):
-            p.input_types[name] = realize.param_dtype(name)
+        b.params_of(opt_leaves(s), params_layout(s)[1], param_shapes(s))
         for name in ("eps", "scale", "two", "one"):
             p.input_types[name] = "f32"
     for name, axes in param_shapes(s).items():
@@ -382,7 +410,7 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
         if members is None:
             continue
         tys = {p.input_types.get(m, dtype if realize is None else None) for m in members}
-        if len(tys) == 1 and None not in tys:
+        if len(tys) == 1 and None not in tys and not tys & {"int8", "int4"}:
             count = 1
             for a in axes[1:]:
                 count *= a.len

@@ -276,15 +276,14 @@ def build(s: LlamaShape, dtype: str = "bf16", mode=None, realize=None) -> tuple:
     b = Builder(p, dtype, realize)
     b.fn = "Llama.apply"
     if realize is not None:
-        for name in param_shapes(s):
-            p.input_types[name] = realize.param_dtype(name)
+        b.params_of(leaves(s), params_layout(s)[1], param_shapes(s))
     for name, axes in param_shapes(s).items():
         b.input(name, axes)
     # each block parameter's layers held in one stacked buffer, as `params
     # Llama` stores them (a checkpoint's leaf decodes straight into it)
     for n, (axes, members) in leaves(s).items():
         tys = {p.input_types.get(m, dtype if realize is None else None) for m in members or []}
-        if members and len(tys) == 1 and None not in tys:
+        if members and len(tys) == 1 and None not in tys and not tys & {"int8", "int4"}:
             p.stack(n, members, tys.pop(), _count(axes[1:]))
     b.input("ids", A(("batch", s.B), ("seq", s.T)), "idx")
     for name in SCALARS:

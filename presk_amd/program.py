@@ -17,7 +17,12 @@ import numpy as np
 from . import hip
 from . import lower as L
 
-BYTES = {"f64": 8, "f32": 4, "bf16": 2, "f16": 2, "e8m15": 3, "i64": 8}
+BYTES = {"f64": 8, "f32": 4, "bf16": 2, "f16": 2, "e8m15": 3, "i64": 8, "int8": 1}
+INTS = ("int8", "int4")     # integer weights (their f32 scales in `<name>#scales`)
+
+
+def nbytes(ty: str, count: int) -> int:
+    return (count + 1) // 2 if ty == "int4" else count * BYTES[ty]
 
 
 def numel(axes) -> int:
@@ -48,11 +53,13 @@ class Buffers:
             if ty != pty or first + count > pcount:
                 raise ValueError(f"buffer {name} ({ty}[{count}]) does not fit {parent} ({pty}[{pcount}]) at {first}")
             whole = self.alloc(parent, pty, pcount)
-            b = hip.DeviceView(whole, first * BYTES[ty], count * BYTES[ty])
+            if ty == "int4" and first % 2:
+                raise ValueError(f"buffer {name}: an int4 slice that starts inside a byte")
+            b = hip.DeviceView(whole, nbytes(ty, first), nbytes(ty, count))
             self.dev[name] = b
             self.meta[name] = (ty, count)
             return b
-        b = hip.DeviceBuffer(max(count, 1) * BYTES[ty])
+        b = hip.DeviceBuffer(max(nbytes(ty, count), 1))
         self.dev[name] = b
         self.meta[name] = (ty, count)
         return b
@@ -71,13 +78,18 @@ class Buffers:
         ty, count = self.meta[name]
         if ty == "e8m15":
             return self.dev[name].download(np.uint8, 3 * count)
+        if ty in INTS:
+            return self.dev[name].download(np.uint8, nbytes(ty, count))
         dt = {"f64": np.float64, "f32": np.float32, "bf16": np.uint16, "f16": np.uint16, "i64": np.int64}[ty]
         return self.dev[name].download(dt, count)
 
 
 class Launch:
-    def __init__(self, low: L.Lowered, ins: list, out: str):
+    def __init__(self, low: L.Lowered, ins: list, out: str, scales=()):
         self.low, self.ins, self.out = low, ins, out
+        # the f32 scales of each integer input, in input order: the KernelFn
+        # slots after the output (crates/presk-cranelift/src/lib.rs:1619-1624)
+        self.scales = list(scales)
         self.compiled: hip.Compiled | None = None
         self.table = None
 
@@ -104,10 +116,14 @@ class Program:
         self.masks: list = []
         self.keys: list = []
         self._keytab = None
+        # integer weights: buffer -> (Quant, its quantised axis, its axes),
+        # stored as `int8`/`int4` with f32 scales in `<buffer>#scales`
+        self.quant: dict = {}
 
-    def add(self, low: L.Lowered, ins: list, out: str) -> str:
-        """Appends one launch of `low` reading buffers `ins`, writing `out`."""
-        self.launches.append(Launch(low, list(ins), out))
+    def add(self, low: L.Lowered, ins: list, out: str, scales=()) -> str:
+        """Appends one launch of `low` reading buffers `ins`, writing `out`
+        (and `scales`, the scales of its integer inputs)."""
+        self.launches.append(Launch(low, list(ins), out, scales))
         return out
 
     def compile(self, cache: dict | None = None):
@@ -181,7 +197,7 @@ class Program:
             names = []
             for n in ln.ins:
                 src_ty, count = self.bufs.meta[n]
-                if src_ty != "i64" and src_ty != ln.low.dtype:
+                if src_ty not in ("i64", ln.low.dtype) + INTS:
                     key = (n, ln.low.dtype)
                     if key not in converted:
                         dst = f"{n}@{ln.low.dtype}"
@@ -192,6 +208,7 @@ class Program:
                 names.append(n)
             self.bufs.alloc(ln.out, ty, numel(ln.low.out_axes))
             ptrs = [self.bufs.dev[n].ptr for n in names] + [self.bufs.dev[ln.out].ptr]
+            ptrs += [self.bufs.dev[n].ptr for n in ln.scales]
             if c.guarded:
                 ptrs.append(self._flag.ptr)
             ln.table = (ctypes.c_void_p * len(ptrs))(*ptrs)

@@ -74,6 +74,8 @@ def run(p, host: dict, threads: int = 1, native: bool = False) -> dict:
         for name, (ty, count) in zip(ln.ins, _input_specs(ln.low)):
             if name in env and name not in types:
                 types[name] = p.input_types.get(name, ty) if ty != "i64" else ty
+            if name in p.quant:
+                types[name] = "int"
     # a stacked buffer (Program.stack): its members one after another, read
     # only after every member is written
     stacks = {}
@@ -88,6 +90,10 @@ def run(p, host: dict, threads: int = 1, native: bool = False) -> dict:
                 env[name] = np.concatenate([np.asarray(env[m]).ravel() for m in members])
                 types[name] = types[members[0]]
             a = env[name]
+            if types[name] == "int":
+                # integer weights: codes and scales (the KernelFn's slots)
+                ins.append((a, env[name + "#scales"]))
+                continue
             if types[name] not in ("i64", ln.low.dtype):
                 a, f = convert(a, types[name], ln.low.dtype, max(count, 1))
                 flag |= f

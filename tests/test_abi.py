@@ -39,12 +39,14 @@ def test_refuses_non_native_formats():
     assert e.value.code == "E7005"
 
 
-def test_refuses_quantised_weights():
+def test_accepts_quantised_weights():
+    """Integer weights are the native backend's to compute (their scales in
+    the slots after the output, crates/presk-cranelift/src/lib.rs:1619-1624),
+    and this executor's too."""
     text = ("kernel dot (%0 : f32[2, 3], %1 : int8/0[3, 2]) -> %2 : f32[2, 2] {\n"
             "  for i0 in 0..2 {\n    for i1 in 0..2 {\n      %2[i0, i1] = 0\n    }\n  }\n}\n")
-    with pytest.raises(hip.HipError) as e:
-        hip.Compiled(text, "f32")
-    assert e.value.code == "E7005"
+    c = hip.Compiled(text, "f32")
+    assert c.read_back() == text and c.n_inputs == 2
 
 
 def test_malformed_text_is_an_executor_error():

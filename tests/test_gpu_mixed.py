@@ -19,7 +19,7 @@ MIXED = Realization.of_json({
                   "Embedding.apply": "e8m15", "LayerNorm.apply.vjp": "f32", "MLP.apply.vjp": "f16"},
     "storage": {"MiniGPT.apply/logits": "f32", "MiniGPT.apply/ce": "f32", "MiniGPT.apply/loss": "f32",
                 "SelfAttention.apply/probs": "f32"},
-    "params": {"head": "f16", "b0.up": "bf16", "tok": "e8m15"}})
+    "params": {"head": "f16", "blocks.ff.up.w": "bf16", "tok": "e8m15"}})
 
 
 @pytest.mark.parametrize("train", [False, True])

@@ -24,7 +24,7 @@ def test_precedence():
 
 
 def test_refusals():
-    for field in ("arith", "product", "accum", "scaled", "quant"):
+    for field in ("arith", "product", "accum", "scaled"):
         with pytest.raises(ValueError, match="E7005"):
             Realization.of_json({"default": "f32", "order": {"kind": "sequential"}, field: {"a/b": "f32"}})
     with pytest.raises(ValueError, match="E7005"):
