@@ -481,7 +481,9 @@ struct ColSumPlan : ClassPlan {
     int n_in = 2;
     long long cols_per_iter = 0;   // output columns one iteration of the split loop covers
     const char* kind() const override { return "colsum"; }
-    std::string order() const override { return "chunked(" + std::to_string(a.chunk) + ")-f32"; }
+    // the executor's own order (a realization's order reaches contractions
+    // only, crates/presk-kernel/src/lower.rs:250-303): chunks of 64 rows
+    std::string order() const override { return "rows-in-chunks(" + std::to_string(a.chunk) + ")-f32"; }
     // the chunk sums, [nchunks][cols] in f32
     size_t workspace_bytes() const override { return sizeof(float) * (size_t)(a.nchunks * a.cols); }
     hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const override {

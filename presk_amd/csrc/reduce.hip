@@ -1,4 +1,4 @@
-// Column reductions in a declared chunked order (FAST mode): `sum_to` of a
+// Column reductions in the executor's own chunked order (FAST mode): `sum_to` of a
 // tensor onto its trailing axes (a bias's gradient, lower.rs:1670-1680),
 // out[c] = sum_r x[r][c]; and `sum_all`/`mean_all` (lower.rs:1221-1233) and
 // `sum_squares` (lower.rs:1693-1703, the terms x * x) as the one column of
@@ -6,9 +6,11 @@
 //
 // The interpreter's order adds the R rows one after another into the output
 // (a running sum of R dependent additions per column: latency-bound with one
-// thread per column).  This kernel uses the reference's declared order
+// thread per column).  This kernel declares an order of its own, in the
+// kernel's info as `rows-in-chunks(64)-f32` -- the shape of the reference's
 // `ReductionOrder::Chunked { size }` (crates/presk-rt/src/lib.rs:262-268;
-// semantics lower.rs:427-464): the rows in chunks of CH consecutive ones, each
+// semantics lower.rs:427-464), which a realization applies to contractions
+// only, never to these sums: the rows in chunks of CH consecutive ones, each
 // chunk summed from zero in row order, the chunk sums then added in chunk
 // order from zero -- in f32, and stored once in the storage type (an f32
 // accumulation format).  Two launches, deterministic.

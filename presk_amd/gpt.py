@@ -182,24 +182,37 @@ class Builder:
     def fused(self, steps, ins, out_like, name=None):
         return self._prim(lambda dt: L.fused(steps, [self.op(i) for i in ins], self.axes[out_like], dt), ins, name)
 
+    def order(self):
+        """The realization's reduction order, applied to the contractions as
+        `lower_planned` applies it (lower.rs:250-303); None when exact."""
+        return L.order_of(self.realize.order) if self.realize is not None else None
+
     def dot(self, x, w, b=None, name=None):
+        o = self.order()
+        if b is not None and not L.exact_order(o):
+            # no contraction nest under a reassociating order, so no epilogue:
+            # the product and the `add` are two launches
+            name = self._name(name)
+            d = self._prim(lambda dt: L.dot([self.op(x), self.op(w)], dt, order=o), [x, w], name + ".dot")
+            return self.binary("add", d, b, name=name)
+
         def make(dt):
-            d = L.dot([self.op(x), self.op(w)], dt)
+            d = L.dot([self.op(x), self.op(w)], dt, order=o)
             if b is None:
                 return d
             return L.dot([self.op(x), self.op(w), self.op(b)], dt, epilogue=(True, d.out_axes))
         return self._prim(make, [x, w] if b is None else [x, w, b], name)
 
     def dot_vjp_l(self, ct, b, name=None):
-        return self._prim(lambda dt: L.dot_vjp_l([self.op(ct), self.op(b)], dt), [ct, b], name)
+        return self._prim(lambda dt: L.dot_vjp_l([self.op(ct), self.op(b)], dt, order=self.order()), [ct, b], name)
 
     def dot_vjp_r(self, a, ct, name=None):
-        return self._prim(lambda dt: L.dot_vjp_r([self.op(a), self.op(ct)], dt), [a, ct], name)
+        return self._prim(lambda dt: L.dot_vjp_r([self.op(a), self.op(ct)], dt, order=self.order()), [a, ct], name)
 
     def ein(self, a, b, la, lb, out, name=None, like=None):
         """`like`: the value whose type the result has -- an operand's, for the
         `ein` of its cotangent (rules.rs:151-169 gives it `tys[j]`)."""
-        r = self._prim(lambda dt: L.ein([self.op(a), self.op(b)], [la, lb], out, dt), [a, b], name)
+        r = self._prim(lambda dt: L.ein([self.op(a), self.op(b)], [la, lb], out, dt, order=self.order()), [a, b], name)
         if like is not None:
             self.axes[r] = list(self.axes[like])
         return r

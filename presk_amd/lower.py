@@ -548,61 +548,167 @@ def emit_contraction(c: Contraction, dtype, ins, layout=None, epilogue=None) -> 
     return kernel(name, dtype, ins, out_axes, "real", bd, nest(ov, c.outer, body))
 
 
-def contraction_chunked(c: Contraction, dtype, ins, size) -> Lowered:
-    """`contraction_ordered` under `Chunked { size }` (lower.rs:427-464)."""
-    if len(c.ks) != 1:
-        raise ValueError("chunked order over several summed axes")
-    k = c.k
-    bd = B()
-    ov = bd.loops(c.outer + [c.i, c.j])
-    cb, t, kvv = bd.iv(), bd.iv(), bd.iv()
-    acc, part = bd.sv(), bd.sv()
-    outer, iI, jJ = ov[:-2], iv(ov[-2]), iv(ov[-1])
-    term = bin_("*", load(0, _slots(c.x_index, outer, iI, "0", [iv(kvv)])), load(1, _slots(c.w_index, outer, "0", jJ, [iv(kvv)])))
+def exact_order(order) -> bool:
+    """`ReductionOrder::is_exact` (crates/presk-rt/src/lib.rs:273-275): the
+    sequential and blocked orders keep the index order of every addition;
+    `("interleaved", n)` and `("chunked", c)` reassociate."""
+    return not order or order[0] not in ("interleaved", "chunked")
 
-    def chunk(start, length):
-        return [Set(part, num(0)),
-                For(t, length, [SetL(kvv, bin_("+", start, iv(t))), Set(part, bin_("+", sv(part), term))]),
-                Set(acc, bin_("+", sv(acc), sv(part)))]
-    body = [Set(acc, num(0))]
-    if k // size > 0:
-        body.append(For(cb, k // size, chunk(bin_("*", iv(cb), str(size)), size)))
-    if k % size > 0:
-        body.extend(chunk(str(k // size * size), k % size))
-    body.append(Store(2, ivs(ov), sv(acc)))
-    return kernel(c.name, dtype, ins, c.out, "real", bd, nest(ov, c.outer + [c.i, c.j], body))
+
+def order_of(o) -> tuple | None:
+    """A realization's `order` ({"kind": ..., "partials"/"size"/"width": n},
+    lib.rs:249-270) as this module's tuple; None for the exact ones."""
+    if o is None:
+        return None
+    kind = o.get("kind") if isinstance(o, dict) else o[0]
+    if kind in ("sequential", "blocked"):
+        return None
+    if kind == "interleaved":
+        return ("interleaved", int(o["partials"] if isinstance(o, dict) else o[1]))
+    if kind == "chunked":
+        return ("chunked", int(o["size"] if isinstance(o, dict) else o[1]))
+    raise ValueError(f"E7001: the reduction order `{kind}`")
+
+
+def _chunked_only(order):
+    """lower.rs:299-303: the derivatives of `dot` and `ein` take a chunked
+    order; any other is the sequential one for them."""
+    return order if order and order[0] == "chunked" else None
+
+
+def contraction_ordered(name, dtype, ins, out, outer_dims, inner_dims, index_x, index_y, order) -> Lowered:
+    """lower.rs:384-475: one output element a thread of the nest, its terms
+    x[index_x] * w[index_y] summed under `order`:
+    - ("interleaved", n), one summed axis that n divides, n >= 2: n partial
+      accumulators, the t-th summing terms cb*n + t in order, added left to
+      right at the end;
+    - ("chunked", c), one summed axis: chunks of c consecutive terms each
+      summed from zero, the chunk sums added to the total in order from
+      zero, the last chunk what is left;
+    - otherwise every term in index order into one accumulator."""
+    if order and order[0] == "interleaved" and len(inner_dims) == 1 and order[1] >= 2 and inner_dims[0] % order[1] == 0:
+        n = order[1]
+        chunks = inner_dims[0] // n
+        bd = B()
+        ov = bd.loops(outer_dims)
+        cb = bd.iv()
+        terms = [bd.iv() for _ in range(n)]
+        accs = [bd.sv() for _ in range(n)]
+        inner = []
+        for t in range(n):
+            inner.append(SetL(terms[t], bin_("+", bin_("*", iv(cb), str(n)), str(t))))
+            inner.append(Set(accs[t], bin_("+", sv(accs[t]), bin_("*", load(0, index_x(ov, [terms[t]])),
+                                                                  load(1, index_y(ov, [terms[t]]))))))
+        body = [Set(a, num(0)) for a in accs]
+        body.append(For(cb, chunks, inner))
+        total = sv(accs[0])
+        for a in accs[1:]:
+            total = bin_("+", total, sv(a))
+        body.append(Store(2, ivs(ov), total))
+        return kernel(name, dtype, ins, out, "real", bd, nest(ov, outer_dims, body))
+    if order and order[0] == "chunked":
+        size = order[1]
+        if len(inner_dims) != 1:
+            raise ValueError(f"{name}: the order chunked({size}) sums one summed axis in chunks, and this sum runs over "
+                             f"{len(inner_dims)} axes")
+        if size == 0:
+            raise ValueError(f"{name}: the order chunked(0) has no chunk")
+        k = inner_dims[0]
+        bd = B()
+        ov = bd.loops(outer_dims)
+        cb, t, kvv = bd.iv(), bd.iv(), bd.iv()
+        acc, part = bd.sv(), bd.sv()
+        term = bin_("*", load(0, index_x(ov, [kvv])), load(1, index_y(ov, [kvv])))
+
+        def chunk(start, length):
+            return [Set(part, num(0)),
+                    For(t, length, [SetL(kvv, bin_("+", start, iv(t))), Set(part, bin_("+", sv(part), term))]),
+                    Set(acc, bin_("+", sv(acc), sv(part)))]
+        body = [Set(acc, num(0))]
+        if k // size > 0:
+            body.append(For(cb, k // size, chunk(bin_("*", iv(cb), str(size)), size)))
+        if k % size > 0:
+            body.extend(chunk(str(k // size * size), k % size))
+        body.append(Store(2, ivs(ov), sv(acc)))
+        return kernel(name, dtype, ins, out, "real", bd, nest(ov, outer_dims, body))
+    bd = B()
+    ov = bd.loops(outer_dims)
+    cv = bd.loops(inner_dims)
+    acc = bd.sv()
+    inner = nest(cv, inner_dims, [Set(acc, bin_("+", sv(acc), bin_("*", load(0, index_x(ov, cv)), load(1, index_y(ov, cv)))))])
+    body = [Set(acc, num(0))] + inner + [Store(2, ivs(ov), sv(acc))]
+    return kernel(name, dtype, ins, out, "real", bd, nest(ov, outer_dims, body))
+
+
+def _dot_ordered(ins, dtype, order) -> Lowered:
+    """lower.rs:481-510: `x[..., K] . w[K, rest...]` as `contraction_ordered`."""
+    x, w = ins[0], ins[1]
+    k = x.axes[-1].len
+    lead = len(x.axes) - 1
+    out = list(x.axes[:lead]) + list(w.axes[1:])
+    return contraction_ordered("dot", dtype, ins, out, dims(out), [k],
+                               lambda ov, cv: [iv(v) for v in ov[:lead]] + [iv(cv[0])],
+                               lambda ov, cv: [iv(cv[0])] + [iv(v) for v in ov[lead:]], order)
+
+
+def _dot_vjp_l_ordered(ins, dtype, order) -> Lowered:
+    """lower.rs:516-546: `ct[..., N...] . b[K, N...]^T -> [..., K]`."""
+    ct, b = ins[0], ins[1]
+    k = len(b.axes) - 1
+    lead = len(ct.axes) - k
+    out = list(ct.axes[:lead]) + [b.axes[0]]
+    return contraction_ordered("dot_vjp_l", dtype, ins, out, dims(out), [a.len for a in b.axes[1:]],
+                               lambda ov, cv: [iv(v) for v in ov[:lead]] + [iv(v) for v in cv],
+                               lambda ov, cv: [iv(ov[lead])] + [iv(v) for v in cv], order)
+
+
+def _dot_vjp_r_ordered(ins, dtype, order) -> Lowered:
+    """lower.rs:552-584: `a[..., K], ct[..., N...] -> [K, N...]` summed over
+    the leading axes."""
+    a, ct = ins[0], ins[1]
+    lead = len(a.axes) - 1
+    out = [a.axes[lead]] + list(ct.axes[lead:])
+    return contraction_ordered("dot_vjp_r", dtype, ins, out, dims(out), [x.len for x in a.axes[:lead]],
+                               lambda ov, cv: [iv(v) for v in cv] + [iv(ov[0])],
+                               lambda ov, cv: [iv(v) for v in cv] + [iv(v) for v in ov[1:]], order)
 
 
 def dot(ins, dtype, order=None, layout=None, epilogue=None) -> Lowered:
-    """`lower_planned` for `dot` (lower.rs:263-266 via Contraction::of)."""
-    c = contraction_of("dot", ins)
+    """`lower_planned` for `dot` (lower.rs:250-266): a contraction nest
+    (Contraction::of, only under an exact order) in its layout, else
+    `dot`'s ordered form."""
+    c = contraction_of("dot", ins) if exact_order(order) else None
     if c is None:
-        raise ValueError("not a contraction nest")
-    if order and order[0] == "chunked":
-        return contraction_chunked(c, dtype, ins, order[1])
+        if epilogue is not None:
+            raise ValueError("dot: an epilogue is a contraction nest's")
+        return _dot_ordered(ins, dtype, order)
     return emit_contraction(c, dtype, ins, layout, epilogue)
 
 
 def dot_vjp_l(ins, dtype, order=None) -> Lowered:
-    c = contraction_of("dot_vjp_l", ins)
-    if order and order[0] == "chunked":
-        return contraction_chunked(c, dtype, ins, order[1])
+    c = contraction_of("dot_vjp_l", ins) if exact_order(order) else None
+    if c is None:
+        return _dot_vjp_l_ordered(ins, dtype, _chunked_only(order))
     return emit_contraction(c, dtype, ins)
 
 
 def dot_vjp_r(ins, dtype, order=None) -> Lowered:
-    c = contraction_of("dot_vjp_r", ins)
+    c = contraction_of("dot_vjp_r", ins) if exact_order(order) else None
+    if c is None:
+        return _dot_vjp_r_ordered(ins, dtype, _chunked_only(order))
     return emit_contraction(c, dtype, ins)
 
 
-def ein(ins, operands, output, dtype) -> Lowered:
+def ein(ins, operands, output, dtype, order=None) -> Lowered:
     """`ein` (lower.rs:586-636): a contraction nest where the operands' roles
-    fit one (`Contraction::of`), else the generic many-operand form: one
-    accumulator per output element over the summed axes, its term
-    `(1 * x0) * x1 ...`."""
-    c = contraction_of("ein", ins, operands, output)
+    fit one (`Contraction::of`, under an exact order), else under a chunked
+    order the chunked contraction of two operands over one summed axis, else
+    the generic many-operand form: one accumulator per output element over
+    the summed axes, its term `(1 * x0) * x1 ...`."""
+    c = contraction_of("ein", ins, operands, output) if exact_order(order) else None
     if c is not None:
         return emit_contraction(c, dtype, ins)
+    order = _chunked_only(order)
     names = []
     for t, ns in zip(ins, operands):
         for a, n in zip(t.axes, ns):
@@ -610,6 +716,17 @@ def ein(ins, operands, output, dtype) -> Lowered:
                 names.append((n, a.len))
     contracted = [(n, l) for n, l in names if n not in output]
     out = [Axis(o, next(l for n, l in names if n == o)) for o in output]
+    name = f"ein[{', '.join(output)}]"
+    if order is not None:
+        if len(ins) != 2 or len(contracted) != 1:
+            raise ValueError(f"{name}: the order chunked({order[1]}) sums the product of two operands over one summed "
+                             f"axis in chunks, and this one has {len(ins)} operands and {len(contracted)} summed axes")
+        pos = [[output.index(n) if n in output else None for n in ns] for ns in operands]
+
+        def at(ix, ov, cv):
+            return [iv(cv[0] if p is None else ov[p]) for p in ix]
+        return contraction_ordered(name, dtype, ins, out, dims(out), [contracted[0][1]],
+                                   lambda ov, cv: at(pos[0], ov, cv), lambda ov, cv: at(pos[1], ov, cv), order)
     allv = list(output) + [n for n, _ in contracted]
     bd = B()
     ov = bd.loops(dims(out))

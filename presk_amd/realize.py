@@ -36,6 +36,8 @@ class Realization:
         self.functions = dict(functions or {})
         self.params = dict(params or {})
         self.order = order or {"kind": "sequential"}
+        from .lower import order_of
+        order_of(self.order)      # refuses an order the schema does not have (E7001)
         self.quant = {}
         for path, q in (quant or {}).items():
             if isinstance(q, Quant):

@@ -48,3 +48,23 @@ def test_mixed_realization_exact(train):
     hip.sync()
     assert all(p.bufs.download(o).tobytes() == v for o, v in eager.items())
     p.release_batch()
+
+
+@pytest.mark.parametrize("order", [{"kind": "interleaved", "partials": 4}, {"kind": "chunked", "size": 8}])
+def test_declared_order_program_exact(order):
+    """The course GPT's forward under a realization's reassociating order
+    (every `dot` interleaved, or every contraction chunked): every buffer
+    equals the oracle's run of the same nests."""
+    s = gpt.TINY
+    r = Realization.of_json({"default": "bf16", "order": order})
+    print(f"[order] {order}", flush=True)
+    p, b, names = gpt.build(s, "bf16", train=False, mode=hip.EXACT, realize=r)
+    host = gpt.host_inputs(s)
+    env = cpu_program.run(p, host)
+    p.compile()
+    configs.load_inputs(p, host)
+    p.prepare()
+    p.run()
+    hip.sync()
+    bad = [ln.out for ln in p.launches if p.bufs.download(ln.out).tobytes() != np.ascontiguousarray(env[ln.out]).tobytes()]
+    assert not bad, bad[:5]

@@ -1,8 +1,9 @@
-"""The FAST-mode column sum (`sum_to` onto trailing axes) in its declared
-order: the reference's `ReductionOrder::Chunked { size: 64 }` semantics
-(crates/presk-kernel/src/lower.rs:427-464: chunks of 64 consecutive rows each
-summed from zero in order, the chunk sums added in order from zero) with f32
-accumulation.  The same order is written here as a PSK-Kernel nest and run by
+"""The FAST-mode column sum (`sum_to` onto trailing axes) in the executor's
+own declared order, `rows-in-chunks(64)-f32`: chunks of 64 consecutive rows
+each summed from zero in order, the chunk sums added in order from zero, in
+f32 -- the shape of the reference's `ReductionOrder::Chunked { size: 64 }`
+(crates/presk-kernel/src/lower.rs:427-464), which a realization applies to
+contractions only.  The same order is written here as a PSK-Kernel nest and run by
 the oracle; the device must give its bits exactly.  Also the row-nest class
 at sizes beyond the zoo's, and the token scatter of `embed_vjp` over several
 scan rounds, bit-exact against the oracle."""
@@ -218,7 +219,7 @@ def chunked_total_text(n, dtype, mean, chunk=64, squares=False):
 @pytest.mark.parametrize("op", ["mean_all", "sum_all"])
 @pytest.mark.parametrize("mode", [hip.FAST, hip.EXACT])
 def test_totals(dt, op, mode):
-    """sum_all / mean_all over 64 x 300 elements: FAST in the chunked(64)
+    """sum_all / mean_all over 64 x 300 elements: FAST in the rows-in-chunks(64)
     order (colsum class), EXACT in index order through the long-row walk
     (rows class, one workgroup staging 4096 elements at a time)"""
     rows = O(A(("batch", 64), ("seq", 300)))
@@ -337,7 +338,7 @@ def test_short_rows_kept_in_registers(dt, T):
 @pytest.mark.parametrize("n", [1500, 590_000])
 def test_sum_squares(dt, mode, n):
     """sum_squares (the optimizer's clipping, lower.rs:1693-1703): FAST in the
-    chunked(64) order with the terms x * x (colsum class: a part chunk, and
+    rows-in-chunks(64) order with the terms x * x (colsum class: a part chunk, and
     9 219 chunks over two segments of the final chain), EXACT in index order;
     bit-exact against the oracle's run of the order as a nest"""
     x = O(A(("model", n)))
@@ -354,3 +355,28 @@ def test_sum_squares(dt, mode, n):
     out = hip.DeviceBuffer(nb)
     ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], out, lanes=low.lanes)
     assert out.download(np.uint8, nb).tobytes() == want.view(np.uint8).tobytes()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_fast_sum_to_band_at_config4_size(dt):
+    """The bias gradients' column sums at config 4's size ([64, 256, 384] ->
+    [384]) against a float64 sum: two f32 orders of a sum of n terms differ
+    by at most gamma_n sum|x| (n = 64 in a chunk + 256 chunk sums), plus one
+    unit of the storage type for the stored total."""
+    B, T, D = 64, 256, 384
+    x = O(A(("batch", B), ("seq", T), ("model", D)))
+    low = L.sum_to([x, O(A(("model", D)))], dt)
+    ex = hip.HipExec(0, mode=hip.FAST)
+    c = ex.compiled(low.text, dt, low.lanes)
+    assert c.kind == "colsum" and c.order == "rows-in-chunks(64)-f32"
+    rng = np.random.default_rng(11)
+    xs = fmt.encode(rng.standard_normal((B, T, D)).astype(np.float32), dt)
+    out = hip.DeviceBuffer(D * hip.STORAGE_BYTES[dt])
+    ex.run(low.text, dt, [hip.DeviceBuffer.of(xs), hip.DeviceBuffer.of(np.zeros(D * hip.STORAGE_BYTES[dt], np.uint8))], out)
+    got = fmt.decode(out.download(np.float32 if dt == "f32" else np.uint16), dt).astype(np.float64)
+    xv = fmt.decode(xs, dt).astype(np.float64).reshape(B * T, D)
+    exact = xv.sum(axis=0)
+    n, u = 64 + B * T // 64, 2.0 ** -24
+    ulp = {"f32": 2.0 ** -24, "bf16": 2.0 ** -8}[dt]
+    bound = n * u / (1 - n * u) * np.abs(xv).sum(axis=0) + ulp * np.abs(exact)
+    assert np.all(np.abs(got - exact) <= bound)

@@ -81,6 +81,18 @@ def cases(dtypes=("f32", "bf16", "f16", "e8m15")):
     out.append(("dot_rowwise-f32", L.dot([x, O(A(7, 3))], "f32")))
     out.append(("dot+add_rowwise-f32", L.dot([x, O(A(7, 3)), O(A(3))], "f32", epilogue=(True, A(("batch", 5), 3)))))
     out.append(("dot_chunked4-f32", L.dot([O(A(("batch", 5), 10)), O(A(10, 8))], "f32", order=("chunked", 4))))
+    # the declared orders a realization applies to contractions
+    # (lower.rs:250-303, 384-475): interleaved on `dot`, chunked on its
+    # derivatives and on `ein`
+    for dt in ("f32", "bf16", "f16"):
+        out.append((f"dot_interleaved4-{dt}", L.dot([O(A(("batch", 5), 12)), O(A(12, 8))], dt, order=("interleaved", 4))))
+        out.append((f"dot_interleaved5_ragged-{dt}", L.dot([O(A(("batch", 5), 12)), O(A(12, 8))], dt, order=("interleaved", 5))))
+        out.append((f"dot_vjp_l_chunked5-{dt}", L.dot_vjp_l([O(A(("batch", 4), 12)), O(A(7, 12))], dt, order=("chunked", 5))))
+        out.append((f"dot_vjp_r_chunked8-{dt}", L.dot_vjp_r([O(A(("batch", 20), 6)), O(A(("batch", 20), 7))], dt, order=("chunked", 8))))
+        q = O(A(("heads", 2), ("seq", 5), ("hd", 9)))
+        k = O(A(("heads", 2), ("seq2", 5), ("hd", 9)))
+        out.append((f"ein_chunked4-{dt}", L.ein([q, k], [["heads", "seq", "hd"], ["heads", "seq2", "hd"]], ["heads", "seq", "seq2"], dt,
+                                               order=("chunked", 4))))
     return out
 
 
