@@ -22,6 +22,56 @@ from .program import Program
 A, O = L.ax, L.Operand
 
 
+def _narrow(x: np.ndarray, t: int, w: int) -> np.ndarray:
+    """The code of a float with t fraction and w exponent bits nearest each
+    f64, rounded once, ties to even: codes.rs's `narrow`
+    (crates/presk-rt/src/codes.rs:29-59) over arrays -- a NaN keeps its sign
+    and top payload bits, made quiet; an f64 subnormal is a signed zero; past
+    the largest finite number, the infinity."""
+    b = np.ascontiguousarray(x, dtype=np.float64).view(np.uint64).ravel()
+    one = np.uint64(1)
+    sign = (b >> np.uint64(63)) << np.uint64(t + w)
+    inf = np.uint64(((1 << w) - 1) << t)
+    ab = b & np.uint64((1 << 63) - 1)
+    field = (ab >> np.uint64(52)).astype(np.int64)
+    m = (ab & np.uint64((1 << 52) - 1)) | np.uint64(1 << 52)
+    lead = field - 1023
+    bias = (1 << (w - 1)) - 1
+    emin = 1 - bias
+    shift = 52 - t + np.maximum(emin - lead, 0)
+    s = np.minimum(shift, 63).astype(np.uint64)
+    q = m >> s
+    low = m & ((one << s) - one)
+    half = one << (s - one)
+    r = q + ((low > half) | ((low == half) & ((q & one) == one))).astype(np.uint64)
+    r = np.where(shift > 63, np.uint64(0), r)
+    code = np.where(lead >= emin, (np.maximum(lead + bias - 1, 0).astype(np.uint64) << np.uint64(t)) + r, r)
+    out = sign | np.minimum(code, inf)
+    nan = sign | inf | np.uint64(1 << (t - 1)) | ((ab >> np.uint64(52 - t)) & np.uint64((1 << (t - 1)) - 1))
+    out = np.where(ab > np.uint64(0x7FF << 52), nan, out)
+    return np.where(field == 0, sign, out)
+
+
+def encode64(x, ty: str) -> np.ndarray:
+    """f64 values -> storage as the host's `Buf::of` makes it
+    (crates/presk-rt/src/lib.rs:868-876): f32 and binary16/e8m15 codes rounded
+    once from the f64, bf16 through the f32 (`f32_to_bf16(x as f32)`)."""
+    x = np.ascontiguousarray(x, dtype=np.float64).ravel()
+    if ty == "f64":
+        return x.copy()
+    if ty in ("f32", "bf16"):
+        with np.errstate(over="ignore"):
+            return encode(x.astype(np.float32), ty)
+    if ty == "f16":
+        return _narrow(x, 10, 5).astype(np.uint16)
+    if ty == "e8m15":
+        c = _narrow(x, 15, 8).astype(np.uint32)
+        out = np.empty(c.size * 3, dtype=np.uint8)
+        out[0::3], out[1::3], out[2::3] = c & 0xFF, (c >> 8) & 0xFF, (c >> 16) & 0xFF
+        return out
+    raise ValueError(ty)
+
+
 def encode(x: np.ndarray, ty: str) -> np.ndarray:
     """f32 values -> storage (rounded once, to nearest even)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
@@ -81,7 +131,7 @@ def mlp(rows=8192, d=768, hidden=3072, dtype="bf16", seed=1):
     p.add(L.dot([H, w2, b2], dtype, epilogue=(True, d2.out_axes)), ["g", "w2", "b2"], "y")
     p.add(L.elementwise_binary("add", [X, O(d2.out_axes)], dtype), ["x", "y"], "out")
     host = {"x": rng.standard_normal((rows, d)).astype(np.float32),
-            "eps": np.array([1e-5], np.float32),
+            "eps": np.array([1e-5], np.float64),
             "gamma": np.ones(d, np.float32), "beta": np.zeros(d, np.float32),
             "w1": xavier(rng, d, hidden), "b1": (rng.standard_normal(hidden) * 0.02).astype(np.float32),
             "w2": xavier(rng, hidden, d), "b2": (rng.standard_normal(d) * 0.02).astype(np.float32)}
@@ -108,6 +158,9 @@ def storage_inputs(p: Program, host: dict) -> dict:
                     qt = Q.quantize(np.asarray(v, np.float32).astype(np.float64), [a.len for a in axes],
                                     Q.Quant(q.bits, over, q.scheme))
                     env[name], env[name + "#scales"] = qt.data, qt.scales
+                elif np.asarray(v).dtype == np.float64:
+                    # the host's f64 values (literals, drawn inputs): one Buf::of
+                    env[name] = encode64(np.asarray(v).reshape(-1)[:max(count, 1)], ty)
                 else:
                     env[name] = encode(np.asarray(v, np.float32).reshape(-1)[:max(count, 1)], ty)
     return env

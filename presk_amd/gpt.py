@@ -503,7 +503,7 @@ def build(s: GptShape, dtype: str = "f32", train: bool = True, mode=None, realiz
     logits = b.dot(xf, "head", name="logits")
     ce = b.cross_entropy(logits, "y", name="ce")
     loss = b.mean_all(ce, name="loss")
-    names = {"loss": loss, "grads": {}}
+    names = {"loss": loss, "logits": logits, "grads": {}}
     if not train:
         return p, b, names
     G = names["grads"]
@@ -644,11 +644,12 @@ def optimizer_inputs(s: GptShape, t: int, total: int, hyper: dict = ADAMW) -> di
             n *= a.len
         out["m." + name] = np.zeros(n, np.float32)
         out["v." + name] = np.zeros(n, np.float32)
+    # the host's literals are f64s, each rounded once into its storage type
     for k, v in _OPT_LITS.items():
-        out[k] = np.array([float(hyper.get(v, v))], np.float32)
-    out["opt.pi"] = np.array([math.pi], np.float32)
-    out["opt.t"] = np.array([float(t)], np.float32)
-    out["opt.total"] = np.array([float(total)], np.float32)
+        out[k] = np.array([float(hyper.get(v, v))], np.float64)
+    out["opt.pi"] = np.array([math.pi], np.float64)
+    out["opt.t"] = np.array([float(t)], np.float64)
+    out["opt.total"] = np.array([float(total)], np.float64)
     return out
 
 
@@ -763,10 +764,10 @@ def host_inputs(s: GptShape, seed: int = 2) -> dict:
     rng = np.random.default_rng(seed + 100)
     host["ids"] = rng.integers(0, s.V, size=(s.B, s.T), dtype=np.int64)
     host["y"] = rng.integers(0, s.V, size=(s.B, s.T), dtype=np.int64)
-    host["eps"] = np.array([1e-5], np.float32)
-    host["scale"] = np.array([math.sqrt(float(s.HD))], np.float32)
-    host["two"] = np.array([2.0], np.float32)
-    host["one"] = np.array([1.0], np.float32)
+    host["eps"] = np.array([1e-5], np.float64)
+    host["scale"] = np.array([math.sqrt(float(s.HD))], np.float64)
+    host["two"] = np.array([2.0], np.float64)
+    host["one"] = np.array([1.0], np.float64)
     return host
 
 

@@ -321,7 +321,7 @@ def host_inputs(s: LlamaShape, seed: int = 5) -> dict:
             out[name] = (rng.standard_normal(shape) * 0.02).astype(np.float32)
     out["ids"] = rng.integers(0, s.V, size=(s.B, s.T), dtype=np.int64)
     for k, v in scalar_values(s).items():
-        out[k] = np.array([v], np.float32)
+        out[k] = np.array([v], np.float64)
     return out
 
 
@@ -361,7 +361,7 @@ def load_device_inputs(p: Program, s: LlamaShape, seed: int = 5):
         hip.check(lib.presk_hip_fill_normal(buf.ptr, ty.encode(), count, seed * 1000003 + i, mean, std, None))
     rng = np.random.default_rng(seed)
     host = {"ids": rng.integers(0, s.V, size=(s.B, s.T), dtype=np.int64)}
-    host.update({k: np.array([v], np.float32) for k, v in scalar_values(s).items()})
+    host.update({k: np.array([v], np.float64) for k, v in scalar_values(s).items()})
     for name, arr in configs.storage_inputs(p, host).items():
         ty, count = specs[name]
         p.declare(name, ty, max(count, 1))
