@@ -33,7 +33,9 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import lower as L
+from . import fusion as FU
 from . import quant as Q
+from .fusion import Let
 from .program import Program
 
 A, O = L.ax, L.Operand
@@ -653,40 +655,125 @@ def optimizer_inputs(s: GptShape, t: int, total: int, hyper: dict = ADAMW) -> di
     return out
 
 
-def _chain(b: Builder, steps, ins, like, name):
-    """One chain of the step's lets: a fused nest in f32 storage (its f32
-    intermediates are the values the lets store), else one nest a let, each
-    result stored -- rounded -- in the storage type, as the host runs the
-    tree operations one kernel at a time."""
-    if b.dt == "f32":
-        return b.fused(steps, ins, like, name=name)
-    vals = []
-    for k, (op, args) in enumerate(steps):
-        srcs = [ins[i] if kind == "in" else vals[i] for kind, i in args]
-        nm = name if k + 1 == len(steps) else f"{name}.{k}"
-        vals.append(b.binary(op, srcs[0], srcs[1], name=nm) if len(srcs) == 2 else b.unary(op, srcs[0], name=nm))
-    return vals[-1]
+# adamw.step's and adamw.lr's bodies as crates/presk-core/src/lower/optim.rs
+# emits them (optim.rs:160-237, 240-310: the clipped step and the cosine
+# schedule), each `let` (name, op, operands, type): `p` the parameter tree,
+# `s` a scalar.  A literal is `Real` of an f64 (not elementwise): the
+# program's 0-dim input of that value (`lit:<input>`); `Real` of a nat the
+# same (`real:<input>`); `pi` is PrimOp::Pi (not elementwise); `g`, `m`, `v`
+# and `theta` are the function's parameters; `lr` the call of adamw.lr.
+def _step_lets():
+    F = Let
+    return [
+        F("n2", "sum_squares", ["g"], "s"),
+        F("norm", "sqrt", ["n2"], "s"), F("tiny", "lit:opt.tiny", [], "s"), F("denom", "add", ["norm", "tiny"], "s"),
+        F("clip", "lit:opt.clip", [], "s"), F("coef", "div", ["clip", "denom"], "s"),
+        F("one_f", "lit:opt.one", [], "s"), F("fd", "sub", ["one_f", "coef"], "s"), F("fr", "relu", ["fd"], "s"),
+        F("factor", "sub", ["one_f", "fr"], "s"),
+        F("gc", "mul", ["g", "factor"], "p"),
+        F("one", "lit:opt.one", [], "s"), F("b1", "lit:opt.b1", [], "s"), F("b2", "lit:opt.b2", [], "s"),
+        F("omb1", "sub", ["one", "b1"], "s"), F("omb2", "sub", ["one", "b2"], "s"),
+        F("ma", "mul", ["m", "b1"], "p"), F("mc", "mul", ["gc", "omb1"], "p"), F("m2", "add", ["ma", "mc"], "p"),
+        F("va", "mul", ["v", "b2"], "p"), F("gg", "mul", ["gc", "gc"], "p"), F("vc", "mul", ["gg", "omb2"], "p"),
+        F("v2", "add", ["va", "vc"], "p"),
+        F("tr", "real:opt.t", [], "s"),
+        F("lnb1", "log", ["b1"], "s"), F("tl1", "mul", ["tr", "lnb1"], "s"), F("pw1", "exp", ["tl1"], "s"),
+        F("bc1", "sub", ["one", "pw1"], "s"),
+        F("lnb2", "log", ["b2"], "s"), F("tl2", "mul", ["tr", "lnb2"], "s"), F("pw2", "exp", ["tl2"], "s"),
+        F("bc2", "sub", ["one", "pw2"], "s"),
+        F("mhat", "div", ["m2", "bc1"], "p"), F("vhat", "div", ["v2", "bc2"], "p"), F("sq", "sqrt", ["vhat"], "p"),
+        F("eps", "lit:opt.eps", [], "s"), F("den", "add", ["sq", "eps"], "p"), F("upd", "div", ["mhat", "den"], "p"),
+        F("lam", "lit:opt.wd", [], "s"), F("decay", "mul", ["theta", "lam"], "p"), F("dir", "add", ["upd", "decay"], "p"),
+        F("lr", "call", [], "s"), F("scaled", "mul", ["dir", "lr"], "p"), F("theta2", "sub", ["theta", "scaled"], "p"),
+        F("s2", "tuple", ["m2", "v2"], "t"), F("res", "tuple", ["theta2", "s2"], "t"),
+    ], "res"
 
 
-def _min1(b: Builder, x, name):
-    """min(1, x) = 1 - relu(1 - x) (optim.rs's `min1`)."""
-    return _chain(b, [("sub", [("in", 0), ("in", 1)]), ("relu", [("step", 0)]), ("sub", [("in", 0), ("step", 1)])],
-                  ["opt.one", x], "opt.one", name)
+def _lr_lets():
+    F = Let
+    return [
+        F("base", "lit:opt.lr", [], "s"), F("tr", "real:opt.t", [], "s"), F("totr", "real:opt.total", [], "s"),
+        F("w", "lit:opt.w", [], "s"), F("one", "lit:opt.one", [], "s"),
+        F("q", "div", ["tr", "w"], "s"), F("one_w", "lit:opt.one", [], "s"), F("wd", "sub", ["one_w", "q"], "s"),
+        F("wr", "relu", ["wd"], "s"), F("warm", "sub", ["one_w", "wr"], "s"),
+        F("num", "sub", ["tr", "w"], "s"), F("den0", "sub", ["totr", "w"], "s"), F("den1", "sub", ["den0", "one"], "s"),
+        F("den2", "relu", ["den1"], "s"), F("den", "add", ["den2", "one"], "s"), F("q2", "div", ["num", "den"], "s"),
+        F("r2", "relu", ["q2"], "s"), F("one_p", "lit:opt.one", [], "s"), F("pd", "sub", ["one_p", "r2"], "s"),
+        F("pr", "relu", ["pd"], "s"), F("p", "sub", ["one_p", "pr"], "s"),
+        F("pi", "lit:opt.pi", [], "s"), F("x", "mul", ["pi", "p"], "s"), F("c", "cos", ["x"], "s"),
+        F("s", "add", ["one", "c"], "s"), F("half", "lit:opt.half", [], "s"), F("dec", "mul", ["s", "half"], "s"),
+        F("f", "mul", ["warm", "dec"], "s"), F("lr", "mul", ["base", "f"], "s"),
+    ], "lr"
+
+
+def _emit_body(b: Builder, lets, result, env: dict, leaves: list, tag: str, special=None):
+    """Runs a body's `let`s as the kernel host runs them: each fusion group
+    (presk_amd.fusion.plan) one nest at its root -- a group of the
+    parameter tree's type mapped over the tree's leaves, one nest a leaf
+    (fusion.rs:104-110) -- every other elementwise `let` a nest of its own,
+    the rest by `special(let, env)`.  `env` maps a value to its buffer, or
+    for a tree to {leaf: buffer}.  Returns `env`."""
+    groups = FU.plan(lets, result)
+    interior = {m for g in groups.values() for m in g.members if m != g.root}
+
+    def arg(v, leaf):
+        x = env[v]
+        return x[leaf] if isinstance(x, dict) else x
+
+    for lt in lets:
+        if lt.var in interior:
+            continue
+        if lt.op.startswith("lit:") or lt.op.startswith("real:"):
+            env[lt.var] = lt.op.split(":", 1)[1]
+            continue
+        if lt.op not in FU.ELEMENTWISE:
+            if special is not None:
+                special(lt, env)
+            continue
+        g = groups.get(lt.var)
+        steps = g.steps if g else [(lt.op, [("in", i) for i in range(len(lt.args))])]
+        ins = g.inputs if g else list(dict.fromkeys(lt.args))
+        if not g:
+            steps = [(lt.op, [("in", ins.index(a)) for a in lt.args])]
+        single = g is None and len(steps) == 1
+        if lt.ty == "p":
+            out = {}
+            for n in leaves:
+                srcs = [arg(v, n) for v in ins]
+                name = f"{tag}.{lt.var}.{n}"
+                if single and len(lt.args) == 2:
+                    out[n] = b.binary(lt.op, arg(lt.args[0], n), arg(lt.args[1], n), name=name)
+                elif single:
+                    out[n] = b.unary(lt.op, arg(lt.args[0], n), name=name)
+                else:
+                    out[n] = b.fused(steps, srcs, n, name=name)
+            env[lt.var] = out
+        else:
+            srcs = [arg(v, None) for v in ins]
+            name = f"{tag}.{lt.var}"
+            if single and len(lt.args) == 2:
+                env[lt.var] = b.binary(lt.op, arg(lt.args[0], None), arg(lt.args[1], None), name=name)
+            elif single:
+                env[lt.var] = b.unary(lt.op, arg(lt.args[0], None), name=name)
+            else:
+                env[lt.var] = b.fused(steps, srcs, "opt.one", name=name)
+    return env
 
 
 def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
-    """adamw.step (crates/presk-core/src/lower/optim.rs:171-237) over the
-    parameters and their gradients, as the host runs it: every tree
-    operation leaf by leaf (host.rs:1732-1787), the scalars as 0-dim
-    kernels, SumSquares as one `sum_squares` nest a leaf added in f64 on the
-    host in leaf order (host.rs:1571-1587) -- here f64 kernels over the
-    leaves' f32 scalars, read through the f32 -> f64 edge conversion, whose
-    result is read back through the f64 -> f32 one (`scalar`'s rounding).
-    Each leaf's m', v' and theta' are one chain each (`_chain`: fused in f32
-    storage, one nest a let in a narrower one).
-    The leaves are `opt_leaves`: a stacked leaf's parameters and gradients
-    are its layers' buffers, held one after another in one buffer
-    (Program.stack), as StackParams lays them out.
+    """adamw.step and adamw.lr (crates/presk-core/src/lower/optim.rs:160-310)
+    over the parameters and their gradients, as the kernel host runs them:
+    the bodies' fusion groups (crates/presk-core/src/fusion.rs:138, restated
+    in presk_amd/fusion.py) each one nest -- values inside a group in f32,
+    the arithmetic type, only its root stored in the storage type -- a group
+    over the parameter tree mapped leaf by leaf (host.rs:1732-1787), the
+    scalars as 0-dim kernels; SumSquares as one `sum_squares` nest a leaf
+    added in f64 on the host in leaf order (host.rs:1571-1587) -- here f64
+    kernels over the leaves' scalars read through the edge conversion to
+    f64, their result read back through the one to the storage type
+    (`scalar`'s rounding).  The leaves are `opt_leaves`: a stacked leaf's
+    parameters and gradients are its layers' buffers, held one after
+    another in one buffer (Program.stack), as StackParams lays them out.
     Returns {leaf: (theta', m', v')}."""
     leaves = opt_leaves(s)
     names = list(leaves)
@@ -707,54 +794,30 @@ def adamw(b: Builder, s: GptShape, grads: dict, hyper: dict = ADAMW) -> dict:
     for n in names:
         b.input("m." + n, b.axes[n])
         b.input("v." + n, b.axes[n])
-    out = {}
-    with b.func("adamw.step"):
-        # clipping to the global norm: g * min(1, c / (sqrt(sum g^2) + 1e-6))
-        ss = [b._prim(lambda dt, g=grads[n]: L.sum_squares([b.op(g)], dt), [grads[n]], f"opt.ss.{n}") for n in names]
-        acc = None
-        for i in range(0, len(ss), _SUM_CHUNK):
-            part = ss[i:i + _SUM_CHUNK]
-            ins = ([acc] if acc else []) + part
-            steps = [("add", [("in", 0), ("in", 1)])] + [("add", [("step", k), ("in", k + 2)]) for k in range(len(ins) - 2)]
-            name = f"opt.n2.{i // _SUM_CHUNK}"
-            acc = b._out(L.fused(steps, [b.op(x) for x in ins], [], "f64"), ins, name)
-        norm = _chain(b, [("sqrt", [("in", 0)]), ("add", [("step", 0), ("in", 1)]), ("div", [("in", 2), ("step", 1)])],
-                       [acc, "opt.tiny", "opt.clip"], "opt.one", "opt.coef")
-        factor = _min1(b, norm, "opt.factor")
-        omb = _chain(b, [("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b1"], "opt.one", "opt.omb1")
-        omb2 = _chain(b, [("sub", [("in", 0), ("in", 1)])], ["opt.one", "opt.b2"], "opt.one", "opt.omb2")
-        # bias corrections 1 - beta^t = 1 - exp(t * ln beta)
-        bc = [_chain(b, [("log", [("in", 1)]), ("mul", [("in", 2), ("step", 0)]), ("exp", [("step", 1)]),
-                       ("sub", [("in", 0), ("step", 2)])], ["opt.one", beta, "opt.t"], "opt.one", f"opt.bc{i + 1}")
-              for i, beta in enumerate(("opt.b1", "opt.b2"))]
     with b.func("adamw.lr"):
-        # cosine(warmup = w): lr * min(1, t/w) * (1 + cos(pi * min(1, relu((t - w) / (relu(total - w - 1) + 1))))) / 2
-        q = _chain(b, [("div", [("in", 0), ("in", 1)])], ["opt.t", "opt.w"], "opt.one", "opt.q")
-        warm = _min1(b, q, "opt.warm")
-        r = _chain(b, [("sub", [("in", 0), ("in", 2)]), ("sub", [("in", 1), ("in", 2)]), ("sub", [("step", 1), ("in", 3)]),
-                     ("relu", [("step", 2)]), ("add", [("step", 3), ("in", 3)]), ("div", [("step", 0), ("step", 4)]),
-                     ("relu", [("step", 5)])], ["opt.t", "opt.total", "opt.w", "opt.one"], "opt.one", "opt.r")
-        prog = _min1(b, r, "opt.p")
-        lr = _chain(b, [("mul", [("in", 0), ("in", 1)]), ("cos", [("step", 0)]), ("add", [("in", 2), ("step", 1)]),
-                      ("mul", [("step", 2), ("in", 3)]), ("mul", [("in", 4), ("step", 3)]), ("mul", [("in", 5), ("step", 4)])],
-                     ["opt.pi", prog, "opt.one", "opt.half", warm, "opt.lr"], "opt.one", "opt.lr_t")
+        lets, res = _lr_lets()
+        lr = _emit_body(b, lets, res, {}, names, "opt.lr")["lr"]
+
+    def special(lt, env):
+        if lt.op == "sum_squares":
+            # the global norm's square: each leaf's sum of squares, added in
+            # f64 in leaf order, at most _SUM_CHUNK a kernel
+            ss = [b._prim(lambda dt, g=grads[n]: L.sum_squares([b.op(g)], dt), [grads[n]], f"opt.ss.{n}") for n in names]
+            acc = None
+            for i in range(0, len(ss), _SUM_CHUNK):
+                part = ss[i:i + _SUM_CHUNK]
+                ins = ([acc] if acc else []) + part
+                steps = [("add", [("in", 0), ("in", 1)])] + [("add", [("step", k), ("in", k + 2)]) for k in range(len(ins) - 2)]
+                acc = b._out(L.fused(steps, [b.op(x) for x in ins], [], "f64"), ins, f"opt.n2.{i // _SUM_CHUNK}")
+            env[lt.var] = acc
+        elif lt.op == "call":
+            env[lt.var] = lr
     with b.func("adamw.step"):
-        for n in names:
-            g, m, v = grads[n], "m." + n, "v." + n
-            # m' = m b1 + (g factor)(1 - b1)
-            m2 = _chain(b, [("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("in", 4)]),
-                          ("add", [("step", 1), ("step", 2)])], [g, factor, m, "opt.b1", omb], n, f"opt.m2.{n}")
-            # v' = v b2 + (g factor)^2 (1 - b2)
-            v2 = _chain(b, [("mul", [("in", 0), ("in", 1)]), ("mul", [("in", 2), ("in", 3)]), ("mul", [("step", 0), ("step", 0)]),
-                          ("mul", [("step", 2), ("in", 4)]), ("add", [("step", 1), ("step", 3)])],
-                         [g, factor, v, "opt.b2", omb2], n, f"opt.v2.{n}")
-            # theta' = theta - lr (m'/bc1 / (sqrt(v'/bc2) + eps) + lambda theta)
-            th = _chain(b, [("div", [("in", 1), ("in", 2)]), ("div", [("in", 3), ("in", 4)]), ("sqrt", [("step", 1)]),
-                          ("add", [("step", 2), ("in", 5)]), ("div", [("step", 0), ("step", 3)]), ("mul", [("in", 0), ("in", 6)]),
-                          ("add", [("step", 4), ("step", 5)]), ("mul", [("step", 6), ("in", 7)]), ("sub", [("in", 0), ("step", 7)])],
-                         [n, m2, bc[0], v2, bc[1], "opt.eps", "opt.wd", lr], n, f"opt.theta.{n}")
-            out[n] = (th, m2, v2)
-    return out
+        lets, res = _step_lets()
+        env = {"g": {n: grads[n] for n in names}, "m": {n: "m." + n for n in names},
+               "v": {n: "v." + n for n in names}, "theta": {n: n for n in names}}
+        env = _emit_body(b, lets, res, env, names, "opt", special)
+    return {n: (env["theta2"][n], env["m2"][n], env["v2"][n]) for n in names}
 
 
 def host_inputs(s: GptShape, seed: int = 2) -> dict:

@@ -111,12 +111,13 @@ def test_dropout_step_graph_takes_each_steps_key():
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_tiny_gpt_step_with_adamw_exact_bits(dt):
-    """the training run's step with its optimizer (adamw.step, f32): the
-    clipped global norm summed in f64 through the edge conversions, the
-    schedule and bias corrections as 0-dim kernels, every leaf's moments
-    and parameters (the blocks' leaves stacked over the layers; in bf16
-    storage every let its own rounded nest) -- every buffer equal to the
-    oracle's, replayed as a graph too"""
+    """the training run's step with its optimizer (adamw.step and adamw.lr,
+    f32 and bf16 storage): the clipped global norm summed in f64 through the
+    edge conversions, each body's fusion groups as fusion.rs forms them (one
+    nest a group, f32 inside it, only its root stored: the schedule one 0-dim
+    nest, m', v' and theta' one nest a leaf), every leaf's moments and
+    parameters (the blocks' leaves stacked over the layers) -- every buffer
+    equal to the oracle's, replayed as a graph too"""
     s = gpt.TINY
     p, b, names = gpt.build(s, dt, train=True, mode=hip.EXACT, optimizer=True)
     host = gpt.host_inputs(s)
