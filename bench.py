@@ -10,8 +10,12 @@ seeded inputs already resident in HBM: every launch of the program
 from __future__ import annotations
 
 import argparse
+import gc
+import hashlib
 import json
 import os
+import statistics
+import subprocess
 import sys
 import time
 
@@ -80,19 +84,32 @@ def launch_key(ln) -> str:
     return f"{ln.low.text.splitlines()[0].rstrip(' {')} | {c.kind} {c.order}"
 
 
+def source_sha() -> str:
+    """sha1 of the executor's device sources: a traffic figure measured on
+    other sources is stale."""
+    h = hashlib.sha1()
+    csrc = os.path.join(ROOT, "presk_amd", "csrc")
+    for f in sorted(os.listdir(csrc)):
+        if f.endswith((".hip", ".cpp", ".hpp")):
+            with open(os.path.join(csrc, f), "rb") as fh:
+                h.update(f.encode() + fh.read())
+    return h.hexdigest()[:16]
+
+
 def _traffic_table() -> dict:
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, then
     WRITE_SIZE, each scaled by the copy probe's reading), as committed in
-    profiles/traffic.json: {launch key: bytes}."""
+    profiles/traffic.json: {launch key: bytes}, empty when the table was
+    measured on other device sources than these."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return {e["key"]: e["bytes_per_launch"] for e in json.load(f)["launches"]}
+            t = json.load(f)
+        if t.get("src_sha") != source_sha():
+            return {}
+        return {e["key"]: e["bytes_per_launch"] for e in t["launches"]}
     except (OSError, ValueError, KeyError):
         return {}
-
-
-TRAFFIC = _traffic_table()
 
 
 def copy_probe():
@@ -111,21 +128,159 @@ def copy_probe():
     print(json.dumps({"copy_probe": low.name, "bytes_read": 4 * n, "bytes_written": 4 * n, "runs": 3}), flush=True)
 
 
-def cpu_baseline(name: str, dtype: str, rows: int, threads: int, realize=None, dropout=0.0, adamw=False):
-    """The oracle (the kernel interpreter's semantics in C, -O3 -march=native,
-    the outermost parallel loop split over OpenMP threads as the native
-    executor splits it) on a bounded sample of the workload's rows."""
+def cpu_child(name, dtype, rows, threads, core, realize, dropout, adamw):
+    """One timed call of the oracle's C restatement in this process (a child
+    of bench.py, started before the GPU is touched), its kernels loaded from
+    the oracle's build cache first; prints {"secs": .., "tokens": ..}."""
+    if core >= 0:
+        os.sched_setaffinity(0, {core})
     from tests import cpu_program
-
     p, host, tokens, _, _ = workload(name, dtype, rows, realize, dropout, adamw)
     cpu_program.compile_all(p, native=True, workers=threads)
-    best = None
-    for _ in range(1 if name.startswith("gpt") else 2):
-        t0 = time.perf_counter()
-        cpu_program.run(p, host, threads=threads, native=True)
-        dt = time.perf_counter() - t0
-        best = dt if best is None else min(best, dt)
-    return tokens / best, best, tokens
+    t0 = time.perf_counter()
+    cpu_program.run(p, host, threads=threads, native=True)
+    secs = time.perf_counter() - t0
+    print(json.dumps({"secs": secs, "tokens": tokens}), flush=True)
+
+
+def cpu_baseline(name, dtype, rows_all, rows_one, realize=None, dropout=0.0, adamw=False, repeats=3):
+    """The oracle (the kernel interpreter's semantics in C, -O3
+    -march=native, sequential sums, the outermost parallel loop split over
+    OpenMP threads as the native executor splits it) on bounded samples of
+    the workload: `repeats` processes on every host core (capped at 16), one
+    after another, and `repeats` one-core processes side by side, each on a
+    core of its own.  The median and the best of each, as the reference's
+    `presk bench` reports (crates/presk-driver/src/bench.rs:28-48), over
+    separate processes (docs/kernels-roadmap.md:482-484).  Runs before the
+    GPU is touched."""
+    from tests import cpu_program
+    cores = sorted(os.sched_getaffinity(0))
+    threads = min(len(cores), 16)
+    # the kernels compiled once, into the oracle's disk cache the children read
+    for rows in (rows_all, rows_one):
+        p, _, _, _, _ = workload(name, dtype, rows, realize, dropout, adamw)
+        cpu_program.compile_all(p, native=True, workers=threads)
+
+    def child(rows, th, core):
+        cmd = [sys.executable, os.path.abspath(__file__), "--cpu-child", str(rows), str(th), str(core),
+               "--workload", name, "--dtype", dtype, "--dropout", str(dropout)]
+        if realize:
+            cmd += ["--realize", realize]
+        if adamw:
+            cmd.append("--adamw")
+        env = dict(os.environ, OMP_NUM_THREADS=str(th))
+        return subprocess.Popen(cmd, stdout=subprocess.PIPE, text=True, env=env)
+
+    def collect(procs):
+        out = []
+        for pr in procs:
+            text, _ = pr.communicate()
+            if pr.returncode != 0:
+                raise RuntimeError(f"cpu baseline child failed ({pr.returncode})")
+            out.append(json.loads(text.strip().splitlines()[-1]))
+        return out
+
+    every = [collect([child(rows_all, threads, -1)])[0] for _ in range(repeats)]
+    one = collect([child(rows_one, 1, cores[(i * 2) % len(cores)]) for i in range(repeats)])
+
+    def summary(rs):
+        rates = sorted(r["tokens"] / r["secs"] for r in rs)
+        return statistics.median(rates), rates[-1], rs[0]["tokens"], [round(r["secs"], 3) for r in rs]
+
+    med, best, toks, secs = summary(every)
+    med1, best1, toks1, secs1 = summary(one)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(med, 1), "best": round(best, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": model, "repeats": repeats,
+            "sample": f"{toks} tokens of the same workload (B {max(toks // 256, 1)} x T 256), {repeats} processes "
+                      f"({secs} s a call): the oracle's C restatement of the same nests (-O3 -march=native, "
+                      f"-ffp-contract=off, sequential sums, the outermost parallel loop split over {threads} OpenMP "
+                      f"threads); value = the median, best = the fastest",
+            "one_core": {"value": round(med1, 2), "best": round(best1, 2), "unit": "tokens/s", "cores": 1,
+                         "sample": f"{toks1} tokens, {repeats} one-thread processes side by side on separate cores "
+                                   f"({secs1} s a call)"}}
+
+
+def measure(name, dtype, steps, warmup, realize=None, dropout=0.0, adamw=False, eager=False, dominant_match=None):
+    """Times one workload: its launches as one HIP graph (or eager), W untimed
+    calls, K timed between synchronizations; then each launch alone with HIP
+    events on its stream, the slowest giving the roofline.  Returns
+    (record, program, the dominant launch)."""
+    from presk_amd import configs, hip
+    p, host, tokens, flops, cfg = workload(name, dtype, realize=realize, dropout=dropout, adamw=adamw)
+    step_keys = []
+    if p.masks:
+        from presk_amd import gpt, keys
+        run_key = keys.from_seed(0)
+        step_keys = [gpt.site_keys(gpt.COURSE, keys.child(run_key, i)) for i in range(warmup + steps)]
+    p.compile()
+    if host is None:
+        from presk_amd import llama
+        llama.load_device_inputs(p, llama.LLAMA_7B)
+    else:
+        configs.load_inputs(p, host)
+    p.prepare()
+    if not eager:
+        p.record(graph=True)
+    for i in range(warmup):
+        if step_keys:
+            p.set_keys(step_keys[i])
+        p.run()
+    hip.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if step_keys:
+            p.set_keys(step_keys[warmup + i])
+        p.run()
+    hip.sync()
+    dt = time.perf_counter() - t0
+    p.check_overflow()
+    ms_step = dt * 1000.0 / steps
+    times = p.kernel_times(reps=max(min(steps, 20), 10))
+    pool = [t for t in times if dominant_match is None or dominant_match in launch_key(t[0])] or times
+    ln, ms = max(pool, key=lambda t: t[1])
+    c = ln.compiled
+    traffic = TRAFFIC.get(launch_key(ln))
+    if c.flops > 0:
+        achieved = c.flops / (ms * 1e-3) / 1e12
+        peak = PEAK_TFLOPS[ln.low.dtype]
+        roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "mfma", "achieved": round(achieved, 2),
+                "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
+                "ms_per_launch": round(ms, 5), "algorithmic_flops": c.flops}
+    else:
+        achieved = c.bytes / (ms * 1e-3) / 1e9
+        roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": HBM_GBS, "unit": "GB/s", "frac": round(achieved / HBM_GBS, 4), "traffic": traffic,
+                "ms_per_launch": round(ms, 5), "algorithmic_bytes": c.bytes}
+    if traffic is None:
+        roof["traffic_note"] = "no counter measurement of this kernel on these device sources (profiles/traffic.json)"
+    agg = {}
+    for l, m in times:
+        e = agg.setdefault(l.low.name, {"kernel": l.low.name, "kind": l.compiled.kind, "launches": 0, "ms": 0.0})
+        e["launches"] += 1
+        e["ms"] += m
+    per_kernel = sorted(agg.values(), key=lambda e: -e["ms"])[:16]
+    for e in per_kernel:
+        e["ms"] = round(e["ms"], 4)
+    # the contractions' time at the MFMA peak of each one's storage type
+    bound_ms = sum(l.compiled.flops / (PEAK_TFLOPS.get(l.low.dtype, PEAK_TFLOPS["f32"]) * 1e12) * 1e3
+                   for l in p.launches if l.compiled.kind == "gemm")
+    cfg = dict(cfg, launch="eager" if eager else "hip graph")
+    rec = {"value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+           "ms_per_step": round(ms_step, 4), "dtype": dtype if realize is None else "mixed", "config": cfg,
+           "matmul_tflops": round(flops / (ms_step * 1e-3) / 1e12, 2), "matmul_frac_of_peak": round(bound_ms / ms_step, 4),
+           "roofline": roof, "kernels": per_kernel, "kernel_ms_sum": round(sum(m for _, m in times), 4)}
+    return rec, p, (ln, c)
+
+
+# the other configurations, timed after the headline (rows of the same line)
+SUPPLEMENTARY = [("gpt-step", "bf16", None), ("gpt-forward", "f32", "@" + os.path.join(ROOT, "presk_amd", "realizations", "course_gpt_mixed.json")),
+                 ("linear", "f32", None), ("mlp", "bf16", None), ("llama", "bf16", None)]
 
 
 def main():
@@ -143,6 +298,7 @@ def main():
                     help="the training step's dropout rate (the course's 0.2): masks drawn on the device, a new "
                          "step key each step")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-supplementary", action="store_true", help="time the headline workload only")
     ap.add_argument("--eager", action="store_true", help="issue the launches one by one instead of one HIP graph")
     ap.add_argument("--dominant-only", type=int, default=0, metavar="N",
                     help="after the timing pass, run the dominant launch alone N times and exit (for rocprofv3 --pmc)")
@@ -152,111 +308,69 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain copy-like nest (neg over 64 Mi f32) 3 times and exit: the counters' calibration")
     ap.add_argument("--cpu-rows", type=int, default=None)
+    ap.add_argument("--cpu-child", nargs=3, type=int, default=None, metavar=("ROWS", "THREADS", "CORE"),
+                    help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
               "multi-GPU sharding is a design (DESIGN.md), not a run.", file=sys.stderr)
         sys.exit(2)
+    dtype = args.dtype or ("bf16" if args.workload in ("mlp", "llama") else "f32")
+    if args.cpu_child:
+        rows, th, core = args.cpu_child
+        cpu_child(args.workload, dtype, rows, th, core, args.realize, args.dropout, args.adamw)
+        return
+    # the CPU baseline first, in child processes, before the GPU is touched
+    cpu = None
+    if not args.no_cpu and not args.copy_probe and not args.dominant_only:
+        # gpt-step: B 16 x T 256, the batch of the reference's own published rows
+        rows_all = args.cpu_rows or {"mlp": 2048, "linear": 512, "gpt-step": 4096, "gpt-forward": 4096}.get(args.workload)
+        rows_one = {"mlp": 256, "linear": 64, "gpt-step": 256, "gpt-forward": 256}.get(args.workload)
+        if rows_all:
+            cpu = cpu_baseline(args.workload, dtype, rows_all, rows_one, args.realize, args.dropout, args.adamw)
 
-    from presk_amd import configs, hip
+    from presk_amd import hip
 
     if args.copy_probe:
         copy_probe()
         return
-    dtype = args.dtype or ("bf16" if args.workload in ("mlp", "llama") else "f32")
-    p, host, tokens, flops, cfg = workload(args.workload, dtype, realize=args.realize, dropout=args.dropout, adamw=args.adamw)
-    # a training run's keys: step i draws from Key::child(run key, i); the site
-    # keys are derived before the timed region, uploaded (608 bytes) each step
-    step_keys = []
-    if p.masks:
-        from presk_amd import gpt, keys
-        run_key = keys.from_seed(0)
-        step_keys = [gpt.site_keys(gpt.COURSE, keys.child(run_key, i)) for i in range(args.warmup + args.steps)]
-    p.compile()
-    if host is None:
-        from presk_amd import llama
-        llama.load_device_inputs(p, llama.LLAMA_7B)
-    else:
-        configs.load_inputs(p, host)
-    p.prepare()
-    if not args.eager:
-        # the step's 587 launches recorded once and replayed as one HIP graph
-        p.record(graph=True)
-    for i in range(args.warmup):
-        if step_keys:
-            p.set_keys(step_keys[i])
-        p.run()
-    hip.sync()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        if step_keys:
-            p.set_keys(step_keys[args.warmup + i])
-        p.run()
-    hip.sync()
-    dt = time.perf_counter() - t0
-    p.check_overflow()
-    ms_step = dt * 1000.0 / args.steps
-
-    # the dominant kernel: the launch with the largest time, timed alone with
-    # HIP events on its stream
-    times = p.kernel_times(reps=max(args.steps, 10))
-    pool = [t for t in times if args.dominant_match is None or args.dominant_match in launch_key(t[0])] or times
-    ln, ms = max(pool, key=lambda t: t[1])
-    c = ln.compiled
-    key = launch_key(ln)
+    rec, p, (ln, c) = measure(args.workload, dtype, args.steps, args.warmup, args.realize, args.dropout, args.adamw,
+                              args.eager, args.dominant_match)
     if args.dominant_only:
         hip.sync()
         for _ in range(args.dominant_only):
             hip.check(hip.lib().presk_hip_run(c.handle, ln.table, 0, max(c.split_bound, 0), None))
         hip.sync()
-        print(json.dumps({"dominant": key, "runs": args.dominant_only}), flush=True)
+        print(json.dumps({"dominant": launch_key(ln), "runs": args.dominant_only}), flush=True)
         return
-    traffic = TRAFFIC.get(key)
-    if c.flops > 0:
-        achieved = c.flops / (ms * 1e-3) / 1e12
-        peak = PEAK_TFLOPS[ln.low.dtype]
-        roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "mfma", "achieved": round(achieved, 2),
-                "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
-                "ms_per_launch": round(ms, 5), "algorithmic_flops": c.flops}
-    else:
-        achieved = c.bytes / (ms * 1e-3) / 1e9
-        roof = {"kernel": f"{ln.low.name} [{c.kind}, {c.order}]", "bound": "hbm", "achieved": round(achieved, 1),
-                "peak": HBM_GBS, "unit": "GB/s", "frac": round(achieved / HBM_GBS, 4), "traffic": traffic,
-                "ms_per_launch": round(ms, 5), "algorithmic_bytes": c.bytes}
-    # per nest name: launches and total ms (the step's time by kind of nest)
-    agg = {}
-    for l, m in times:
-        e = agg.setdefault(l.low.name, {"kernel": l.low.name, "kind": l.compiled.kind, "launches": 0, "ms": 0.0})
-        e["launches"] += 1
-        e["ms"] += m
-    per_kernel = sorted(agg.values(), key=lambda e: -e["ms"])[:16]
-    for e in per_kernel:
-        e["ms"] = round(e["ms"], 4)
-
-    cfg = dict(cfg, launch="eager" if args.eager else "hip graph")
-    # the contractions' time at the MFMA peak of each one's storage type over
-    # the step's time: flops / peak for one type, weighted for a mixed one
-    bound_ms = sum(l.compiled.flops / (PEAK_TFLOPS.get(l.low.dtype, PEAK_TFLOPS["f32"]) * 1e12) * 1e3
-                   for l in p.launches if l.compiled.kind == "gemm")
     metric = {"gpt-step": METRIC, "gpt-forward": "tokens/sec course-GPT forward and loss (config 3)",
               "llama": "tokens/sec Llama-7B-shaped forward (config 5); matmul TFLOP/s as % of MFMA peak"}.get(
         args.workload, f"rows/sec {args.workload} (a supplementary workload)")
-    rec = {"metric": metric, "value": round(tokens / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
-           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": DATA.get(args.workload, "synthetic (seeded N(0,1) inputs, xavier weights)"),
-           "config": cfg, "matmul_tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
-           "matmul_frac_of_peak": round(bound_ms / ms_step, 4), "roofline": roof,
-           "kernels": per_kernel}
-    if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
-        rows = args.cpu_rows or {"mlp": 4096, "linear": 1024, "gpt-step": 2048, "gpt-forward": 4096}[args.workload]
-        v, secs, n = cpu_baseline(args.workload, dtype, rows, threads, args.realize, args.dropout, args.adamw)
-        rec["cpu_baseline"] = {"value": round(v, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-                               "sample": f"{n} of {tokens} tokens (rows) of the same workload: the oracle's C restatement of "
-                                         f"the same default-layout nests (-O3 -march=native, -ffp-contract=off, sequential "
-                                         f"sums, the outermost parallel loop split over OpenMP threads): {secs:.2f} s"}
-    print(json.dumps(rec), flush=True)
+    out = {"metric": metric, "value": rec["value"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": rec["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": rec["dtype"],
+           "data": DATA.get(args.workload, "synthetic (seeded N(0,1) inputs, xavier weights)"),
+           "config": rec["config"], "matmul_tflops": rec["matmul_tflops"], "matmul_frac_of_peak": rec["matmul_frac_of_peak"],
+           "roofline": rec["roofline"], "kernels": rec["kernels"], "kernel_ms_sum": rec["kernel_ms_sum"]}
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
+    del p
+    if not args.no_supplementary and args.workload == "gpt-step" and not args.realize and not args.adamw and not args.eager:
+        sup = []
+        for name, dt, real in SUPPLEMENTARY:
+            if (name, dt) == (args.workload, dtype):
+                continue
+            r, q, _ = measure(name, dt, 10 if name != "llama" else 5, 3 if name != "llama" else 2, real)
+            del q
+            gc.collect()
+            sup.append({k: r[k] for k in ("value", "unit", "ms_per_step", "dtype", "config", "matmul_tflops",
+                                          "matmul_frac_of_peak", "roofline")})
+            print(f"[bench] {name} {dt}: {r['ms_per_step']} ms", file=sys.stderr, flush=True)
+        out["supplementary"] = sup
+    print(json.dumps(out), flush=True)
 
+
+TRAFFIC = _traffic_table()
 
 if __name__ == "__main__":
     main()
