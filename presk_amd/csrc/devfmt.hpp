@@ -111,6 +111,27 @@ PK_DEV void pk_st24(unsigned char* p, long long e, unsigned c) {
     p[3 * e + 2] = (unsigned char)(c >> 16);
 }
 
+// x / z correctly rounded, by Markstein's method for a divisor used many
+// times (P. Markstein, "Computation of elementary functions on the IBM RISC
+// System/6000 processor", IBM J. Res. Dev. 34(1), 1990; J.-M. Muller et al.,
+// Handbook of Floating-Point Arithmetic, the theorem on the correction
+// step): with rz = RN(1/z), q0 = RN(x * rz) lies within one ulp of x / z,
+// the residual x - z * q0 is exact in an fma, and RN(q0 + r * rz) is
+// RN(x / z) -- when neither the quotient nor the residual leaves the normal
+// range.  pk_div_by_ok says when that holds (x zero, or |x| in [2^-100,
+// 2^100] with z in [1, 2^24]: the quotient then lies in [2^-124, 2^100]);
+// elsewhere the caller divides.
+PK_DEV float pk_div_by(float x, float z, float rz) {
+    const float q0 = x * rz;
+    const float r = __builtin_fmaf(-q0, z, x);
+    // a zero quotient keeps x's sign (the correction step would give +0)
+    return x == 0.f ? q0 : __builtin_fmaf(r, rz, q0);
+}
+PK_DEV bool pk_div_by_ok(float x, float z) {
+    const float ax = __builtin_fabsf(x);
+    return z >= 1.f && z <= 16777216.f && (x == 0.f || (ax >= 0x1p-100f && ax <= 0x1p100f));
+}
+
 // Rust's `f as i64`: saturating, NaN to zero.
 PK_DEV long long pk_i64(double x) {
     if (x != x) return 0;

@@ -534,7 +534,29 @@ __device__ __forceinline__ void exps(float (&f)[VEC], float m, unsigned al) {
     }
 }
 
-constexpr int SR = 16, SCW = 64, STS = SCW + 4;   // STS = 4 (mod 32): b128 tile reads and writes
+// f[u] <- f[u] / z, correctly rounded: Markstein's correction step with
+// rz = 1/z (pk_div_by), the division itself for a wave where some element
+// falls outside the range the step is exact in -- the same bits.
+template <int VEC>
+__device__ __forceinline__ void quotients(float (&f)[VEC], float z, float rz) {
+    float q[VEC];
+    bool need = false;
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+        q[u] = pk_div_by(f[u], z, rz);
+        need = need || !pk_div_by_ok(f[u], z);
+    }
+    if (__any(need)) {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) q[u] = pk_div_by_ok(f[u], z) ? q[u] : f[u] / z;
+    }
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) f[u] = q[u];
+}
+
+// SR rows a wave (eight waves a SIMD hide the passes' latency better than
+// fewer, longer ones), SD chunks of loads in flight
+constexpr int SR = 8, SCW = 64, STS = SCW + 4, SD = 4;   // STS = 4 (mod 32): b128 tile reads and writes
 
 // A lane moves 16 bytes a load: VEC elements of one row.  Lane l in slot q of
 // a chunk holds row q * RPI + l / LPR, columns (l % LPR) * VEC ..+VEC.
@@ -592,19 +614,58 @@ __global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
         if (!MASKED) return live;
         return (mrow[q][c >> 5] >> (c & 31)) & live;
     };
-    auto pass = [&](auto&& body) {
-        U4 w[NQ], nx[NQ];
-        load(0, w);
-        for (long long c0 = 0; c0 < n; c0 += SCW) {
-            const bool more = c0 + SCW < n;
-            if (more) load(c0 + SCW, nx);
-            body(c0, w);
-            if (more) {
+    // whether any of the group's rows allows an element of the chunk at c0:
+    // a chunk no row allows adds nothing to a max or to a sum (z + 0 is z)
+    // and stores zeros, so it is neither read nor computed (the rows above a
+    // causal mask's diagonal).  The verdicts of 64 chunks at a time, one
+    // chunk a lane (its two mask words in each of the group's rows, all
+    // loads in flight together), joined by a ballot.
+    unsigned long long lmask = ~0ull;
+    long long lbase = -1;
+    auto live = [&](long long c0) -> bool {
+        if (!MASKED) return true;
+        const long long ch = c0 / SCW, grp = ch / 64;
+        if (grp != lbase) {
+            lbase = grp;
+            const long long mine = grp * 64 + lane;
+            unsigned any = 0u;
+            if (mine * SCW < n) {
 #pragma unroll
-                for (int q = 0; q < NQ; ++q) w[q] = nx[q];
+                for (int r = 0; r < SR; ++r) {
+                    const unsigned* w = a.mbits + ((row0 + (r < nr ? r : nr - 1) + a.mask_row0) % a.mask_rows) * MW + 2 * mine;
+                    any |= w[0] | w[1];
+                }
+            }
+            lmask = __ballot(any != 0u);
+        }
+        return (lmask >> (ch - lbase * 64)) & 1ull;
+    };
+    // a pass over the row group's chunks, SD chunks' loads in flight ahead
+    // of the one in use (a ring of registers, its slots fixed by unrolling)
+    auto pass = [&](auto&& body, auto&& dead) {
+        const long long nch = (n + SCW - 1) / SCW;
+        U4 ring[SD][NQ];
+        bool lv[SD];
+#pragma unroll
+        for (int j = 0; j < SD; ++j) {
+            lv[j] = j < nch && live((long long)j * SCW);
+            if (lv[j]) load((long long)j * SCW, ring[j]);
+        }
+        for (long long c = 0; c < nch; c += SD) {
+#pragma unroll
+            for (int j = 0; j < SD; ++j) {
+                const long long ch = c + j;
+                if (ch < nch) {
+                    if (lv[j]) body(ch * SCW, ring[j]);
+                    else dead(ch * SCW);
+                    const long long nx = ch + SD;
+                    lv[j] = nx < nch && live(nx * SCW);
+                    if (lv[j]) load(nx * SCW, ring[j]);
+                }
             }
         }
     };
+    auto nothing = [](long long) {};
 
     // 1. the max: each lane's allowed non-NaN max and first allowed column,
     //    per row it holds; joined over the row's lanes
@@ -629,7 +690,7 @@ __global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
                 fa[q] = ok && fa[q] == BIG ? (int)(c0 + lc + u) : fa[q];
             }
         }
-    });
+    }, nothing);
     float mq[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -677,13 +738,14 @@ __global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
             }
         }
         __syncthreads();
-    });
-    float zq[NQ];
+    }, nothing);
+    float zq[NQ], rz[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
         // row q * RPI + lane / LPR's z, from its walking lane
         const int src = q * RPI + lane / LPR;
         zq[q] = __shfl(z, src, 64);
+        rz[q] = 1.f / zq[q];
     }
 
     // 3. the outputs, 16 bytes a lane
@@ -699,17 +761,14 @@ __global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
             exps<VEC>(f, mq[q], al);
 #pragma unroll
             for (int u = 0; u < VEC; ++u) {
-                const bool ok = ((al >> u) & 1u) != 0;
-                const float e = f[u];
-                float v;
                 if (TWO) {
-                    if (ST == 2) ovf |= pk_overflows_f16(e);
-                    v = stored<ST>(e) / zq[q];
-                } else {
-                    v = e / zq[q];
+                    if (ST == 2) ovf |= pk_overflows_f16(f[u]);
+                    f[u] = stored<ST>(f[u]);
                 }
-                f[u] = ok ? v : 0.f;
             }
+            quotients<VEC>(f, zq[q], rz[q]);
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) f[u] = ((al >> u) & 1u) != 0 ? f[u] : 0.f;
             U4 o;
             if (ST == 0) {
 #pragma unroll
@@ -724,6 +783,14 @@ __global__ void __launch_bounds__(64) softmax_stream_kernel(RowArgs a) {
                 }
             }
             *(U4*)((char*)a.out + ((row0 + row) * n + c0 + lc) * (ST == 0 ? 4 : 2)) = o;
+        }
+    }, [&](long long c0) {
+        // a chunk no row allows: zeros
+        if (c0 + lc >= n) return;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int row = q * RPI + lane / LPR;
+            if (row < nr) *(U4*)((char*)a.out + ((row0 + row) * n + c0 + lc) * (ST == 0 ? 4 : 2)) = U4{0u, 0u, 0u, 0u};
         }
     });
     if (ovf && a.flag) atomicOr(a.flag, 1u);
@@ -831,9 +898,12 @@ __global__ void __launch_bounds__(64) softmax_short_kernel(RowArgs a) {
         }
         __syncthreads();
     }
-    float zq[NQ];
+    float zq[NQ], rz[NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) zq[q] = __shfl(z, q * RPI + lane / LPR, 64);
+    for (int q = 0; q < NQ; ++q) {
+        zq[q] = __shfl(z, q * RPI + lane / LPR, 64);
+        rz[q] = 1.f / zq[q];
+    }
 
     // 3. the outputs, 16 bytes a lane
 #pragma unroll
@@ -846,17 +916,15 @@ __global__ void __launch_bounds__(64) softmax_short_kernel(RowArgs a) {
             float f[VEC];
 #pragma unroll
             for (int u = 0; u < VEC; ++u) {
-                const bool ok = ((al >> u) & 1u) != 0;
-                const float e = v[c][q][u];
-                float o;
+                f[u] = v[c][q][u];
                 if (TWO) {
-                    if (ST == 2) ovf |= pk_overflows_f16(e);
-                    o = stored<ST>(e) / zq[q];
-                } else {
-                    o = e / zq[q];
+                    if (ST == 2) ovf |= pk_overflows_f16(f[u]);
+                    f[u] = stored<ST>(f[u]);
                 }
-                f[u] = ok ? o : 0.f;
             }
+            quotients<VEC>(f, zq[q], rz[q]);
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) f[u] = ((al >> u) & 1u) != 0 ? f[u] : 0.f;
             U4 o;
             if (ST == 0) {
 #pragma unroll

@@ -47,6 +47,9 @@ __device__ unsigned long long narrow64(unsigned long long b, unsigned t, unsigne
     return sign | (code > inf ? inf : code);
 }
 
+__device__ const float kDivisors[16] = {1.f, 1.0000001f, 1.5f, 1.9999999f, 2.f, 3.1415927f, 7.f, 10.f, 100.25f, 1000.3f,
+                                         12345.678f, 65535.9f, 1048577.f, 8388607.5f, 16777215.f, 16777216.f};
+
 __device__ unsigned eval1(int fn, unsigned long long i) {
     const float x = pk_float((unsigned)i);
     switch (fn) {
@@ -58,6 +61,13 @@ __device__ unsigned eval1(int fn, unsigned long long i) {
         case 5: return pk_bits(pk_cosf(x));
         // expf through the softmax's fast path where it applies: expf's bits
         case 6: return pk_bits(pk_expf_le0_ok(x) ? pk_expf_le0(x) : pk_expf(x));
+        // x / z for a table of divisors z >= 1: the softmax's quotient
+        // (Markstein's step where it applies, else the division) and the
+        // correctly rounded division itself
+        case 7: case 8: {
+            const float z = kDivisors[(i >> 3) % 16];
+            return pk_bits(fn == 8 || !pk_div_by_ok(x, z) ? x / z : pk_div_by(x, z, 1.f / z));
+        }
         case 10: return pk_f32_to_bf16(x);
         case 11: return pk_f32_to_f16(x);
         case 12: return pk_f32_to_e8m15(x);
@@ -94,7 +104,7 @@ __global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long 
 }  // namespace
 
 hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
-    const int known[] = {0, 1, 2, 3, 4, 5, 6, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
+    const int known[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
     bool ok = false;
     for (int f : known) ok |= f == fn;
     if (!ok || hi < lo) return hipErrorInvalidValue;

@@ -41,3 +41,17 @@ def test_expf_fast_path_is_expf(golden):
         if format(d.value, "016x") != g["blocks"][i]:
             bad.append(i)
     assert not bad, f"blocks {bad[:8]} differ from the reference's expf"
+
+
+def test_softmax_quotient_is_the_division():
+    """the softmax's quotient x / z (Markstein's correction step with 1/z
+    where pk_div_by_ok says it is exact, the division elsewhere) equals the
+    correctly rounded f32 division over every f32 x, each against one of 16
+    divisors from 1 to 2^24 (in 2^32 / 2^28 blocks, digest against digest)"""
+    hip.init(0)
+    step = 1 << 28
+    for lo in range(0, 1 << 32, step):
+        a, b = ctypes.c_uint64(), ctypes.c_uint64()
+        hip.check(hip.lib().presk_hip_scalar_digest(7, lo, lo + step, ctypes.byref(a)))
+        hip.check(hip.lib().presk_hip_scalar_digest(8, lo, lo + step, ctypes.byref(b)))
+        assert a.value == b.value, hex(lo)
