@@ -123,7 +123,7 @@ struct GemmPlan : ClassPlan {
 
     const char* kind() const override { return "gemm"; }
     std::string order() const override {
-        std::string o = storage == kF32 ? "mfma-f32-k4" : "mfma-k32";
+        std::string o = storage == kF32 ? "mfma-f32-k4" : g.bm == 256 ? "mfma-k16" : "mfma-k32";
         if (g.splits > 1) o += "-split" + std::to_string(g.splits);
         return o;
     }
@@ -166,7 +166,7 @@ struct GemmPlan : ClassPlan {
                 a.C = (char*)a.C + m0 * a.sc_m * esz;
                 if (a.bias && a.bias_kind == 2) a.bias = (const char*)a.bias + m0 * a.N * esz;
                 a.M = count * rows_per_iter;
-                a.tiles_m = (int)((a.M + gemm_tile_m() - 1) / gemm_tile_m());
+                a.tiles_m = (int)((a.M + gemm_tile_m_of(a) - 1) / gemm_tile_m_of(a));
             }
         }
         // the clamped 16-byte loads need whole aligned vectors along the
@@ -200,6 +200,7 @@ int storage_of(Ty t) {
 }
 
 void plan_tiles(GemmArgs& g) {
+    g.bm = 128;
     g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
     // tile columns: 128, 96 or 64, whichever finishes first when the tiles
     // run in rounds of 512 (two workgroups per CU) and a tile takes time in
@@ -246,6 +247,23 @@ void plan_tiles(GemmArgs& g) {
             g.splits = (int)s;
             g.k_per_split = (nkb + s - 1) / s * bk;  // the longest split
         }
+    }
+    // 16-bit storage without a k-split, whole k-blocks and strides of whole
+    // 16-byte vectors: 256 x 128 tiles of 32x32x16 MFMAs loaded straight
+    // into LDS
+    auto vec_strides = [&](long long other, const long long* bs) {
+        if (other % 8) return false;
+        for (int d = 0; d < g.nbatch; ++d)
+            if (bs[d] % 8) return false;
+        return true;
+    };
+    const bool a_rows_vec = g.a_kcontig || g.M % 8 == 0, b_rows_vec = g.b_kcontig || g.N % 8 == 0;
+    if (g.storage != kF32 && g.splits == 1 && g.K % gemm_block_k(g.storage) == 0 && a_rows_vec && b_rows_vec &&
+        vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) && vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b)) {
+        g.bm = 256;
+        g.bn = 128;
+        g.tiles_m = (int)((g.M + 255) / 256);
+        g.tiles_n = (int)((g.N + 127) / 128);
     }
 }
 

@@ -7,12 +7,21 @@
 // through general strides, so NN (`dot`), NT (`dot_vjp_l`, QK^T), TN
 // (`dot_vjp_r`) and batched (`ein`) forms are one kernel.
 //
-// Order (declared, not the interpreter's index order): each 16x16 output tile
-// accumulates on MFMA in f32 -- v_mfma_f32_16x16x32_{bf16,f16} for 16-bit
-// storage (the product of two 16-bit values is exact in f32), and
-// v_mfma_f32_16x16x4_f32 for f32 storage -- over k-blocks of 64 (32 for f32)
-// in increasing k; when K is split across workgroups, the partial sums are
-// added in increasing split order by a second kernel (deterministic).
+// Order (declared, not the interpreter's index order): each output tile
+// accumulates on MFMA in f32 -- v_mfma_f32_16x16x32_{bf16,f16} (order
+// "mfma-k32") or, on the 256 x 128 tiles, v_mfma_f32_32x32x16_{bf16,f16}
+// ("mfma-k16") for 16-bit storage (the product of two 16-bit values is exact
+// in f32), and v_mfma_f32_16x16x4_f32 for f32 storage -- over k-blocks of 64
+// (32 for f32) in increasing k; when K is split across workgroups, the
+// partial sums are added in increasing split order by a second kernel
+// (deterministic).
+//
+// 16-bit storage, whole k-blocks and strides of whole 16-byte vectors (the
+// plan's choice when K is not split): 256 x 128 tiles, each wave 128 x 64 as
+// 4 x 2 MFMAs of 32x32x16, operands loaded straight into LDS three k-blocks
+// deep (D16Loader), the fragments of each 16-k step read while the previous
+// step's MFMAs run.  One workgroup a CU (144 KB of LDS); every other shape
+// takes the 128-row tiles below.
 //
 // Workgroup: 256 threads (4 waves as 2x2), tile (2*WM*16) x (2*WN*16), each
 // wave WM x WN MFMA tiles of 16x16.  Operands are staged through LDS,
@@ -29,6 +38,8 @@
 // tile (global_load_lds_dwordx4), the same products in the same order.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "devfmt.hpp"
 #include "gemm.hpp"
 
@@ -39,6 +50,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
 
@@ -228,6 +240,104 @@ __device__ __forceinline__ float frag_dl(const float* xs, int base, int kk, int 
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
+// 16-bit operand tiles (64 k) loaded straight into LDS, three stages deep, in
+// 16-byte chunks placed by an XOR swizzle (lane i of a wave's load fills slot
+// i of the wave's 1 KB segment; the swizzle picks which chunk each lane
+// fetches):
+//   k-contiguous, [row][8 chunks of 8 k]: chunk c of row r in slot
+//     8 r + (c ^ ((r ^ (r >> 3)) & 7))
+//   m/n-contiguous, [k][ROWS / 8 chunks of 8 rows]: chunk j of k-row r in slot
+//     (ROWS / 8) r + (j ^ (2 (r & 3) ^ 8 (r & 1)))
+// so that the 32x32x16 fragment reads below hit distinct banks in every
+// 16-lane (and 32-lane) phase: 16-byte reads of 16 consecutive rows, and
+// transposing 8-byte reads of 4 k-rows x 32 (64) bytes.  Rows past the
+// operand read its last row (or last whole vector); the launcher takes this
+// path only for whole k-blocks (K % 64 == 0) of aligned vectors.
+//
+// The loads (global_load_lds_dwordx4, saddr form: a wave-uniform base plus a
+// 32-bit lane offset, the wave's LDS segment in m0) are issued by inline
+// assembly: the compiler then tracks no LDS write for them and adds no
+// vmcnt(0) before the barrier or the transposing reads, which would drain the
+// blocks in flight; the kernel waits for them itself (wait_vm) before the
+// barrier that precedes every read of a stage.  The lane offsets are fixed
+// for the whole k-loop; a block moves the uniform base only.
+template <bool KCONTIG, int ROWS>
+struct D16Loader {
+    static constexpr int BK = 64;
+    static constexpr int CPR = KCONTIG ? 8 : ROWS / 8;    // chunks per LDS row
+    static constexpr int SLOTS = ROWS * BK / 8;           // chunks per tile
+    static constexpr int ROUNDS = SLOTS / NT;             // loads per thread
+    static constexpr int BYTES = SLOTS * 16;
+    static_assert(SLOTS % NT == 0, "whole rounds");
+    unsigned voff[ROUNDS];      // byte offsets of this thread's chunks from the origin
+    const char* origin;         // the operand's first k-block (uniform)
+    long long block_bytes;      // how far one k-block moves the origin (uniform)
+    unsigned lds0;              // this wave's segment of the stage-0 tile (uniform)
+
+    __device__ static __forceinline__ int swz(int r) { return KCONTIG ? ((r ^ (r >> 3)) & 7) : ((2 * (r & 3)) ^ (8 * (r & 1))); }
+    __device__ __forceinline__ void init(const unsigned short* p, int rows, long long rs, long long ks, int row0, int k0,
+                                         unsigned tile) {
+        const int t = threadIdx.x;
+        origin = (const char*)(p + (KCONTIG ? (long long)k0 : (long long)k0 * ks));
+        block_bytes = KCONTIG ? 2LL * BK : 2LL * BK * ks;
+#pragma unroll
+        for (int q = 0; q < ROUNDS; ++q) {
+            const int slot = q * NT + t;
+            const int r = slot / CPR, c = (slot % CPR) ^ swz(r);
+            long long e;
+            if (KCONTIG) {
+                int row = row0 + r;
+                row = row < rows ? row : rows - 1;
+                e = row * rs + 8 * c;
+            } else {
+                int row = row0 + 8 * c;
+                row = row + 8 <= rows ? row : rows - 8;
+                e = r * ks + row;
+            }
+            voff[q] = (unsigned)(2 * e);
+        }
+        lds0 = __builtin_amdgcn_readfirstlane(tile + (unsigned)(t & ~63) * 16u);
+    }
+    // k-block kb into the tile `stage` bytes past the stage-0 tile
+    __device__ __forceinline__ void issue(int kb, unsigned stage) const {
+        const char* const src = origin + kb * block_bytes;
+#pragma unroll
+        for (int q = 0; q < ROUNDS; ++q)
+            asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                         : : "v"(voff[q]), "s"(src), "s"(lds0 + stage + (unsigned)(q * NT * 16)) : "memory", "m0");
+    }
+    // the 32x32x16 fragment: lane holds k = kk + 8 (lane >> 5) .. + 8 of row
+    // base + (lane & 31) -- one 16-byte read from [row][k], or two
+    // transposing reads from [k][row] (16-lane group g takes the 16 rows from
+    // base + 16 (g & 1), k from kk + 8 (g >> 1))
+    __device__ static __forceinline__ u16x8 frag(const unsigned char* xs, int base, int kk, int lane) {
+        if constexpr (KCONTIG) {
+            const int r = base + (lane & 31), c = (kk >> 3) + (lane >> 5);
+            return *(const u16x8*)(xs + (r * 8 + (c ^ swz(r))) * 16);
+        } else {
+            const int L = lane & 15, g = lane >> 4;
+            const int r = kk + 8 * (g >> 1) + (L >> 2), col = base + 16 * (g & 1) + 4 * (L & 3);
+            const int off = r * ROWS * 2 + (((col >> 3) ^ swz(r)) << 4) + (col & 7) * 2;
+            typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+            // k-row r + 4 has r's swizzle
+            const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(xs + off));
+            const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(xs + off + 4 * ROWS * 2));
+            u16x8 f;
+            f[0] = (unsigned short)lo[0]; f[1] = (unsigned short)lo[1]; f[2] = (unsigned short)lo[2]; f[3] = (unsigned short)lo[3];
+            f[4] = (unsigned short)hi[0]; f[5] = (unsigned short)hi[1]; f[6] = (unsigned short)hi[2]; f[7] = (unsigned short)hi[3];
+            return f;
+        }
+    }
+};
+
+// wait until at most N of this thread's vector-memory operations are
+// outstanding (expcnt and lgkmcnt not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // One MFMA operand fragment: k = kk + (lane >> 4) * KPL .. + KPL of row
 // base + (lane & 15), from a tile laid out [row][k] (KC) or [k][row].
 template <int ST, bool KC, int LDX>
@@ -250,6 +360,36 @@ __device__ __forceinline__ typename St<ST>::Frag frag(const typename St<ST>::S* 
         f[4] = (unsigned short)hi[0]; f[5] = (unsigned short)hi[1]; f[6] = (unsigned short)hi[2]; f[7] = (unsigned short)hi[3];
         return f;
     }
+}
+
+// A 16-bit operand fragment of the 32x32x16 MFMA from a padded register-staged
+// tile: k = kk + 8 * (lane >> 5) .. + 8 of row base + (lane & 31), from
+// [row][k] (KC) by one 16-byte read, or from [k][row] by two transposing
+// reads a 16-lane group (group g takes the 16 rows from base + 16 * (g & 1),
+// k from kk + 8 * (g >> 1)).
+template <bool KC, int LDX>
+__device__ __forceinline__ u16x8 frag32(const unsigned short* xs, int base, int kk, int lane) {
+    if constexpr (KC) {
+        return *(const u16x8*)&xs[(base + (lane & 31)) * LDX + kk + (lane >> 5) * 8];
+    } else {
+        const int L = lane & 15;
+        const int r = kk + 8 * (lane >> 5) + (L >> 2), c = base + 16 * ((lane >> 4) & 1) + 4 * (L & 3);
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(xs + r * LDX + c));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(xs + (r + 4) * LDX + c));
+        u16x8 f;
+        f[0] = (unsigned short)lo[0]; f[1] = (unsigned short)lo[1]; f[2] = (unsigned short)lo[2]; f[3] = (unsigned short)lo[3];
+        f[4] = (unsigned short)hi[0]; f[5] = (unsigned short)hi[1]; f[6] = (unsigned short)hi[2]; f[7] = (unsigned short)hi[3];
+        return f;
+    }
+}
+
+template <int ST>
+__device__ __forceinline__ f32x16 mfma32(u16x8 a, u16x8 b, f32x16 acc) {
+    if constexpr (ST == kBF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
 }
 
 template <int ST>
@@ -318,13 +458,16 @@ __device__ __forceinline__ float load_bias(const void* p, long long off) {
     return pk_f16_to_f32(((const unsigned short*)p)[off]);
 }
 
-template <int ST, bool AK, bool BK_, int WM, int WN, bool SAFE, bool DL>
+template <int ST, bool AK, bool BK_, int WM, int WN, bool SAFE, bool DL, int MF>
 __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
-    static_assert(!DL || (ST == kF32 && !SAFE), "direct loads: f32 with whole vectors");
+    static_assert(!DL || !SAFE, "direct loads: whole vectors");
+    static_assert(MF == 16 || ST != kF32, "32x32 tiles: 16-bit storage");
+    constexpr bool D16 = DL && MF == 32;
     typedef typename St<ST>::S S;
     typedef typename St<ST>::Frag Frag;
-    constexpr int BK = St<ST>::BK, LD = BK + St<ST>::PAD, KSTEP = St<ST>::KSTEP, KPL = St<ST>::KPL;
-    constexpr int BM = 2 * WM * 16, BN = 2 * WN * 16;
+    typedef typename std::conditional<MF == 32, f32x16, f32x4>::type Acc;
+    constexpr int BK = St<ST>::BK, LD = BK + St<ST>::PAD, KSTEP = MF == 32 ? 16 : St<ST>::KSTEP, KPL = St<ST>::KPL;
+    constexpr int BM = 2 * WM * MF, BN = 2 * WN * MF;
     // LDS: the double-buffered operand tiles, reused by the epilogue for the
     // tile's f32 sums
     typedef Loader<ST, AK, BM> LA;
@@ -334,7 +477,10 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     constexpr int ASZ = DL ? DA::SIZE : LA::SIZE, BSZ = DL ? DB::SIZE : LB::SIZE;
     constexpr int LDA = AK ? LD : LA::LDR, LDB = BK_ ? LD : LB::LDR;
     constexpr int CLD = BN + 4;
-    constexpr int OPER = 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = BM * CLD * 4;
+    typedef D16Loader<AK, BM> QA;
+    typedef D16Loader<BK_, BN> QB;
+    constexpr int STAGE = QA::BYTES + QB::BYTES;
+    constexpr int OPER = D16 ? 3 * STAGE : 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = BM * CLD * 4;
     __shared__ __attribute__((aligned(16))) char smem[OPER > CTILE ? OPER : CTILE];
     S* const As0 = (S*)smem;
     S* const Bs0 = As0 + 2 * ASZ;
@@ -375,15 +521,93 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     const int sa_m = (int)g.sa_m, sa_k = (int)g.sa_k, sb_k = (int)g.sb_k, sb_n = (int)g.sb_n;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * (WM * 16), wn = (wave & 1) * (WN * 16);
-    f32x4 acc[WM][WN];
+    const int wm = (wave >> 1) * (WM * MF), wn = (wave & 1) * (WN * MF);
+    Acc acc[WM][WN];
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < WN; ++j) acc[i][j] = Acc{};
 
     const int nk = (kend - kbeg + BK - 1) / BK;
-    if constexpr (DL) {
+    if constexpr (D16) {
+        // Three stages: block kt + 2 streams into LDS while block kt is
+        // multiplied.  The fragments of each 16-k step are read while the
+        // previous step's MFMAs run; before the last step of a block, the
+        // next block's first fragments are read once this thread's loads of
+        // that block have landed (those of the block after may still be in
+        // flight) and a barrier has seen every thread's -- the barrier also
+        // retires every read of the stage the next loads overwrite.
+        constexpr int NL = QA::ROUNDS + QB::ROUNDS;   // loads a thread issues per block
+        QA qa;
+        QB qb;
+        unsigned char* const st0 = (unsigned char*)smem;
+        const unsigned lds = (unsigned)(size_t)(lds_void_t*)st0;
+        qa.init((const unsigned short*)A, M, sa_m, sa_k, (int)m0, kbeg, lds);
+        qb.init((const unsigned short*)B, N, sb_n, sb_k, (int)n0, kbeg, lds + QA::BYTES);
+        auto fetch = [&](int kb, int s) {
+            qa.issue(kb, (unsigned)(s * STAGE));
+            qb.issue(kb, (unsigned)(s * STAGE));
+        };
+        u16x8 a[WM], b[WN];
+        auto read = [&](const unsigned char* st, int kk) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i) a[i] = QA::frag(st, wm + i * 32, kk, lane);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) b[j] = QB::frag(st + QA::BYTES, wn + j * 32, kk, lane);
+        };
+        if (nk > 0) {
+            fetch(0, 0);
+            if (nk > 1) {
+                fetch(1, 1);
+                wait_vm<NL>();
+            } else {
+                wait_vm<0>();
+            }
+            __syncthreads();
+            read(st0, 0);
+        }
+        auto block = [&](int kt, auto stage) {
+            constexpr int S = decltype(stage)::value;
+            if (kt + 2 < nk) fetch(kt + 2, (S + 2) % 3);
+            const unsigned char* const st = st0 + S * STAGE;
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += KSTEP) {
+                u16x8 ca[WM], cb[WN];
+#pragma unroll
+                for (int i = 0; i < WM; ++i) ca[i] = a[i];
+#pragma unroll
+                for (int j = 0; j < WN; ++j) cb[j] = b[j];
+                if (kk + KSTEP < BK) {
+                    read(st, kk + KSTEP);
+                } else if (kt + 1 < nk) {
+                    if (kt + 2 < nk) wait_vm<NL>();
+                    else wait_vm<0>();
+                    __syncthreads();
+                    read(st0 + ((S + 1) % 3) * STAGE, 0);
+                }
+                // the reads stay ahead of this step's MFMAs (the scheduler
+                // would otherwise pair each read with the MFMA that uses it)
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j) acc[i][j] = mfma32<ST>(ca[i], cb[j], acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        // whole rounds of the three stages, then the last one or two blocks
+        // (straight-line rounds keep the accumulators in place)
+        int kt = 0;
+        for (; kt + 3 <= nk; kt += 3) {
+            block(kt, std::integral_constant<int, 0>{});
+            block(kt + 1, std::integral_constant<int, 1>{});
+            block(kt + 2, std::integral_constant<int, 2>{});
+        }
+        if (kt < nk) {
+            block(kt, std::integral_constant<int, 0>{});
+            if (kt + 1 < nk) block(kt + 1, std::integral_constant<int, 1>{});
+        }
+    } else if constexpr (DL && MF == 16) {
         // One k-block ahead: block kt+1 streams into one LDS buffer while
         // block kt is multiplied out of the other; a block ends with this
         // wave's loads complete, then a barrier for every wave's.
@@ -444,15 +668,27 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
             const S* bs = Bs0 + cur * BSZ;
 #pragma unroll
             for (int kk = 0; kk < BK; kk += KSTEP) {
-                Frag a[WM], b[WN];
+                if constexpr (MF == 32) {
+                    u16x8 a[WM], b[WN];
 #pragma unroll
-                for (int i = 0; i < WM; ++i) a[i] = frag<ST, AK, LDA>(as, wm + i * 16, kk, lane);
+                    for (int i = 0; i < WM; ++i) a[i] = frag32<AK, LDA>((const unsigned short*)as, wm + i * 32, kk, lane);
 #pragma unroll
-                for (int j = 0; j < WN; ++j) b[j] = frag<ST, BK_, LDB>(bs, wn + j * 16, kk, lane);
+                    for (int j = 0; j < WN; ++j) b[j] = frag32<BK_, LDB>((const unsigned short*)bs, wn + j * 32, kk, lane);
 #pragma unroll
-                for (int i = 0; i < WM; ++i)
+                    for (int i = 0; i < WM; ++i)
 #pragma unroll
-                    for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
+                        for (int j = 0; j < WN; ++j) acc[i][j] = mfma32<ST>(a[i], b[j], acc[i][j]);
+                } else {
+                    Frag a[WM], b[WN];
+#pragma unroll
+                    for (int i = 0; i < WM; ++i) a[i] = frag<ST, AK, LDA>(as, wm + i * 16, kk, lane);
+#pragma unroll
+                    for (int j = 0; j < WN; ++j) b[j] = frag<ST, BK_, LDB>(bs, wn + j * 16, kk, lane);
+#pragma unroll
+                    for (int i = 0; i < WM; ++i)
+#pragma unroll
+                        for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
+                }
             }
             if (kt + 1 < nk) {
                 la.store(As0 + (cur ^ 1) * ASZ);
@@ -467,12 +703,24 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     // 16 contiguous bytes of one output row.
     __syncthreads();
     float* const cs = (float*)smem;
+    if constexpr (MF == 32) {
+        // a 32x32 tile: lane holds column lane & 31, rows 8 * (r >> 2) +
+        // 4 * (lane >> 5) + (r & 3), r = 0 .. 15
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
+            for (int j = 0; j < WN; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) cs[(wm + i * 16 + (lane >> 4) * 4 + r) * CLD + wn + j * 16 + (lane & 15)] = acc[i][j][r];
+                for (int r = 0; r < 16; ++r)
+                    cs[(wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * CLD + wn + j * 32 + (lane & 31)] = acc[i][j][r];
+    } else {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) cs[(wm + i * 16 + (lane >> 4) * 4 + r) * CLD + wn + j * 16 + (lane & 15)] = acc[i][j][r];
+    }
     __syncthreads();
 
     constexpr int OV = 16 / (int)sizeof(S);  // output elements per 16-byte store
@@ -559,16 +807,16 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
 
-template <int ST, int WM, int WN, bool SAFE, bool DL = false>
+template <int ST, int WM, int WN, bool SAFE, bool DL = false, int MF = 16>
 hipError_t launch_shape(const GemmArgs& g, hipStream_t stream) {
     const long long items = (long long)g.tiles_m * g.tiles_n * g.batch * g.splits;
     if (items <= 0) return hipSuccess;
     if (items > 0x7fffffffLL) return hipErrorInvalidValue;
     dim3 grid((unsigned)items, 1, 1);
-    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
-    else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
-    else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
-    else gemm_kernel<ST, false, false, WM, WN, SAFE, DL><<<grid, NT, 0, stream>>>(g);
+    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
+    else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
+    else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
+    else gemm_kernel<ST, false, false, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
     return hipGetLastError();
 }
 
@@ -583,6 +831,19 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
         if (g.bn == 96) e = launch_shape<ST, 4, 3, false, ST == kF32>(g, stream);
         else if (g.bn == 64) e = launch_shape<ST, 4, 2, false, ST == kF32>(g, stream);
         else e = launch_shape<ST, 4, 4, false, ST == kF32>(g, stream);
+    } else if (ST != kF32 && g.bm == 256) {
+        // 256 x 128 tiles of 32x32x16 MFMAs (a wave 128 x 64), operands
+        // straight into LDS (the plan takes these tiles for whole k-blocks);
+        // operand pointers off 16 bytes: the same products from
+        // register-staged tiles, element-wise loads
+        if constexpr (ST != kF32) {
+            if (fast && g.K % St<ST>::BK == 0 && (g.splits <= 1 || g.k_per_split % St<ST>::BK == 0))
+                e = launch_shape<ST, 4, 2, false, true, 32>(g, stream);
+            else
+                e = launch_shape<ST, 4, 2, true, false, 32>(g, stream);
+        } else {
+            e = hipErrorInvalidValue;
+        }
     } else if (g.bn == 96) {
         e = fast ? launch_shape<ST, 4, 3, false>(g, stream) : launch_shape<ST, 4, 3, true>(g, stream);
     } else if (g.bn == 64) {
@@ -600,6 +861,7 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
 
 int gemm_block_k(int storage) { return storage == kF32 ? St<kF32>::BK : St<kBF16>::BK; }
 int gemm_tile_m() { return 128; }
+int gemm_tile_m_of(const GemmArgs& g) { return g.bm == 256 ? 256 : 128; }
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream) {
     switch (g.storage) {

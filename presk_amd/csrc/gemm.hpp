@@ -28,11 +28,13 @@ struct GemmArgs {
     int splits;
     long long k_per_split;
     int tiles_m, tiles_n;
+    int bm;                         // tile rows: 128, or 256 (16-bit storage, 32x32 MFMA tiles)
     int bn;                         // tile columns: 128, 96 or 64
 };
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream);
 int gemm_block_k(int storage);
 int gemm_tile_m();
+int gemm_tile_m_of(const GemmArgs& g);
 
 }  // namespace presk

@@ -68,6 +68,18 @@ def cases():
         w2 = O(A(("groups", 2), ("per", 3), ("hd", 32), ("model", 72)))
         out.append((f"ein_oproj-{dt}", L.ein([og, w2], [["batch", "seq", "groups", "per", "hd"], ["groups", "per", "hd", "model"]],
                                              ["batch", "seq", "model"], dt), None))
+    # 16-bit storage, whole k-blocks, aligned vectors: 256 x 128 tiles loaded
+    # straight into LDS in three stages -- each operand layout (k-contiguous or
+    # not), 1, 2, 5 and 6 k-blocks, rows past a tile, a transposed operand
+    # whose last vectors are clamped
+    for dt in ("bf16", "f16"):
+        out.append((f"d16-nn-{dt}", L.dot([O(A(("batch", 3), ("seq", 300), 320)), O(A(320, 200))], dt), None))
+        out.append((f"d16-nt-{dt}", L.dot_vjp_l([O(A(("batch", 2), ("seq", 130), 128)), O(A(264, 128))], dt), None))
+        out.append((f"d16-tn-{dt}", L.dot_vjp_r([O(A(("batch", 4), ("seq", 96), 104)), O(A(("batch", 4), ("seq", 96), 136))], dt), None))
+        out.append((f"d16-tt-{dt}", L.ein([O(A(("k", 64), ("m", 264))), O(A(("n", 72), ("k", 64)))], [["k", "m"], ["n", "k"]],
+                                          ["m", "n"], dt), None))
+        out.append((f"d16-bias-{dt}", L.dot([O(A(("batch", 520), 384)), O(A(384, 256)), O(A(256))], dt,
+                                            epilogue=(True, A(("batch", 520), 256))), None))
     # a K that is not a multiple of the k-block, M and N below one tile
     out.append(("dot-odd-bf16", L.dot([O(A(("batch", 5), 77)), O(A(77, 24))], "bf16"), None))
     return out
