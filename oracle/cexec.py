@@ -19,8 +19,9 @@ the operations `exec::run_guarded` performs (crates/presk-kernel/src/exec.rs:
   converted (exec.rs:688-689), a real read as an index is `as i64` (Rust's
   saturating cast);
 - `+ - * /` are single IEEE operations in the arithmetic type, never fused
-  (built with -ffp-contract=off); exp/log/tanh/erf are the fdlibm-method f32
-  functions of oracle/libm.c; sqrt and abs are IEEE;
+  (built with -ffp-contract=off); exp/log/tanh/erf/sin/cos are the
+  fdlibm-method functions of oracle/libm.c (f32, or the double ones in an f64
+  kernel, exec.rs:115-130); sqrt and abs are IEEE;
 - the vector form evaluates every lane of a vector expression, then assigns
   (exec.rs:730-756).
 
@@ -53,7 +54,7 @@ WIDTH_RANK = {"f64": 0, "f32": 1, "bf16": 2, "f16": 2, "e8m15": 2}
 
 class Refused(Exception):
     """A kernel the oracle does not restate (quantised weights, non-native
-    formats, f64 transcendentals)."""
+    formats)."""
 
 
 def _hexlit(x: float) -> str:
@@ -150,10 +151,8 @@ class _Printer:
                 return f"fabs{'f' if A == 'float' else ''}({a})"
             if f == "sqrt":
                 return f"sqrt{'f' if A == 'float' else ''}({a})"
-            if A == "double":
-                raise Refused("f64 transcendentals are not restated")
             if f in ("exp", "log", "tanh", "erf", "sin", "cos"):
-                return f"ok_{f}f({a})"
+                return f"ok_{f}{'f' if A == 'float' else ''}({a})"
             raise AssertionError(f)
         if tag == "select":
             return f"({self.boolx(e[1])} ? {self.real(e[2])} : {self.real(e[3])})"
@@ -325,6 +324,8 @@ PRELUDE = r"""
 #include "codes.h"
 float ok_expf(float); float ok_logf(float); float ok_tanhf(float); float ok_erff(float);
 float ok_sinf(float); float ok_cosf(float);
+double ok_exp(double); double ok_log(double); double ok_tanh(double); double ok_erf(double);
+double ok_sin(double); double ok_cos(double);
 /* Rust's `f as i64`: saturating, NaN to 0 */
 static inline int64_t rs_i64(double x) {
     if (x != x) return 0;

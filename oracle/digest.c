@@ -27,6 +27,12 @@
 #define F_ERF presk_erff
 #define F_SIN presk_sinf
 #define F_COS presk_cosf
+#define D_EXP presk_exp
+#define D_LOG presk_log
+#define D_TANH presk_tanh
+#define D_ERF presk_erf
+#define D_SIN presk_sin
+#define D_COS presk_cos
 static inline uint16_t C_BF16(float x) { return presk_f32_to_bf16(x); }
 static inline uint16_t C_F16(float x) { return presk_f32_to_f16(x); }
 static inline uint32_t C_E8(float x) { return presk_f32_to_e8m15_code(x); }
@@ -45,6 +51,18 @@ float ok_tanhf(float);
 float ok_erff(float);
 float ok_sinf(float);
 float ok_cosf(float);
+double ok_exp(double);
+double ok_log(double);
+double ok_tanh(double);
+double ok_erf(double);
+double ok_sin(double);
+double ok_cos(double);
+#define D_EXP ok_exp
+#define D_LOG ok_log
+#define D_TANH ok_tanh
+#define D_ERF ok_erf
+#define D_SIN ok_sin
+#define D_COS ok_cos
 #define F_SIN ok_sinf
 #define F_COS ok_cosf
 #define F_EXP ok_expf
@@ -88,10 +106,45 @@ uint64_t pd_sample_f64_bits(uint64_t i)
     return (r & (1ull << 63)) | (e << 52) | frac;
 }
 
+/* The argument sample of f64 function fn (40 + 0..5), sample i: one in
+ * eight any bit pattern (NaNs, infinities, subnormals, zeros), one in eight
+ * any exponent, the rest exponents in [-30, 12] (|x| from 1e-9 to 8192,
+ * where the reductions' branches lie), mantissa and sign uniform. */
+uint64_t pd_sample_f64_arg(int fn, uint64_t i)
+{
+    const uint64_t r = mix64(i * 0x9e3779b97f4a7c15ull + 0x2545f4914f6cdd1dull * (uint64_t)(fn + 1));
+    const uint64_t cls = i & 7;
+    if (cls == 0)
+        return r;
+    const uint64_t m = mix64(r);
+    const uint64_t e = cls == 1 ? m % 2047 : 1023 - 30 + m % 43;
+    return (r & (1ull << 63)) | (e << 52) | (r & ((1ull << 52) - 1));
+}
+
+static inline double d_of(uint64_t b) { double x; memcpy(&x, &b, 8); return x; }
+static inline uint64_t bd_of(double x) { uint64_t b; memcpy(&b, &x, 8); return b; }
+
+/* an f64 function's value at x */
+static inline double evald(int fn, double x, int *ok)
+{
+    *ok = 1;
+    switch (fn) {
+    case 40: return D_EXP(x);
+    case 41: return D_LOG(x);
+    case 42: return D_TANH(x);
+    case 43: return D_ERF(x);
+    case 44: return D_SIN(x);
+    case 45: return D_COS(x);
+    default: *ok = 0; return 0;
+    }
+}
+
 /* Function ids: 0 expf, 1 logf, 2 tanhf, 3 erff, 4 sinf, 5 cosf (every f32);
  * 10 f32->bf16, 11 f32->f16, 12 f32->e8m15, 32 f16 guard, 33 e8m15 guard
  * (every f32); 20 bf16->f32, 21 f16->f32 (every code of 16 bits),
- * 22 e8m15->f32 (every 24-bit code); 30 f64->f16, 31 f64->e8m15 (the sample). */
+ * 22 e8m15->f32 (every 24-bit code); 30 f64->f16, 31 f64->e8m15 (the sample);
+ * 40 exp, 41 log, 42 tanh, 43 erf, 44 sin, 45 cos of f64 (their argument
+ * sample; the result's 64 bits folded to 32 by the top half of mix64). */
 static inline uint32_t eval1(int fn, uint64_t i, int *ok)
 {
     *ok = 1;
@@ -112,6 +165,8 @@ static inline uint32_t eval1(int fn, uint64_t i, int *ok)
     case 31: { uint64_t b = pd_sample_f64_bits(i); double x; memcpy(&x, &b, 8); return D_E8(x); }
     case 32: return O_F16(f_of((uint32_t)i));
     case 33: return O_E8(f_of((uint32_t)i));
+    case 40: case 41: case 42: case 43: case 44: case 45:
+        return (uint32_t)(mix64(bd_of(evald(fn, d_of(pd_sample_f64_arg(fn, i)), ok))) >> 32);
     default: *ok = 0; return 0;
     }
 }
@@ -137,6 +192,18 @@ int pd_eval(int fn, const uint64_t *in, uint32_t *out, size_t n)
     for (size_t k = 0; k < n; k++) {
         int ok;
         out[k] = eval1(fn, in[k], &ok);
+        if (!ok)
+            return -1;
+    }
+    return 0;
+}
+
+/* An f64 function at given arguments, the results' bits. */
+int pd_eval_f64(int fn, const double *in, uint64_t *out, size_t n)
+{
+    for (size_t k = 0; k < n; k++) {
+        int ok;
+        out[k] = bd_of(evald(fn, in[k], &ok));
         if (!ok)
             return -1;
     }

@@ -77,6 +77,8 @@ def encode(x: np.ndarray, ty: str) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     if ty == "f32":
         return x.ravel()
+    if ty == "f64":
+        return x.astype(np.float64).ravel()
     b = x.view(np.uint32).astype(np.uint64).ravel()
     if ty == "bf16":
         return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)

@@ -166,12 +166,14 @@ struct Printer {
                     case Un::Neg: return "(-" + a + ")";
                     case Un::Abs: return std::string(f ? "__builtin_fabsf(" : "__builtin_fabs(") + a + ")";
                     case Un::Sqrt: return std::string(f ? "__builtin_sqrtf(" : "__builtin_sqrt(") + a + ")";
-                    case Un::Exp: if (f) return "pk_expf(" + a + ")"; break;
-                    case Un::Log: if (f) return "pk_logf(" + a + ")"; break;
-                    case Un::Tanh: if (f) return "pk_tanhf(" + a + ")"; break;
-                    case Un::Erf: if (f) return "pk_erff(" + a + ")"; break;
-                    case Un::Sin: if (f) return "pk_sinf(" + a + ")"; break;
-                    case Un::Cos: if (f) return "pk_cosf(" + a + ")"; break;
+                    // f32 arithmetic: the f32 functions; f64: the double ones
+                    // (exec.rs:115-130, musl's exp/log/tanh/erf/sin/cos)
+                    case Un::Exp: return std::string(f ? "pk_expf(" : "pk_exp(") + a + ")";
+                    case Un::Log: return std::string(f ? "pk_logf(" : "pk_log(") + a + ")";
+                    case Un::Tanh: return std::string(f ? "pk_tanhf(" : "pk_tanh(") + a + ")";
+                    case Un::Erf: return std::string(f ? "pk_erff(" : "pk_erf(") + a + ")";
+                    case Un::Sin: return std::string(f ? "pk_sinf(" : "pk_sin(") + a + ")";
+                    case Un::Cos: return std::string(f ? "pk_cosf(" : "pk_cos(") + a + ")";
                 }
                 err = "the function " + show_expr(*e) + " is not on this executor yet";
                 return "0";

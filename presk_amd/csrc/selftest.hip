@@ -25,6 +25,27 @@ __device__ __forceinline__ unsigned long long sample_f64_bits(unsigned long long
     return (r & (1ull << 63)) | (e << 52) | frac;
 }
 
+// the argument sample of f64 function fn (oracle/digest.c pd_sample_f64_arg)
+__device__ __forceinline__ unsigned long long sample_f64_arg(int fn, unsigned long long i) {
+    const unsigned long long r = mix64(i * 0x9e3779b97f4a7c15ull + 0x2545f4914f6cdd1dull * (unsigned long long)(fn + 1));
+    const unsigned long long cls = i & 7;
+    if (cls == 0) return r;
+    const unsigned long long m = mix64(r);
+    const unsigned long long e = cls == 1 ? m % 2047 : 1023 - 30 + m % 43;
+    return (r & (1ull << 63)) | (e << 52) | (r & ((1ull << 52) - 1));
+}
+
+__device__ double eval_f64(int fn, double x) {
+    switch (fn) {
+        case 40: return pk_exp(x);
+        case 41: return pk_log(x);
+        case 42: return pk_tanh(x);
+        case 43: return pk_erf(x);
+        case 44: return pk_sin(x);
+        default: return pk_cos(x);
+    }
+}
+
 // A double's narrowing as a native kernel performs it: the value is an f32
 // when a kernel stores it, so these go through the f32 of the double only
 // when it is exact; otherwise the f64 path of codes.rs:29-56, written here
@@ -78,6 +99,9 @@ __device__ unsigned eval1(int fn, unsigned long long i) {
         case 31: return (unsigned)narrow64(sample_f64_bits(i), 15, 8);
         case 32: return pk_overflows_f16(x) ? 1u : 0u;
         case 33: return pk_overflows_e8m15(x) ? 1u : 0u;
+        // f64 functions over their argument sample, the result folded to 32 bits
+        case 40: case 41: case 42: case 43: case 44: case 45:
+            return (unsigned)(mix64(pk_bits64(eval_f64(fn, pk_double(sample_f64_arg(fn, i))))) >> 32);
         default: return 0;
     }
 }
@@ -104,7 +128,7 @@ __global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long 
 }  // namespace
 
 hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
-    const int known[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33};
+    const int known[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33, 40, 41, 42, 43, 44, 45};
     bool ok = false;
     for (int f : known) ok |= f == fn;
     if (!ok || hi < lo) return hipErrorInvalidValue;

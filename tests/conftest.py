@@ -26,6 +26,8 @@ def oracle_lib():
     lib.pd_digest.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64]
     lib.pd_eval.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32), ctypes.c_size_t]
     lib.pd_eval.restype = ctypes.c_int
+    lib.pd_eval_f64.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.pd_eval_f64.restype = ctypes.c_int
     return lib
 
 

@@ -6,7 +6,9 @@ crates/presk-export-c/c/presk_rt.h and presk_libm.c.  The digests are data:
 per function, the order-free digest (oracle/digest.c) of each of its 256
 blocks of inputs (every f32 for the f32 functions and conversions, every code
 for the widenings, a fixed sample for the narrowings from f64), plus a few
-hundred sample input/output pairs per function for readable failures.
+hundred sample input/output pairs per function for readable failures; for
+the f64 functions, 16 blocks of their argument sample and their values at the
+special arguments of tests/golden/spec.py.
 
     python tests/golden/make_golden.py [NAME ...]
 
@@ -16,6 +18,8 @@ import ctypes
 import json
 import os
 import sys
+
+import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
@@ -45,6 +49,19 @@ def main():
         arr_out = (ctypes.c_uint32 * len(ins))()
         assert lib.pd_eval(fid, arr_in, arr_out, len(ins)) == 0
         out["functions"][name] = {"id": fid, "domain": domain, "blocks": digs, "samples": [[i, o] for i, o in zip(ins, arr_out)]}
+        print(name, digs[0], flush=True)
+    lib.pd_eval_f64.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    out.setdefault("functions_f64", {})
+    for name, fid in spec.F64.items():
+        if only and name not in only:
+            continue
+        digs = [format(lib.pd_digest(fid, lo, hi), "016x") for lo, hi in spec.f64_blocks()]
+        xs = np.array(spec.f64_specials(), np.float64)
+        ys = np.zeros(len(xs), np.uint64)
+        assert lib.pd_eval_f64(fid, xs.ctypes.data, ys.ctypes.data, len(xs)) == 0
+        out["functions_f64"][name] = {"id": fid, "domain": spec.F64_DOMAIN, "blocks": digs,
+                                      "specials": [[format(int(x), "016x"), format(int(y), "016x")]
+                                                   for x, y in zip(xs.view(np.uint64), ys)]}
         print(name, digs[0], flush=True)
     with open(path, "w") as f:
         json.dump(out, f, indent=0)

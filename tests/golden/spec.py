@@ -44,3 +44,32 @@ def sample_inputs(domain, n=512):
         k += 1
         ins.append((k * 0x9E3779B97F4A7C15 >> 17) % domain)
     return ins[:n]
+
+
+# f64 functions (the interpreter's f64 arm): name -> function id of
+# oracle/digest.c and the device self-test, each over its argument sample
+# (pd_sample_f64_arg) of F64_DOMAIN inputs in 16 blocks
+F64 = {"exp": 40, "log": 41, "tanh": 42, "erf": 43, "sin": 44, "cos": 45}
+F64_DOMAIN = 1 << 24
+
+
+def f64_blocks():
+    step = F64_DOMAIN // 16
+    return [(i * step, (i + 1) * step) for i in range(16)]
+
+
+def f64_specials():
+    """Arguments at the f64 functions' branch points, overflow and underflow
+    thresholds, reduction boundaries and near multiples of pi/2, their
+    negatives and next doubles up."""
+    import math
+    import numpy as np
+    base = [0.0, 1.0, 5e-324, 1e-320, 2.2250738585072014e-308, 1e-300, 2.0 ** -54, 2.0 ** -28, 3.0e-10, 0.25541281188299536,
+            0.5493061443340549, 0.84375, 1.25, 1 / 0.35, 6.0, 20.0, 28.0, 0.5 * math.log(2), 1.5 * math.log(2),
+            56 * math.log(2), 708.3964185322641, 709.782712893383973096, 709.7827128933841, 745.1332191019411,
+            745.1332191019412, 0.7853981633974483, math.pi / 2, math.pi, 3 * math.pi / 2, 2 * math.pi, 5 * math.pi / 4,
+            9 * math.pi / 4, 2 ** 20 * math.pi / 2, 1e22, 1e300, 2.0 ** 1023, 1.7976931348623157e308, math.inf, math.nan]
+    out = base + [-x for x in base]
+    with np.errstate(over="ignore"):
+        out += [float(np.nextafter(x, math.inf)) for x in base if math.isfinite(x)]
+    return out

@@ -1,6 +1,7 @@
 """The course-GPT training step (presk_amd/gpt.py) end to end on the device,
 at the reference's TINY constants: in EXACT mode every buffer of the step
-(loss, gradients, every intermediate) equals the oracle's byte for byte; in
+(loss, gradients, every intermediate) equals the oracle's byte for byte, in
+f32, bf16 and f64 (the f64 arm's exp/log/tanh of the double functions); in
 FAST mode the loss and gradients stay within the reassociation band of the
 MFMA contractions."""
 import numpy as np
@@ -26,14 +27,14 @@ def device_run(p, host):
 def oracle_tiny():
     s = gpt.TINY
     out = {}
-    for dt in ("f32", "bf16"):
+    for dt in ("f32", "bf16", "f64"):
         p, b, names = gpt.build(s, dt, train=True, mode=hip.EXACT)
         host = gpt.host_inputs(s)
         out[dt] = (cpu_program.run(p, host), names)
     return out
 
 
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f64"])
 def test_tiny_gpt_step_exact_bits(oracle_tiny, dt):
     s = gpt.TINY
     p, b, names = gpt.build(s, dt, train=True, mode=hip.EXACT)

@@ -1,8 +1,9 @@
 """The device's conversions and transcendentals over their whole domains:
 every f32 input of expf/logf/tanhf/erff and the narrowings, every code of the
-widenings, the f64 sample of the narrowings from f64.  Each block's digest
-must equal the reference's (tests/golden/digests.json, made from the
-reference's compiled presk_rt.h/presk_libm.c)."""
+widenings, the f64 sample of the narrowings from f64, and the f64 functions
+over their argument sample of 2^24.  Each block's digest must equal the
+reference's (tests/golden/digests.json, made from the reference's compiled
+presk_rt.h/presk_libm.c)."""
 import ctypes
 
 import pytest
@@ -55,3 +56,17 @@ def test_softmax_quotient_is_the_division():
         hip.check(hip.lib().presk_hip_scalar_digest(7, lo, lo + step, ctypes.byref(a)))
         hip.check(hip.lib().presk_hip_scalar_digest(8, lo, lo + step, ctypes.byref(b)))
         assert a.value == b.value, hex(lo)
+
+
+@pytest.mark.parametrize("name", list(spec.F64))
+def test_device_f64_function_sample(name, golden):
+    hip.init(0)
+    g = golden["functions_f64"][name]
+    bad = []
+    for i, (lo, hi) in enumerate(spec.f64_blocks()):
+        d = ctypes.c_uint64()
+        hip.check(hip.lib().presk_hip_scalar_digest(g["id"], lo, hi, ctypes.byref(d)))
+        if format(d.value, "016x") != g["blocks"][i]:
+            bad.append(i)
+    print(f"[scalar] {name} (f64): {len(bad)} of 16 blocks differ", flush=True)
+    assert not bad, f"{name}: blocks {bad} differ from the reference"
