@@ -117,6 +117,8 @@ struct GemmPlan : ClassPlan {
     // (the first batch axis), rows_per_iter rows of M, or cols_per_iter
     // columns of N (an `ein` whose first output axis is J)
     bool split_on_batch = false;
+    bool e8 = false;               // e8m15 storage: f32 products of the exact widenings
+    long long numel_in[2] = {0, 0}, numel_out = 0;
     bool swapped = false;          // operand 1 is A (an `ein` whose operand 1 carries I)
     long long rows_per_iter = 0;
     long long cols_per_iter = 0;
@@ -127,9 +129,14 @@ struct GemmPlan : ClassPlan {
         if (g.splits > 1) o += "-split" + std::to_string(g.splits);
         return o;
     }
-    // split-K partials, [splits][M][N] in f32
+    // e8m15: the operands' and the output's f32 copies, each 256-byte
+    // aligned; then the split-K partials, [splits][M][N] in f32
+    static size_t up256(size_t n) { return (n + 255) / 256 * 256; }
+    size_t e8_bytes() const {
+        return e8 ? up256(4 * (size_t)numel_in[0]) + up256(4 * (size_t)numel_in[1]) + up256(4 * (size_t)numel_out) : 0;
+    }
     size_t workspace_bytes() const override {
-        return g.splits > 1 ? (size_t)g.splits * (size_t)g.M * (size_t)g.N * sizeof(float) : 0;
+        return e8_bytes() + (g.splits > 1 ? (size_t)g.splits * (size_t)g.M * (size_t)g.N * sizeof(float) : 0);
     }
 
     hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const override {
@@ -142,32 +149,58 @@ struct GemmPlan : ClassPlan {
         a.bias = epilogue ? bufs[2] : nullptr;
         a.C = bufs[n_in];
         a.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
+        // e8m15: the kernel multiplies exact f32 widenings of the operands
+        // into an f32 copy of the output, which is narrowed afterwards
+        unsigned char* e8_out = nullptr;
+        const unsigned char* e8_bias = nullptr;
+        if (e8) {
+            if (!work) return hipErrorInvalidValue;
+            float* const w0 = (float*)work;
+            float* const w1 = (float*)((char*)work + up256(4 * (size_t)numel_in[0]));
+            float* const wc = (float*)((char*)w1 + up256(4 * (size_t)numel_in[1]));
+            hipError_t e = gemm_e8_widen(bufs[0], w0, numel_in[0], stream);
+            if (e == hipSuccess) e = gemm_e8_widen(bufs[1], w1, numel_in[1], stream);
+            if (e != hipSuccess) return e;
+            a.A = swapped ? w1 : w0;
+            a.B = swapped ? w0 : w1;
+            e8_out = (unsigned char*)a.C;
+            e8_bias = (const unsigned char*)a.bias;
+            a.C = wc;
+            a.bias = nullptr;
+            work = (char*)work + e8_bytes();
+        }
         const int esz = storage == kF32 ? 4 : 2;
         // a partial range: the same tiles, k-blocks and split of K as the
         // whole call, over fewer batch entries, rows or columns -- each
         // element is summed by the same steps, so its bits do not change
         if (count > 0 && count < split) {
+            // element offsets of the range's first output and bias elements
+            long long c_off = 0, bias_off = 0;
             if (split_on_batch) {
                 a.A = (const char*)a.A + first * a.sa_b[0] * esz;
                 a.B = (const char*)a.B + first * a.sb_b[0] * esz;
-                a.C = (char*)a.C + first * a.sc_b[0] * esz;
+                c_off = first * a.sc_b[0];
                 a.batch = a.batch / a.bdim[0] * count;
                 a.bdim[0] = count;
             } else if (cols_per_iter > 0) {
                 const long long n0 = first * cols_per_iter;
                 a.B = (const char*)a.B + n0 * a.sb_n * esz;
-                a.C = (char*)a.C + n0 * esz;
-                if (a.bias && a.bias_kind == 1) a.bias = (const char*)a.bias + n0 * esz;
+                c_off = n0;
+                if (a.bias_kind == 1) bias_off = n0;
                 a.N = count * cols_per_iter;
                 a.tiles_n = (int)((a.N + a.bn - 1) / a.bn);
             } else {
                 const long long m0 = first * rows_per_iter;
                 a.A = (const char*)a.A + m0 * a.sa_m * esz;
-                a.C = (char*)a.C + m0 * a.sc_m * esz;
-                if (a.bias && a.bias_kind == 2) a.bias = (const char*)a.bias + m0 * a.N * esz;
+                c_off = m0 * a.sc_m;
+                if (a.bias_kind == 2) bias_off = m0 * a.N;
                 a.M = count * rows_per_iter;
                 a.tiles_m = (int)((a.M + gemm_tile_m_of(a) - 1) / gemm_tile_m_of(a));
             }
+            a.C = (char*)a.C + c_off * esz;
+            if (a.bias) a.bias = (const char*)a.bias + bias_off * esz;
+            if (e8_out) e8_out += 3 * c_off;
+            if (e8_bias) e8_bias += 3 * bias_off;
         }
         // the clamped 16-byte loads need whole aligned vectors along the
         // loaded axis: k when it is contiguous, else the rows
@@ -186,7 +219,13 @@ struct GemmPlan : ClassPlan {
             if (!work) return hipErrorInvalidValue;
             a.work = (float*)work;
         }
-        return gemm_launch(a, stream);
+        if (!e8) return gemm_launch(a, stream);
+        unsigned* const flag = a.flag;
+        a.flag = nullptr;
+        hipError_t e = gemm_launch(a, stream);
+        if (e != hipSuccess) return e;
+        a.flag = flag;
+        return gemm_e8_narrow(a, e8_out, e8_bias, stream);
     }
 };
 
@@ -273,7 +312,9 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     const bool is_l = n == "dot_vjp_l", is_r = n == "dot_vjp_r";
     const bool is_ein = n.compare(0, 4, "ein[") == 0;
     if (!(is_dot || is_l || is_r || is_ein)) return nullptr;
-    const int st = storage_of(k.dtype);
+    // e8m15 storage runs as f32 on the exact widenings of its codes
+    const bool e8 = k.dtype == Ty::E8M15;
+    const int st = e8 ? kF32 : storage_of(k.dtype);
     if (st < 0 || k.output.ty != k.dtype) return nullptr;
     for (auto& b : k.inputs)
         if (b.ty != k.dtype) return nullptr;       // indices or widened parameters: generic
@@ -281,6 +322,10 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     if ((int)k.inputs.size() != (epi ? 3 : 2)) return nullptr;
     const BufSpec &x = k.inputs[0], &w = k.inputs[1], &o = k.output;
     auto p = std::make_unique<GemmPlan>();
+    p->e8 = e8;
+    p->numel_in[0] = x.numel();
+    p->numel_in[1] = w.numel();
+    p->numel_out = o.numel();
     GemmArgs& g = p->g;
     g.storage = st;
     g.batch = 1;

@@ -857,7 +857,45 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     return hipGetLastError();
 }
 
+__global__ void __launch_bounds__(256) e8_widen_kernel(const unsigned char* __restrict__ src, float* __restrict__ dst,
+                                                       long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = pk_e8m15_to_f32(pk_ld24(src, i));
+}
+
+__global__ void __launch_bounds__(256) e8_narrow_kernel(GemmArgs g, unsigned char* __restrict__ out,
+                                                        const unsigned char* __restrict__ bias) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= g.batch * g.M * g.N) return;
+    const long long n = idx % g.N, m = (idx / g.N) % g.M, b = idx / (g.N * g.M);
+    const long long off = batch_offset(g, b, g.sc_b) + m * g.sc_m + n;
+    const float sum = ((const float*)g.C)[off];
+    bool ovf = pk_overflows_e8m15(sum);
+    unsigned h = pk_f32_to_e8m15(sum);
+    if (bias) {
+        const long long bo = g.bias_kind == 1 ? n : g.bias_kind == 2 ? m * g.N + n : 0;
+        const float v = pk_e8m15_to_f32(h) + pk_e8m15_to_f32(pk_ld24(bias, bo));
+        ovf |= pk_overflows_e8m15(v);
+        h = pk_f32_to_e8m15(v);
+    }
+    pk_st24(out, off, h);
+    if (ovf && g.flag) atomicOr(g.flag, 1u);
+}
+
 }  // namespace
+
+hipError_t gemm_e8_widen(const void* src, float* dst, long long n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    e8_widen_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>((const unsigned char*)src, dst, n);
+    return hipGetLastError();
+}
+
+hipError_t gemm_e8_narrow(const GemmArgs& g, void* out, const void* bias, hipStream_t stream) {
+    const long long n = g.batch * g.M * g.N;
+    if (n <= 0) return hipSuccess;
+    e8_narrow_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(g, (unsigned char*)out, (const unsigned char*)bias);
+    return hipGetLastError();
+}
 
 int gemm_block_k(int storage) { return storage == kF32 ? St<kF32>::BK : St<kBF16>::BK; }
 int gemm_tile_m() { return 128; }

@@ -33,6 +33,14 @@ struct GemmArgs {
 };
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream);
+
+// e8m15 contractions (the f32 kernel on exact widenings): an e8m15 code is
+// the top 24 bits of its f32, so the n codes at src widen to dst exactly
+hipError_t gemm_e8_widen(const void* src, float* dst, long long n, hipStream_t stream);
+// the e8m15 output of every element g's M, N and batch cover (C's layout):
+// the f32 sum at g.C rounded (overflow guard at g.flag), then, with a bias,
+// read back, the bias added in f32 and rounded again (lower.rs:1053-1060)
+hipError_t gemm_e8_narrow(const GemmArgs& g, void* out, const void* bias, hipStream_t stream);
 int gemm_block_k(int storage);
 int gemm_tile_m();
 int gemm_tile_m_of(const GemmArgs& g);

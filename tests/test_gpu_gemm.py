@@ -20,7 +20,7 @@ from tests import fmt
 pytestmark = pytest.mark.gpu
 A, O = L.ax, L.Operand
 
-ULP = {"f32": 2.0 ** -23, "bf16": 2.0 ** -7, "f16": 2.0 ** -10}
+ULP = {"f32": 2.0 ** -23, "bf16": 2.0 ** -7, "f16": 2.0 ** -10, "e8m15": 2.0 ** -15}
 
 
 def cases():
@@ -80,6 +80,19 @@ def cases():
                                           ["m", "n"], dt), None))
         out.append((f"d16-bias-{dt}", L.dot([O(A(("batch", 520), 384)), O(A(384, 256)), O(A(256))], dt,
                                             epilogue=(True, A(("batch", 520), 256))), None))
+    # e8m15: the codes widened exactly to f32, the f32 kernel, the sums
+    # narrowed (with the bias added after the first rounding)
+    x, w = O(A(("batch", 3), ("seq", 200), 96)), O(A(96, 136))
+    d = L.dot([x, w], "e8m15")
+    out.append(("dot-e8m15", d, None))
+    out.append(("dot+add-e8m15", L.dot([x, w, O(A(136))], "e8m15", epilogue=(True, d.out_axes)), None))
+    out.append(("dot_vjp_l-e8m15", L.dot_vjp_l([O(A(("batch", 2), ("seq", 130), 200)), O(A(72, 200))], "e8m15"), None))
+    out.append(("dot_vjp_r-split-e8m15", L.dot_vjp_r([O(A(("batch", 4), ("seq", 600), 96)),
+                                                       O(A(("batch", 4), ("seq", 600), 80))], "e8m15"), None))
+    q = O(A(("batch", 2), ("heads", 3), ("seq", 40), ("hd", 64)))
+    kk = O(A(("batch", 2), ("heads", 3), ("seq2", 40), ("hd", 64)))
+    out.append(("ein_qk-e8m15", L.ein([q, kk], [["batch", "heads", "seq", "hd"], ["batch", "heads", "seq2", "hd"]],
+                                      ["batch", "heads", "seq", "seq2"], "e8m15"), None))
     # a K that is not a multiple of the k-block, M and N below one tile
     out.append(("dot-odd-bf16", L.dot([O(A(("batch", 5), 77)), O(A(77, 24))], "bf16"), None))
     return out

@@ -4,7 +4,8 @@ The native backend divides the iterations [0, n) of a nest's split loop
 among its workers, each calling the kernel on [lo, hi), and its tests hold
 that the result does not change by a bit (crates/presk-cranelift/src/
 lib.rs:1656-1691, crates/presk-cranelift/tests/native.rs:331).  Here every
-kernel class -- MFMA contractions (row, batch and split-K ranges), the row
+kernel class -- MFMA contractions (row, batch and split-K ranges; e8m15's
+widen-multiply-narrow form too), the row
 class, the column and scatter classes (whose nests have no split loop), and
 the generic printer -- runs whole and then in 1, 2, 3 and 7 pieces into an
 output poisoned with 0xff; the bytes must be equal."""
@@ -54,6 +55,14 @@ def cases():
         out.append((f"embed_vjp-{dt}", L.embed_vjp([O(A(("vocab", 65), ("model", 96))), ids, xs], dt), hip.EXACT, "scatter"))
         out.append((f"gelu-{dt}", L.unary("gelu", [xs], dt), hip.EXACT, "generic"))
         out.append((f"dot_exact-{dt}", d, hip.EXACT, "generic"))
+    # e8m15 contractions (the f32 kernel on widened copies, then narrowed):
+    # row, bias and split-K ranges
+    x, w = O(A(("batch", 6), ("seq", 40), 96)), O(A(96, 136))
+    d = L.dot([x, w], "e8m15")
+    out.append(("dot-e8m15", d, hip.FAST, "gemm"))
+    out.append(("dot+add-e8m15", L.dot([x, w, O(A(136))], "e8m15", epilogue=(True, d.out_axes)), hip.FAST, "gemm"))
+    out.append(("dot_vjp_r-split-e8m15", L.dot_vjp_r([O(A(("batch", 4), ("seq", 600), 96)),
+                                                       O(A(("batch", 4), ("seq", 600), 80))], "e8m15"), hip.FAST, "gemm"))
     return out
 
 
