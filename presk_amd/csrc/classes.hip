@@ -287,9 +287,12 @@ void plan_tiles(GemmArgs& g) {
             g.k_per_split = (nkb + s - 1) / s * bk;  // the longest split
         }
     }
-    // 16-bit storage without a k-split, whole k-blocks and strides of whole
-    // 16-byte vectors: 256 x 128 tiles of 32x32x16 MFMAs loaded straight
-    // into LDS
+    // 16-bit storage without a k-split, whole k-blocks, K of 3072 or more
+    // and strides of whole 16-byte vectors: 256 x 128 tiles of 32x32x16
+    // MFMAs loaded straight into LDS (measured at the Llama, MLP and course
+    // shapes: 10-25 % faster from K 3072 up -- 4096 x 2048 x 4096 80 against
+    // 105 us -- but slower at K 128-2048, where the 128-row tiles' two
+    // workgroups a CU hide their prologue and epilogue)
     auto vec_strides = [&](long long other, const long long* bs) {
         if (other % 8) return false;
         for (int d = 0; d < g.nbatch; ++d)
@@ -297,7 +300,7 @@ void plan_tiles(GemmArgs& g) {
         return true;
     };
     const bool a_rows_vec = g.a_kcontig || g.M % 8 == 0, b_rows_vec = g.b_kcontig || g.N % 8 == 0;
-    if (g.storage != kF32 && g.splits == 1 && g.K % gemm_block_k(g.storage) == 0 && a_rows_vec && b_rows_vec &&
+    if (g.storage != kF32 && g.splits == 1 && g.K >= 3072 && g.K % gemm_block_k(g.storage) == 0 && a_rows_vec && b_rows_vec &&
         vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) && vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b)) {
         g.bm = 256;
         g.bn = 128;

@@ -68,10 +68,9 @@ def cases():
         w2 = O(A(("groups", 2), ("per", 3), ("hd", 32), ("model", 72)))
         out.append((f"ein_oproj-{dt}", L.ein([og, w2], [["batch", "seq", "groups", "per", "hd"], ["groups", "per", "hd", "model"]],
                                              ["batch", "seq", "model"], dt), None))
-    # 16-bit storage, whole k-blocks, aligned vectors: 256 x 128 tiles loaded
-    # straight into LDS in three stages -- each operand layout (k-contiguous or
-    # not), 1, 2, 5 and 6 k-blocks, rows past a tile, a transposed operand
-    # whose last vectors are clamped
+    # 16-bit storage, whole k-blocks, aligned vectors below K 3072: the
+    # 128-row tiles in each operand layout (the 256-row tiles at K >= 3072
+    # are test_d16_tiles_within_band's)
     for dt in ("bf16", "f16"):
         out.append((f"d16-nn-{dt}", L.dot([O(A(("batch", 3), ("seq", 300), 320)), O(A(320, 200))], dt), None))
         out.append((f"d16-nt-{dt}", L.dot_vjp_l([O(A(("batch", 2), ("seq", 130), 128)), O(A(264, 128))], dt), None))
@@ -141,3 +140,49 @@ def test_fast_contraction_within_band(ex, case):
     assert np.all(np.isfinite(got)), f"{name}: unwritten or non-finite outputs"
     assert np.all(err <= bound), f"{name} [{c.order}]: {np.count_nonzero(err > bound)} elements outside the band"
     assert np.median(err / bound) < 1 / 64, f"{name}: median error {np.median(err / bound):.3g} of the band"
+
+
+# K >= 3072, whole k-blocks, aligned vectors, enough tiles for no k-split:
+# 256 x 128 tiles of 32x32x16 MFMAs loaded straight into LDS three k-blocks
+# deep.  Each operand layout (k-contiguous or not), 48, 49 and 50 k-blocks
+# (every remainder of the three-stage rounds), rows past a tile, the bias.
+# Against the f64 product of the same rounded operands (numpy), within
+# gamma_K S plus the storage type's unit of the sum and the result.
+D16 = {
+    "nn": (lambda dt: L.dot([O(A(("batch", 1100), 3136)), O(A(3136, 4104))], dt), lambda a, b: a @ b),
+    "nt": (lambda dt: L.dot_vjp_l([O(A(("batch", 2056), 3200)), O(A(2048, 3200))], dt), lambda a, b: a @ b.T),
+    "tn": (lambda dt: L.dot_vjp_r([O(A(("batch", 3072), 2048)), O(A(("batch", 3072), 2056))], dt), lambda a, b: a.T @ b),
+    "tt": (lambda dt: L.ein([O(A(("k", 3072), ("m", 2048))), O(A(("n", 2048), ("k", 3072)))], [["k", "m"], ["n", "k"]],
+                            ["m", "n"], dt), lambda a, b: a.T @ b.T),
+    "bias": (lambda dt: L.dot([O(A(("batch", 2048), 3072)), O(A(3072, 2048)), O(A(2048))], dt,
+                              epilogue=(True, A(("batch", 2048), 2048))), lambda a, b: a @ b),
+}
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("layout", list(D16))
+def test_d16_tiles_within_band(ex, layout, dt):
+    from oracle import kernel_text as kt
+    mk, prod = D16[layout]
+    low = mk(dt)
+    print(f"[gemm] d16 {layout} {dt}", flush=True)
+    k = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(5)
+    vals = [fmt.roundtrip(rng.standard_normal(b.dims).astype(np.float32), dt).astype(np.float64) for b in k.inputs]
+    out = hip.DeviceBuffer(k.output.numel * 2)
+    out.upload(np.full(k.output.numel * 2, 0xFF, np.uint8))
+    c = ex.run(low.text, dt, [hip.DeviceBuffer.of(fmt.encode(v.astype(np.float32), dt)) for v in vals], out, lanes=low.lanes)
+    assert c.kind == "gemm" and c.order == "mfma-k16", (c.kind, c.order)
+    got = fmt.decode(out.download(np.uint16), dt).astype(np.float64).reshape(k.output.dims)
+    a, b = vals[0].reshape(k.inputs[0].dims), vals[1].reshape(k.inputs[1].dims)
+    exact = prod(a, b)
+    S = prod(np.abs(a), np.abs(b))
+    if layout == "bias":
+        exact = fmt.roundtrip(exact.astype(np.float32), dt).astype(np.float64) + vals[2]
+    K = c.flops / (2 * k.output.numel)
+    gamma = K * 2.0 ** -24 / (1 - K * 2.0 ** -24)
+    bound = gamma * S + ULP[dt] * (S + 2 * np.maximum(np.abs(exact), np.abs(got))) + 1e-30
+    err = np.abs(got - exact)
+    assert np.all(np.isfinite(got)), "unwritten or non-finite outputs"
+    assert np.all(err <= bound), f"{np.count_nonzero(err > bound)} elements outside the band"
+    assert np.median(err / bound) < 1 / 16, f"median error {np.median(err / bound):.3g} of the band"
