@@ -167,6 +167,20 @@ PK_DEV float pk_ldexpf(float y, int n) {
     return y * pk_float((unsigned)(0x7f + n) << 23);
 }
 
+// expf's quotient r c / (2 - c): |r| <= 0.35, so 2 - c lies in [1.6, 2.4]
+// and |r c| < 0.13.  Markstein's step on a reciprocal refined once from the
+// hardware estimate (y0 = rcp(b), y = y0 + y0 (1 - b y0); q0 = a y,
+// q = q0 + y (a - b q0), each in one fma) in place of the correctly rounded
+// division's scale/fixup sequence.  Not correctly rounded in general: it
+// gives the division's bits on every argument expf sees (pinned by the
+// all-f32 digests of pk_expf and its softmax fast path).
+PK_DEV float pk_expf_quot(float a, float b) {
+    const float y0 = __builtin_amdgcn_rcpf(b);
+    const float y = __builtin_fmaf(__builtin_fmaf(-b, y0, 1.0f), y0, y0);
+    const float q0 = a * y;
+    return __builtin_fmaf(__builtin_fmaf(-q0, b, a), y, q0);
+}
+
 // fdlibm's expf, its branches written as selects (the same operations on
 // every path, so the same bits): k = 0 is the general reduction with k = 0
 // (x - 0 * ln2_hi is x, 0 * ln2_lo is 0), scalbnf's one pre-scaling step is
@@ -187,7 +201,7 @@ PK_DEV float pk_expf(float x) {
     const float r = hi - lo;
     const float rr = r * r;
     const float c = r - rr * (p1 + rr * p2);
-    const float y = 1.0f + (r * c / (2.0f - c) - lo + hi);
+    const float y = 1.0f + (pk_expf_quot(r * c, 2.0f - c) - lo + hi);
     // y * 2^k as scalbnf computes it (k lies in [-150, 150])
     const bool up = k > 127, down = k < -126;
     const float s = up ? 0x1p127f : down ? 0x1p-102f : 1.0f;
@@ -218,7 +232,7 @@ PK_DEV float pk_expf_le0(float x) {
     const float r = hi - lo;
     const float rr = r * r;
     const float c = r - rr * (p1 + rr * p2);
-    const float y = 1.0f + (r * c / (2.0f - c) - lo + hi);
+    const float y = 1.0f + (pk_expf_quot(r * c, 2.0f - c) - lo + hi);
     const float res = k == 0 ? y : y * pk_float((unsigned)(0x7f + k) << 23);
     return ax <= 0x39000000u ? 1.0f + x : res;
 }
