@@ -181,6 +181,11 @@ PK_DEV float pk_expf_quot(float a, float b) {
     return __builtin_fmaf(__builtin_fmaf(-q0, b, a), y, q0);
 }
 
+// The same quotient for erff's rational approximations, whose denominators
+// lie in [1, 50] there and whose numerators are bounded: the division's bits
+// on every f32 (pinned by the all-f32 digest of erff).
+PK_DEV float pk_erf_quot(float a, float b) { return pk_expf_quot(a, b); }
+
 // fdlibm's expf, its branches written as selects (the same operations on
 // every path, so the same bits): k = 0 is the general reduction with k = 0
 // (x - 0 * ln2_hi is x, 0 * ln2_lo is 0), scalbnf's one pre-scaling step is
@@ -355,7 +360,7 @@ PK_DEV float pk_erf_mid(float x) {
     const float s = __builtin_fabsf(x) - 1.0f;
     const float p = a0 + s * (a1 + s * (a2 + s * (a3 + s * (a4 + s * (a5 + s * a6)))));
     const float q = 1.0f + s * (b1 + s * (b2 + s * (b3 + s * (b4 + s * (b5 + s * b6)))));
-    return 1.0f - erx - p / q;
+    return 1.0f - erx - pk_erf_quot(p, q);
 }
 
 PK_DEV float pk_erfc_tail(unsigned ax, float x) {
@@ -389,7 +394,7 @@ PK_DEV float pk_erff(float x) {
         const float z = x * x;
         const float r = 1.2837916613e-01f + z * (-3.2504209876e-01f + z * (-2.8481749818e-02f + z * (-5.7702702470e-03f + z * -2.3763017452e-05f)));
         const float s = 1.0f + z * (3.9791721106e-01f + z * (6.5022252500e-02f + z * (5.0813062117e-03f + z * (1.3249473704e-04f + z * -3.9602282413e-06f))));
-        const float y = r / s;
+        const float y = pk_erf_quot(r, s);
         return x + x * y;
     }
     float y;
