@@ -306,6 +306,14 @@ void plan_tiles(GemmArgs& g) {
         g.bn = 128;
         g.tiles_m = (int)((g.M + 255) / 256);
         g.tiles_n = (int)((g.N + 127) / 128);
+        // 256 x 256 tiles (a wave 128 x 128, a third fewer operand bytes a
+        // flop) where they fill three rounds of the CUs or more: measured 7 %
+        // faster at [2048 x 4096] . [4096 x 32000], slower at 344 tiles
+        const long long t256 = (long long)g.tiles_m * ((g.N + 255) / 256) * g.batch;
+        if (t256 >= 768) {
+            g.bn = 256;
+            g.tiles_n = (int)((g.N + 255) / 256);
+        }
     }
 }
 

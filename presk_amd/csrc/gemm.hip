@@ -480,7 +480,14 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     typedef D16Loader<AK, BM> QA;
     typedef D16Loader<BK_, BN> QB;
     constexpr int STAGE = QA::BYTES + QB::BYTES;
-    constexpr int OPER = D16 ? 3 * STAGE : 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = BM * CLD * 4;
+    // straight-into-LDS stages: three where they fit (256 x 128 tiles, 144 KB),
+    // else two (256 x 256, 128 KB)
+    constexpr int NS = 3 * STAGE <= 150 * 1024 ? 3 : 2;
+    // the epilogue stages the tile's f32 sums in LDS whole, or in two halves
+    // of rows when the whole would not fit beside nothing else (256 x 256)
+    constexpr int EH = BM * CLD * 4 <= 150 * 1024 ? 1 : 2, EROWS = BM / EH;
+    constexpr int OPER = D16 ? NS * STAGE : 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = EROWS * CLD * 4;
+    static_assert(EH == 1 || (WM * MF) % EROWS == 0, "each wave's rows lie in one half");
     __shared__ __attribute__((aligned(16))) char smem[OPER > CTILE ? OPER : CTILE];
     S* const As0 = (S*)smem;
     S* const Bs0 = As0 + 2 * ASZ;
@@ -530,7 +537,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
 
     const int nk = (kend - kbeg + BK - 1) / BK;
     if constexpr (D16) {
-        // Three stages: block kt + 2 streams into LDS while block kt is
+        // NS stages: block kt + NS - 1 streams into LDS while block kt is
         // multiplied.  The fragments of each 16-k step are read while the
         // previous step's MFMAs run; before the last step of a block, the
         // next block's first fragments are read once this thread's loads of
@@ -538,6 +545,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
         // flight) and a barrier has seen every thread's -- the barrier also
         // retires every read of the stage the next loads overwrite.
         constexpr int NL = QA::ROUNDS + QB::ROUNDS;   // loads a thread issues per block
+        constexpr int LA = NS - 1;                    // blocks in flight ahead
         QA qa;
         QB qb;
         unsigned char* const st0 = (unsigned char*)smem;
@@ -557,7 +565,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
         };
         if (nk > 0) {
             fetch(0, 0);
-            if (nk > 1) {
+            if (LA == 2 && nk > 1) {
                 fetch(1, 1);
                 wait_vm<NL>();
             } else {
@@ -568,7 +576,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
         }
         auto block = [&](int kt, auto stage) {
             constexpr int S = decltype(stage)::value;
-            if (kt + 2 < nk) fetch(kt + 2, (S + 2) % 3);
+            if (kt + LA < nk) fetch(kt + LA, (S + LA) % NS);
             const unsigned char* const st = st0 + S * STAGE;
 #pragma unroll
             for (int kk = 0; kk < BK; kk += KSTEP) {
@@ -580,10 +588,10 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
                 if (kk + KSTEP < BK) {
                     read(st, kk + KSTEP);
                 } else if (kt + 1 < nk) {
-                    if (kt + 2 < nk) wait_vm<NL>();
+                    if (LA == 2 && kt + 2 < nk) wait_vm<NL>();
                     else wait_vm<0>();
                     __syncthreads();
-                    read(st0 + ((S + 1) % 3) * STAGE, 0);
+                    read(st0 + ((S + 1) % NS) * STAGE, 0);
                 }
                 // the reads stay ahead of this step's MFMAs (the scheduler
                 // would otherwise pair each read with the MFMA that uses it)
@@ -595,17 +603,25 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
-        // whole rounds of the three stages, then the last one or two blocks
-        // (straight-line rounds keep the accumulators in place)
+        // whole rounds of the stages, then the last blocks (straight-line
+        // rounds keep the accumulators in place)
         int kt = 0;
-        for (; kt + 3 <= nk; kt += 3) {
-            block(kt, std::integral_constant<int, 0>{});
-            block(kt + 1, std::integral_constant<int, 1>{});
-            block(kt + 2, std::integral_constant<int, 2>{});
-        }
-        if (kt < nk) {
-            block(kt, std::integral_constant<int, 0>{});
-            if (kt + 1 < nk) block(kt + 1, std::integral_constant<int, 1>{});
+        if constexpr (NS == 3) {
+            for (; kt + 3 <= nk; kt += 3) {
+                block(kt, std::integral_constant<int, 0>{});
+                block(kt + 1, std::integral_constant<int, 1>{});
+                block(kt + 2, std::integral_constant<int, 2>{});
+            }
+            if (kt < nk) {
+                block(kt, std::integral_constant<int, 0>{});
+                if (kt + 1 < nk) block(kt + 1, std::integral_constant<int, 1>{});
+            }
+        } else {
+            for (; kt + 2 <= nk; kt += 2) {
+                block(kt, std::integral_constant<int, 0>{});
+                block(kt + 1, std::integral_constant<int, 1>{});
+            }
+            if (kt < nk) block(kt, std::integral_constant<int, 0>{});
         }
     } else if constexpr (DL && MF == 16) {
         // One k-block ahead: block kt+1 streams into one LDS buffer while
@@ -701,28 +717,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     // The tile's sums go through LDS (lane holds column lane & 15, rows
     // 4*(lane >> 4) + r of each 16x16 tile) so that each thread then stores
     // 16 contiguous bytes of one output row.
-    __syncthreads();
     float* const cs = (float*)smem;
-    if constexpr (MF == 32) {
-        // a 32x32 tile: lane holds column lane & 31, rows 8 * (r >> 2) +
-        // 4 * (lane >> 5) + (r & 3), r = 0 .. 15
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    cs[(wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * CLD + wn + j * 32 + (lane & 31)] = acc[i][j][r];
-    } else {
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) cs[(wm + i * 16 + (lane >> 4) * 4 + r) * CLD + wn + j * 16 + (lane & 15)] = acc[i][j][r];
-    }
-    __syncthreads();
-
     constexpr int OV = 16 / (int)sizeof(S);  // output elements per 16-byte store
     constexpr int TPR = BN / OV, RPR = NT / TPR;  // threads past TPR*RPR store nothing
     bool ovf = false;
@@ -738,8 +733,36 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     for (int e = 0; e < OV; ++e)
         bcol[e] = g.bias && g.bias_kind == 1 && g.splits <= 1 && n + e < N ? load_bias<ST>(g.bias, n + e) : 0.f;
     const float bscalar = g.bias && g.bias_kind == 3 && g.splits <= 1 ? load_bias<ST>(g.bias, 0) : 0.f;
-    for (int rr = threadIdx.x < TPR * RPR ? (int)threadIdx.x / TPR : BM; rr < BM; rr += RPR) {
-        const int m = (int)m0 + rr;
+#pragma unroll 1
+    for (int h = 0; h < EH; ++h) {
+    // the waves whose rows lie in this half stage their sums
+    __syncthreads();
+    if (EH == 1 || wm / EROWS == h) {
+        const int w0 = wm - h * EROWS;
+        if constexpr (MF == 32) {
+            // a 32x32 tile: lane holds column lane & 31, rows 8 * (r >> 2) +
+            // 4 * (lane >> 5) + (r & 3), r = 0 .. 15
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        cs[(w0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * CLD + wn + j * 32 + (lane & 31)] =
+                            acc[i][j][r];
+        } else {
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        cs[(w0 + i * 16 + (lane >> 4) * 4 + r) * CLD + wn + j * 16 + (lane & 15)] = acc[i][j][r];
+        }
+    }
+    __syncthreads();
+    for (int rr = threadIdx.x < TPR * RPR ? (int)threadIdx.x / TPR : EROWS; rr < EROWS; rr += RPR) {
+        const int m = (int)m0 + h * EROWS + rr;
         if (m >= M || n >= N) continue;
         float v[OV];
 #pragma unroll
@@ -776,6 +799,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
         } else {
             for (int e = 0; e < OV && n + e < N; ++e) c[e] = out[e];
         }
+    }
     }
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
@@ -837,10 +861,11 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
         // operand pointers off 16 bytes: the same products from
         // register-staged tiles, element-wise loads
         if constexpr (ST != kF32) {
-            if (fast && g.K % St<ST>::BK == 0 && (g.splits <= 1 || g.k_per_split % St<ST>::BK == 0))
-                e = launch_shape<ST, 4, 2, false, true, 32>(g, stream);
+            const bool whole = fast && g.K % St<ST>::BK == 0 && (g.splits <= 1 || g.k_per_split % St<ST>::BK == 0);
+            if (g.bn == 256)  // 256 x 256 tiles, a wave 128 x 128
+                e = whole ? launch_shape<ST, 4, 4, false, true, 32>(g, stream) : launch_shape<ST, 4, 4, true, false, 32>(g, stream);
             else
-                e = launch_shape<ST, 4, 2, true, false, 32>(g, stream);
+                e = whole ? launch_shape<ST, 4, 2, false, true, 32>(g, stream) : launch_shape<ST, 4, 2, true, false, 32>(g, stream);
         } else {
             e = hipErrorInvalidValue;
         }
