@@ -586,7 +586,8 @@ std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
     const int st = k.dtype == Ty::F32 ? 0 : k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : -1;
     if (st < 0 || k.inputs.empty() || k.inputs[0].ty != k.dtype || k.output.ty != k.dtype) return nullptr;
     const bool squares = k.name == "sum_squares";
-    if ((k.name == "sum_all" || k.name == "mean_all" || squares) && k.inputs.size() == 1 && k.output.dims.empty()) {
+    // the totals SumAll / MeanAll are the kernels `sum` and `mean` (PrimOp::name)
+    if ((k.name == "sum" || k.name == "mean" || squares) && k.inputs.size() == 1 && k.output.dims.empty()) {
         // every element, as one column
         auto p = std::make_unique<ColSumPlan>();
         p->n_in = 1;
@@ -596,7 +597,7 @@ std::unique_ptr<ClassPlan> classify_sum_to(const Kernel& k) {
         p->a.chunk = 64;
         p->a.nchunks = (p->a.rows + p->a.chunk - 1) / p->a.chunk;
         if (p->a.nchunks > 65535) return nullptr;
-        p->a.div = k.name == "mean_all" ? (float)(double)p->a.rows : 0.f;
+        p->a.div = k.name == "mean" ? (float)(double)p->a.rows : 0.f;
         p->a.square = squares ? 1 : 0;
         p->a.storage = st;
         p->a.ld = 1;
@@ -697,12 +698,12 @@ std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
         return !x.names.back().empty() && x.names.back() == name;
     };
     std::string rest;
-    if ((n == "mean_all" || n == "sum_all") && k.inputs.size() == 1 && k.output.dims.empty()) {
+    if ((n == "mean" || n == "sum") && k.inputs.size() == 1 && k.output.dims.empty()) {
         // every element as one row, summed in index order (lower.rs:1221-1233)
         p->a.rows = 1;
         p->a.n = x.numel();
         p->a.n_real = (float)(double)p->a.n;
-        p->a.op = n == "mean_all" ? kRowMean : kRowSum;
+        p->a.op = n == "mean" ? kRowMean : kRowSum;
     } else if (last_axis("mean axis ", &rest) && rest.empty() && k.inputs.size() == 1) {
         p->a.op = kRowMean;
     } else if (last_axis("sum axis ", &rest) && rest.empty() && k.inputs.size() == 1) {

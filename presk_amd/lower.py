@@ -309,7 +309,8 @@ def unary(op, ins, dtype) -> Lowered:
     bd = B()
     v = bd.loops(dims(a.axes))
     x = f"real({load(0, ivs(v))})" if a.kind == "idx" else load(0, ivs(v))
-    name = {"pow2": "pow(2)"}.get(op, op)
+    # PrimOp::name (crates/presk-core/src/ir.rs:345-420): `pow n`, `gelu'`
+    name = f"pow {op[3:]}" if op.startswith("pow") else {"gelu_deriv": "gelu'"}.get(op, op)
     return kernel(name, dtype, ins, a.axes, "real", bd, nest(v, dims(a.axes), [Store(1, ivs(v), unary_expr(op, x))]))
 
 
@@ -752,14 +753,17 @@ def _axis_pos(axes, name):
 
 
 def reduce_all(op, ins, dtype) -> Lowered:
-    """lower.rs:1221-1233 (`sum_all`/`mean_all`)."""
+    """lower.rs:1221-1233 (SumAll/MeanAll: the kernels `sum` and `mean`,
+    PrimOp::name, crates/presk-core/src/ir.rs:371-372); `op` "sum"/"mean"
+    ("sum_all"/"mean_all" name the same)."""
+    op = {"sum_all": "sum", "mean_all": "mean"}.get(op, op)
     t = ins[0]
     bd = B()
     v = bd.loops(dims(t.axes))
     acc = bd.sv()
     body = [Set(acc, num(0))] + nest(v, dims(t.axes), [Set(acc, bin_("+", sv(acc), load(0, ivs(v))))])
     n = math.prod(dims(t.axes))
-    value = bin_("/", sv(acc), num(n)) if op == "mean_all" else sv(acc)
+    value = bin_("/", sv(acc), num(n)) if op == "mean" else sv(acc)
     body.append(Store(1, [], value))
     return kernel(op, dtype, ins, [], "real", bd, body)
 
