@@ -438,7 +438,45 @@ __global__ void __launch_bounds__(64) rows_walk_kernel(RowArgs a) {
             put();
             __syncthreads();
             if (ch + 1 < nch) fetch(c0 + CW, (int)(n - c0 - CW < CW ? n - c0 - CW : CW));
-            if (walker) {
+            if (walker && cw == CW) {
+                const float* t = &tile[lane * TS];
+                if constexpr (OP == kRowMean || OP == kRowSum || (OP == kSumToRows && ST == 0)) {
+                    // one add an element: the chunk straight through, in
+                    // groups of 16 elements, each group's four LDS reads
+                    // issued three groups (48 dependent adds) ahead of their
+                    // use; the scheduler barriers keep them there
+                    constexpr int NG = CW / 16, AHEAD = 3;
+                    float4 q[NG][4];
+                    auto rdg = [&](int g) {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) q[g][u] = *(const float4*)&t[16 * g + 4 * u];
+                    };
+#pragma unroll
+                    for (int g = 0; g < AHEAD && g < NG; ++g) rdg(g);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int g = 0; g < NG; ++g) {
+                        if (g + AHEAD < NG) rdg(g + AHEAD);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            visit(q[g][u].x);
+                            visit(q[g][u].y);
+                            visit(q[g][u].z);
+                            visit(q[g][u].w);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else {
+#pragma unroll 8
+                    for (int j = 0; j < CW; j += 4) {
+                        const float4 q = *(const float4*)&t[j];
+                        visit(q.x);
+                        visit(q.y);
+                        visit(q.z);
+                        visit(q.w);
+                    }
+                }
+            } else if (walker) {
                 const float* t = &tile[lane * TS];
                 int j = 0;
 #pragma unroll 8
