@@ -75,7 +75,19 @@ typedef struct {
 
 /* Selects the device and sets the executor up.  No counterpart in the
  * reference (its executors need none); must be called before any other
- * function that touches the device. */
+ * function that touches the device.  `device` -1 takes PRESK_HIP_DEVICE
+ * (an ordinal; device 0 when unset).  The environment's other switches are
+ * checked here, a malformed one failing the call (E10001):
+ *   PRESK_HIP_MODE=exact|fast       every kernel compiled in that mode, whatever
+ *                                   presk_hip_compile is asked (exact: the
+ *                                   interpreter's order in every kernel);
+ *   PRESK_HIP_GEMM_TILE=<bm>x<bn>[/<splits>]
+ *                                   contraction tiles (128 x 64/96/128, or
+ *                                   256 x 128/256 on 16-bit storage) and k
+ *                                   splits (1-64, single-entry contractions)
+ *                                   in place of the planner's, where they apply;
+ *   PRESK_HIP_CACHE, PRESK_HIP_DUMP  the generated kernels' code-object cache
+ *                                   and a directory to keep their sources in. */
 int presk_hip_init(int device);
 
 /* The message of the calling thread's last failed call ("" if none). */

@@ -8,6 +8,8 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 #include <functional>
 #include <map>
 #include <mutex>
@@ -238,6 +240,53 @@ int storage_of(Ty t) {
     }
 }
 
+}  // namespace
+
+bool tile_override(TileOverride* t, std::string* err) {
+    *t = TileOverride{};
+    const char* env = std::getenv("PRESK_HIP_GEMM_TILE");
+    if (!env || !*env) return true;
+    int bm = 0, bn = 0, splits = 0, used = 0;
+    bool ok = std::sscanf(env, "%dx%d%n", &bm, &bn, &used) == 2;
+    const char* rest = env + used;
+    if (ok && *rest == '/') {
+        ok = std::sscanf(rest, "/%d%n", &splits, &used) == 1 && splits >= 1 && splits <= 64;
+        rest += ok ? used : 0;
+    }
+    const bool shape = (bm == 128 && (bn == 64 || bn == 96 || bn == 128)) || (bm == 256 && (bn == 128 || bn == 256));
+    if (!ok || *rest != '\0' || !shape) {
+        *err = std::string("PRESK_HIP_GEMM_TILE=") + env +
+               ": expected <bm>x<bn>[/<splits>] with bm 128 (bn 64, 96, 128) or 256 (bn 128, 256) and splits 1-64";
+        return false;
+    }
+    *t = TileOverride{bm, bn, splits};
+    return true;
+}
+
+namespace {
+
+// The override's tiles and splits where they apply to `g` (see tile_override).
+void apply_override(GemmArgs& g) {
+    TileOverride t;
+    std::string err;
+    if (!tile_override(&t, &err) || t.bm == 0) return;
+    if (t.bm == 128 || g.storage != kF32) {
+        g.bm = t.bm;
+        g.bn = t.bn;
+        g.tiles_m = (int)((g.M + g.bm - 1) / g.bm);
+        g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
+    }
+    const int bk = gemm_block_k(g.storage);
+    const long long nkb = (g.K + bk - 1) / bk;
+    if (g.bm == 256) {
+        g.splits = 1;
+        g.k_per_split = g.K;
+    } else if (t.splits > 0 && g.batch == 1 && t.splits <= nkb) {
+        g.splits = t.splits;
+        g.k_per_split = t.splits > 1 ? (nkb + t.splits - 1) / t.splits * bk : g.K;
+    }
+}
+
 void plan_tiles(GemmArgs& g) {
     g.bm = 128;
     g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
@@ -315,6 +364,7 @@ void plan_tiles(GemmArgs& g) {
             g.tiles_n = (int)((g.N + 255) / 256);
         }
     }
+    apply_override(g);
 }
 
 std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {

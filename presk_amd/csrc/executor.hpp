@@ -47,6 +47,19 @@ struct ClassPlan {
 // nullptr when the nest is left to the generic printer.
 std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode);
 
+// PRESK_HIP_GEMM_TILE=<bm>x<bn>[/<splits>] (e.g. "256x256", "128x64/4"):
+// the contraction tiles, and the k splits of a single-entry contraction, that
+// every contraction takes where they apply, in place of the plan's choice.
+// bm 128 takes bn 64, 96 or 128; bm 256 (16-bit storage, no k split) takes
+// bn 128 or 256; splits 1 to 64.  Where an override does not apply (bm 256
+// on f32, splits on a batched `ein`, more splits than k-blocks), that part
+// is left to the plan.  False with a message when the variable is set and
+// malformed; an unset or empty variable is no override (bm 0).
+struct TileOverride {
+    int bm = 0, bn = 0, splits = 0;
+};
+bool tile_override(TileOverride* t, std::string* err);
+
 // The algorithmic bytes of a launch (inputs once + output once at storage
 // width, crates/presk-kernel/src/cost.rs:26-95) and the contraction flops.
 double kernel_bytes(const Kernel& k);

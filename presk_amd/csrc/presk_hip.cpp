@@ -51,6 +51,18 @@ uint64_t fnv1a(const std::string& s) {
     return h;
 }
 
+// PRESK_HIP_MODE=exact|fast: every kernel compiled in that mode whatever
+// the caller asks (exact: the interpreter's order everywhere, the parity
+// switch); -1 when unset or empty, -2 with a message when malformed
+int forced_mode(std::string* err) {
+    const char* env = std::getenv("PRESK_HIP_MODE");
+    if (!env || !*env) return -1;
+    if (std::strcmp(env, "exact") == 0) return PRESK_HIP_EXACT;
+    if (std::strcmp(env, "fast") == 0) return PRESK_HIP_FAST;
+    *err = std::string("PRESK_HIP_MODE=") + env + ": expected exact or fast";
+    return -2;
+}
+
 std::string cache_dir() {
     const char* env = std::getenv("PRESK_HIP_CACHE");
     if (env && *env) return env;
@@ -219,6 +231,20 @@ extern "C" {
 const char* presk_hip_last_error(void) { return g_error.c_str(); }
 
 int presk_hip_init(int device) {
+    // device -1: PRESK_HIP_DEVICE, else device 0
+    if (device < 0) {
+        const char* env = std::getenv("PRESK_HIP_DEVICE");
+        char* end = nullptr;
+        const long d = env && *env ? std::strtol(env, &end, 10) : 0;
+        if (env && *env && (*end != '\0' || d < 0 || d > 1 << 16))
+            return fail(PRESK_HIP_ERR, std::string("E10001: PRESK_HIP_DEVICE=") + env + ": expected a device ordinal");
+        device = (int)d;
+    }
+    // the environment's switches are checked once, here
+    std::string err;
+    TileOverride t;
+    if (!tile_override(&t, &err)) return fail(PRESK_HIP_ERR, "E10001: " + err);
+    if (forced_mode(&err) == -2) return fail(PRESK_HIP_ERR, "E10001: " + err);
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
     g_device = device;
@@ -238,6 +264,8 @@ int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, 
     if (!k->arith.empty())
         return fail(PRESK_HIP_REFUSED, "E7005: the kernel `" + k->name + "` computes in " + k->arith +
                                            ", which only the kernel interpreter emulates");
+    if (const int forced = forced_mode(&err); forced >= 0) mode = forced;
+    if (mode != PRESK_HIP_EXACT && mode != PRESK_HIP_FAST) return fail(PRESK_HIP_ERR, "E10001: mode is neither EXACT nor FAST");
     auto h = std::make_unique<presk_hip_kernel>();
     h->mode = mode;
     h->plan = classify(*k, mode);

@@ -104,6 +104,7 @@ _initialized = None
 
 
 def init(device: int = 0):
+    """presk_hip_init; device -1 takes PRESK_HIP_DEVICE (device 0 when unset)."""
     global _initialized
     if _initialized != device:
         check(lib().presk_hip_init(device))

@@ -1,0 +1,54 @@
+"""The executor's environment switches, without a GPU: PRESK_HIP_MODE (the
+parity switch), PRESK_HIP_GEMM_TILE (contraction tiles and k splits in place
+of the planner's) and PRESK_HIP_DEVICE, each malformed value refused by
+presk_hip_init before any device is touched."""
+import ctypes
+
+import pytest
+
+from presk_amd import hip, lower as L
+
+A, O = L.ax, L.Operand
+
+
+def dot(m, k, n, dt):
+    return L.dot([O(A(("seq", m), ("model", k))), O(A(k, n))], dt)
+
+
+def compiled(low, mode=hip.FAST):
+    return hip.Compiled(low.text, low.dtype, low.lanes, mode)
+
+
+def test_mode_switch_forces_exact(monkeypatch):
+    low = dot(256, 512, 256, "f32")
+    assert compiled(low).kind == "gemm"
+    exact = compiled(low, hip.EXACT)
+    monkeypatch.setenv("PRESK_HIP_MODE", "exact")
+    forced = compiled(low, hip.FAST)
+    assert (forced.kind, forced.order) == (exact.kind, exact.order) and forced.kind != "gemm"
+    monkeypatch.setenv("PRESK_HIP_MODE", "fast")
+    assert compiled(low, hip.EXACT).kind == "gemm"
+
+
+def test_tile_override(monkeypatch):
+    bf = dot(2048, 1024, 2048, "bf16")
+    f32 = dot(256, 8192, 256, "f32")
+    assert compiled(bf).order == "mfma-k32"          # the planner: 128-row tiles at K 1024
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "256x256")
+    assert compiled(bf).order == "mfma-k16"          # 256-row tiles of 32x32x16 MFMAs
+    assert compiled(f32).order.startswith("mfma-f32-k4")  # no 256-row f32 tiles: the planner's
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x64/4")
+    assert compiled(f32).order == "mfma-f32-k4-split4"
+    assert compiled(bf).order == "mfma-k32-split4"
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x128/1")
+    assert compiled(f32).order == "mfma-f32-k4"
+
+
+@pytest.mark.parametrize("var,value", [("PRESK_HIP_GEMM_TILE", "256x64"), ("PRESK_HIP_GEMM_TILE", "128x128/0"),
+                                       ("PRESK_HIP_GEMM_TILE", "128x128x"), ("PRESK_HIP_MODE", "fastest"),
+                                       ("PRESK_HIP_DEVICE", "one")])
+def test_malformed_switch_fails_init(monkeypatch, var, value):
+    monkeypatch.setenv(var, value)
+    assert hip.lib().presk_hip_init(-1) != 0
+    msg = hip.lib().presk_hip_last_error().decode()
+    assert msg.startswith("E10001") and var in msg
