@@ -500,29 +500,48 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     // range over all XCDs measures faster: items go in plain order.  Within a
     // run, tiles go 8 row-tiles at a time across the columns, so that
     // concurrent tiles share A rows.
-    const long long tiles = (long long)g.tiles_m * g.tiles_n;
-    const long long total = (long long)gridDim.x;
-    const long long xcd = blockIdx.x % 8, local = blockIdx.x / 8;
-    const long long q8 = total / 8, r8 = total % 8;
-    const long long item = g.splits > 1 ? (long long)blockIdx.x : xcd * q8 + (xcd < r8 ? xcd : r8) + local;
-    const int split = (int)(item / (tiles * g.batch));
-    const long long batch = (item / tiles) % g.batch;
-    const long long bid = item % tiles;
-    constexpr long long GROUP = 8;
-    const long long group_size = GROUP * g.tiles_n;
-    const long long grp = bid / group_size;
-    const long long first_m = grp * GROUP;
-    const long long gm = (g.tiles_m - first_m) < GROUP ? (g.tiles_m - first_m) : GROUP;
-    const long long tm_idx = first_m + (bid % group_size) % gm;
-    const long long tn_idx = (bid % group_size) / gm;
-    const long long m0 = tm_idx * BM, n0 = tn_idx * BN;
+    // The arithmetic is 32-bit: the launcher keeps the items below 2^31 and
+    // the plan the batch below 2^16 (64-bit divisions cost hundreds of scalar
+    // instructions a wave, before the first load is issued).
+    const unsigned tiles = (unsigned)g.tiles_m * (unsigned)g.tiles_n;
+    const unsigned total = gridDim.x;
+    const unsigned nb = (unsigned)g.batch;
+    const unsigned xcd = blockIdx.x % 8, local = blockIdx.x / 8;
+    const unsigned q8 = total / 8, r8 = total % 8;
+    const unsigned item = g.splits > 1 ? blockIdx.x : xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    const unsigned tb = item / tiles;
+    const int split = (int)(tb / nb);
+    const unsigned batch = tb - (unsigned)split * nb;
+    const unsigned bid = item - tb * tiles;
+    constexpr unsigned GROUP = 8;
+    const unsigned tiles_m = (unsigned)g.tiles_m;
+    const unsigned group_size = GROUP * (unsigned)g.tiles_n;
+    const unsigned grp = bid / group_size;
+    const unsigned first_m = grp * GROUP;
+    const unsigned gm = (tiles_m - first_m) < GROUP ? (tiles_m - first_m) : GROUP;
+    const unsigned in_grp = bid - grp * group_size;
+    const unsigned tn_idx = in_grp / gm;
+    const unsigned tm_idx = first_m + (in_grp - tn_idx * gm);
+    const long long m0 = (long long)tm_idx * BM, n0 = (long long)tn_idx * BN;
 
-    const S* A = (const S*)g.A + batch_offset(g, batch, g.sa_b);
-    const S* B = (const S*)g.B + batch_offset(g, batch, g.sb_b);
+    // the batch entry's offsets in A, B and C, one decomposition for all three
+    long long a_off = 0, b_off = 0, c_off = 0;
+    {
+        unsigned rest = batch;
+        for (int d = g.nbatch - 1; d >= 0; --d) {
+            const unsigned dim = (unsigned)g.bdim[d], q = rest / dim, i = rest - q * dim;
+            rest = q;
+            a_off += (long long)i * g.sa_b[d];
+            b_off += (long long)i * g.sb_b[d];
+            c_off += (long long)i * g.sc_b[d];
+        }
+    }
+    const S* A = (const S*)g.A + a_off;
+    const S* B = (const S*)g.B + b_off;
     // split s of S takes k-blocks [s*nkb/S, (s+1)*nkb/S)
-    const long long nkb = (g.K + BK - 1) / BK;
-    const int kbeg = (int)((long long)split * nkb / g.splits * BK);
-    int kend = (int)(((long long)split + 1) * nkb / g.splits * BK);
+    const unsigned nkb = (unsigned)((g.K + BK - 1) / BK), ns = (unsigned)g.splits;
+    const int kbeg = (int)((unsigned)split * nkb / ns * BK);
+    int kend = (int)(((unsigned)split + 1) * nkb / ns * BK);
     if (kend > (int)g.K) kend = (int)g.K;
     const int M = (int)g.M, N = (int)g.N;
     const int sa_m = (int)g.sa_m, sa_k = (int)g.sa_k, sb_k = (int)g.sb_k, sb_n = (int)g.sb_n;
@@ -721,7 +740,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     constexpr int OV = 16 / (int)sizeof(S);  // output elements per 16-byte store
     constexpr int TPR = BN / OV, RPR = NT / TPR;  // threads past TPR*RPR store nothing
     bool ovf = false;
-    const long long cbase = batch_offset(g, batch, g.sc_b);
+    const long long cbase = c_off;
     S* C = (S*)g.C + cbase;
     const int nl = (threadIdx.x % TPR) * OV;
     const int n = (int)n0 + nl;
@@ -809,7 +828,9 @@ template <int ST>
 __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= g.M * g.N) return;
-    const long long m = idx / g.N, n = idx % g.N;
+    // M * N < 2^31 (the plan's bound): 32-bit division
+    const unsigned nn = (unsigned)g.N, mq = (unsigned)idx / nn;
+    const long long m = mq, n = (unsigned)idx - mq * nn;
     // the partials in increasing split order, eight loads in flight
     const long long mn = g.M * g.N;
     float s = g.work[idx];
