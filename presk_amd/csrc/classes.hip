@@ -127,7 +127,9 @@ struct GemmPlan : ClassPlan {
 
     const char* kind() const override { return "gemm"; }
     std::string order() const override {
-        std::string o = storage == kF32 ? "mfma-f32-k4" : g.bm == 256 ? "mfma-k16" : "mfma-k32";
+        // 16-bit storage: 32x32x16 MFMAs (k in steps of 16) on every tile but
+        // the 128 x 96 one (16x16x32, steps of 32)
+        std::string o = storage == kF32 ? "mfma-f32-k4" : g.bm == 256 || g.bn != 96 ? "mfma-k16" : "mfma-k32";
         if (g.splits > 1) o += "-split" + std::to_string(g.splits);
         return o;
     }

@@ -8,20 +8,22 @@
 // (`dot_vjp_r`) and batched (`ein`) forms are one kernel.
 //
 // Order (declared, not the interpreter's index order): each output tile
-// accumulates on MFMA in f32 -- v_mfma_f32_16x16x32_{bf16,f16} (order
-// "mfma-k32") or, on the 256 x 128 tiles, v_mfma_f32_32x32x16_{bf16,f16}
-// ("mfma-k16") for 16-bit storage (the product of two 16-bit values is exact
+// accumulates on MFMA in f32 -- v_mfma_f32_32x32x16_{bf16,f16} (order
+// "mfma-k16") or, on the 128 x 96 tiles, v_mfma_f32_16x16x32_{bf16,f16}
+// ("mfma-k32") for 16-bit storage (the product of two 16-bit values is exact
 // in f32), and v_mfma_f32_16x16x4_f32 for f32 storage -- over k-blocks of 64
 // (32 for f32) in increasing k; when K is split across workgroups, the
 // partial sums are added in increasing split order by a second kernel
 // (deterministic).
 //
-// 16-bit storage, whole k-blocks and strides of whole 16-byte vectors (the
-// plan's choice when K is not split): 256 x 128 tiles, each wave 128 x 64 as
-// 4 x 2 MFMAs of 32x32x16, operands loaded straight into LDS three k-blocks
-// deep (D16Loader), the fragments of each 16-k step read while the previous
-// step's MFMAs run.  One workgroup a CU (144 KB of LDS); every other shape
-// takes the 128-row tiles below.
+// 16-bit storage, whole k-blocks and strides of whole 16-byte vectors:
+// 256 x 128 or 256 x 256 tiles (K of 3072 or more, no split), each wave
+// 128 x 64 or 128 x 128 as MFMAs of 32x32x16, operands loaded straight into
+// LDS three (two) k-blocks deep (D16Loader), the fragments of each 16-k step
+// read while the previous step's MFMAs run, one workgroup a CU; 128 x 128
+// and 128 x 64 tiles the same way in two stages, two workgroups a CU.
+// Operands off 16 bytes or partial k-blocks take the same tiles and MFMAs
+// from register-staged operands; 128 x 96 tiles take the 16x16 MFMAs below.
 //
 // Workgroup: 256 threads (4 waves as 2x2), tile (2*WM*16) x (2*WN*16), each
 // wave WM x WN MFMA tiles of 16x16.  Operands are staged through LDS,
@@ -247,7 +249,8 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 //   k-contiguous, [row][8 chunks of 8 k]: chunk c of row r in slot
 //     8 r + (c ^ ((r ^ (r >> 3)) & 7))
 //   m/n-contiguous, [k][ROWS / 8 chunks of 8 rows]: chunk j of k-row r in slot
-//     (ROWS / 8) r + (j ^ (2 (r & 3) ^ 8 (r & 1)))
+//     (ROWS / 8) r + (j ^ (2 (r & 3) ^ 8 (r & 1)))   (ROWS >= 128)
+//     (ROWS / 8) r + (j ^ 2 (r & 3))                 (ROWS = 64)
 // so that the 32x32x16 fragment reads below hit distinct banks in every
 // 16-lane (and 32-lane) phase: 16-byte reads of 16 consecutive rows, and
 // transposing 8-byte reads of 4 k-rows x 32 (64) bytes.  Rows past the
@@ -274,9 +277,13 @@ struct D16Loader {
     long long block_bytes;      // how far one k-block moves the origin (uniform)
     unsigned lds0;              // this wave's segment of the stage-0 tile (uniform)
 
-    __device__ static __forceinline__ int swz(int r) { return KCONTIG ? ((r ^ (r >> 3)) & 7) : ((2 * (r & 3)) ^ (8 * (r & 1))); }
+    // (a 64-row tile has 8 chunks a k-row: its swizzle stays below 8)
+    __device__ static __forceinline__ int swz(int r) {
+        return KCONTIG ? ((r ^ (r >> 3)) & 7) : ((2 * (r & 3)) ^ (ROWS >= 128 ? 8 * (r & 1) : 0));
+    }
     __device__ __forceinline__ void init(const unsigned short* p, int rows, long long rs, long long ks, int row0, int k0,
                                          unsigned tile) {
+        static_assert(KCONTIG || ROWS == 64 || ROWS % 128 == 0, "the swizzle stays inside a k-row");
         const int t = threadIdx.x;
         origin = (const char*)(p + (KCONTIG ? (long long)k0 : (long long)k0 * ks));
         block_bytes = KCONTIG ? 2LL * BK : 2LL * BK * ks;
@@ -481,8 +488,9 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     typedef D16Loader<BK_, BN> QB;
     constexpr int STAGE = QA::BYTES + QB::BYTES;
     // straight-into-LDS stages: three where they fit (256 x 128 tiles, 144 KB),
-    // else two (256 x 256, 128 KB)
-    constexpr int NS = 3 * STAGE <= 150 * 1024 ? 3 : 2;
+    // else two (256 x 256, 128 KB); two for 128-row tiles (64 or 48 KB), so
+    // that two workgroups share a CU
+    constexpr int NS = BM == 128 ? 2 : 3 * STAGE <= 150 * 1024 ? 3 : 2;
     // the epilogue stages the tile's f32 sums in LDS whole, or in two halves
     // of rows when the whole would not fit beside nothing else (256 x 256)
     constexpr int EH = BM * CLD * 4 <= 150 * 1024 ? 1 : 2, EROWS = BM / EH;
@@ -887,6 +895,22 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
                 e = whole ? launch_shape<ST, 4, 4, false, true, 32>(g, stream) : launch_shape<ST, 4, 4, true, false, 32>(g, stream);
             else
                 e = whole ? launch_shape<ST, 4, 2, false, true, 32>(g, stream) : launch_shape<ST, 4, 2, true, false, 32>(g, stream);
+        } else {
+            e = hipErrorInvalidValue;
+        }
+    } else if (ST != kF32 && (g.bn == 128 || g.bn == 64)) {
+        // 128 x 128 and 128 x 64 tiles of 32x32x16 MFMAs (a wave 64 x 64 or
+        // 64 x 32), operands straight into LDS in two stages (two workgroups
+        // a CU); operands off 16 bytes or partial k-blocks: the same products
+        // from register-staged tiles.  Measured 10-20 % faster than the
+        // register-staged 16x16x32 tiles at K 128-1536 (the course step's,
+        // the MLP block's and the Llama attention scores' shapes).
+        if constexpr (ST != kF32) {
+            const bool whole = fast && g.K % St<ST>::BK == 0 && (g.splits <= 1 || g.k_per_split % St<ST>::BK == 0);
+            if (g.bn == 128)
+                e = whole ? launch_shape<ST, 2, 2, false, true, 32>(g, stream) : launch_shape<ST, 2, 2, true, false, 32>(g, stream);
+            else
+                e = whole ? launch_shape<ST, 2, 1, false, true, 32>(g, stream) : launch_shape<ST, 2, 1, true, false, 32>(g, stream);
         } else {
             e = hipErrorInvalidValue;
         }

@@ -33,12 +33,16 @@ def test_mode_switch_forces_exact(monkeypatch):
 def test_tile_override(monkeypatch):
     bf = dot(2048, 1024, 2048, "bf16")
     f32 = dot(256, 8192, 256, "f32")
-    assert compiled(bf).order == "mfma-k32"          # the planner: 128-row tiles at K 1024
+    assert compiled(bf).order == "mfma-k16"          # the planner: 128 x 128 tiles of 32x32x16 MFMAs
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x96")
+    assert compiled(bf).order == "mfma-k32"          # 128 x 96 tiles of 16x16x32 MFMAs
     monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "256x256")
-    assert compiled(bf).order == "mfma-k16"          # 256-row tiles of 32x32x16 MFMAs
+    assert compiled(bf).order == "mfma-k16"
     assert compiled(f32).order.startswith("mfma-f32-k4")  # no 256-row f32 tiles: the planner's
     monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x64/4")
     assert compiled(f32).order == "mfma-f32-k4-split4"
+    assert compiled(bf).order == "mfma-k16-split4"
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x96/4")
     assert compiled(bf).order == "mfma-k32-split4"
     monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x128/1")
     assert compiled(f32).order == "mfma-f32-k4"
