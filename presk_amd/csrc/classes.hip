@@ -292,18 +292,34 @@ void apply_override(GemmArgs& g) {
 void plan_tiles(GemmArgs& g) {
     g.bm = 128;
     g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
-    // tile columns: 128, 96 or 64, whichever finishes first when the tiles
-    // run in rounds of 512 (two workgroups per CU) and a tile takes time in
-    // proportion to its width -- N = 384 fills the CUs in 4 columns of 96
-    // rather than 3 of 128, and N = 64 wastes nothing in 64 -- the widest on
-    // a tie (fewer operand bytes per flop)
     long long best = -1;
-    for (int bn : {128, 96, 64}) {
-        const long long t = (long long)g.tiles_m * ((g.N + bn - 1) / bn) * g.batch;
-        const long long cost = (t + 511) / 512 * bn;
-        if (best < 0 || cost < best) {
-            best = cost;
-            g.bn = bn;
+    if (g.storage == kF32) {
+        // tile columns: 128, 96 or 64, whichever finishes first when the
+        // tiles run in rounds of 512 (two workgroups per CU) and a tile takes
+        // time in proportion to its width -- N = 384 fills the CUs in 4
+        // columns of 96 rather than 3 of 128, and N = 64 wastes nothing in 64
+        // -- the widest on a tie (fewer operand bytes per flop)
+        for (int bn : {128, 96, 64}) {
+            const long long t = (long long)g.tiles_m * ((g.N + bn - 1) / bn) * g.batch;
+            const long long cost = (t + 511) / 512 * bn;
+            if (best < 0 || cost < best) {
+                best = cost;
+                g.bn = bn;
+            }
+        }
+    } else {
+        // 16-bit: 128 or 64 columns (32x32x16 MFMAs), in rounds of 512 and
+        // 768 workgroups (two and three a CU by their LDS), a 128 x 64 tile
+        // taking 3/4 of a 128 x 128 one's time (its A panel is the same) --
+        // fitted to the course step's, the MLP block's and the Llama's
+        // shapes, where this picks the faster of the two or one within 2 %
+        for (int bn : {128, 64}) {
+            const long long t = (long long)g.tiles_m * ((g.N + bn - 1) / bn) * g.batch;
+            const long long cost = bn == 128 ? (t + 511) / 512 * 4 : (t + 767) / 768 * 3;
+            if (best < 0 || cost < best) {
+                best = cost;
+                g.bn = bn;
+            }
         }
     }
     g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
@@ -339,11 +355,11 @@ void plan_tiles(GemmArgs& g) {
         }
     }
     // 16-bit storage without a k-split, whole k-blocks, K of 3072 or more
-    // and strides of whole 16-byte vectors: 256 x 128 tiles of 32x32x16
-    // MFMAs loaded straight into LDS (measured at the Llama, MLP and course
-    // shapes: 10-25 % faster from K 3072 up -- 4096 x 2048 x 4096 80 against
-    // 105 us -- but slower at K 128-2048, where the 128-row tiles' two
-    // workgroups a CU hide their prologue and epilogue)
+    // and strides of whole 16-byte vectors: 256 x 256 tiles (a wave 128 x
+    // 128, half the operand bytes a flop of a 128 x 128 tile, one workgroup a
+    // CU) where they fill three rounds of the CUs or more -- measured 5 %
+    // faster than 128 x 128 tiles at [2048 x 4096] . [4096 x 32000], slower
+    // at fewer tiles
     auto vec_strides = [&](long long other, const long long* bs) {
         if (other % 8) return false;
         for (int d = 0; d < g.nbatch; ++d)
@@ -351,20 +367,13 @@ void plan_tiles(GemmArgs& g) {
         return true;
     };
     const bool a_rows_vec = g.a_kcontig || g.M % 8 == 0, b_rows_vec = g.b_kcontig || g.N % 8 == 0;
+    const long long t256 = (long long)((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
     if (g.storage != kF32 && g.splits == 1 && g.K >= 3072 && g.K % gemm_block_k(g.storage) == 0 && a_rows_vec && b_rows_vec &&
-        vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) && vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b)) {
+        vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) && vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b) && t256 >= 768) {
         g.bm = 256;
-        g.bn = 128;
+        g.bn = 256;
         g.tiles_m = (int)((g.M + 255) / 256);
-        g.tiles_n = (int)((g.N + 127) / 128);
-        // 256 x 256 tiles (a wave 128 x 128, a third fewer operand bytes a
-        // flop) where they fill three rounds of the CUs or more: measured 7 %
-        // faster at [2048 x 4096] . [4096 x 32000], slower at 344 tiles
-        const long long t256 = (long long)g.tiles_m * ((g.N + 255) / 256) * g.batch;
-        if (t256 >= 768) {
-            g.bn = 256;
-            g.tiles_n = (int)((g.N + 255) / 256);
-        }
+        g.tiles_n = (int)((g.N + 255) / 256);
     }
     apply_override(g);
 }

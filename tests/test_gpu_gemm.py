@@ -142,10 +142,11 @@ def test_fast_contraction_within_band(ex, case):
     assert np.median(err / bound) < 1 / 64, f"{name}: median error {np.median(err / bound):.3g} of the band"
 
 
-# K >= 3072, whole k-blocks, aligned vectors, enough tiles for no k-split:
-# 256 x 128 tiles of 32x32x16 MFMAs loaded straight into LDS three k-blocks
-# deep, and 256 x 256 tiles (two k-blocks deep, the sums staged in two halves)
-# where they make three rounds of the CUs.  Each operand layout
+# K >= 3072, whole k-blocks, aligned vectors, no k-split: 128 x 128 and
+# 128 x 64 tiles of 32x32x16 MFMAs loaded straight into LDS two k-blocks
+# deep, 256 x 256 tiles (two k-blocks deep, the sums staged in two halves)
+# where they make three rounds of the CUs, and, under PRESK_HIP_GEMM_TILE,
+# the 256 x 128 tiles (three k-blocks deep).  Each operand layout
 # (k-contiguous or not), every remainder of the stage rounds, rows past a
 # tile, the bias.  Every output must be written (the buffer is poisoned with
 # NaNs) and 20 000 sampled elements must lie within gamma_K S plus the
@@ -168,12 +169,16 @@ D16 = {
 
 
 # the 256 x 256 tiles are the same code in f16 as in bf16: bf16 covers them at size
-@pytest.mark.parametrize("layout,dt", [(lay, dt) for lay in D16 for dt in ("bf16", "f16") if dt == "bf16" or D16[lay][2] <= 256 * 128])
-def test_d16_tiles_within_band(ex, layout, dt):
+@pytest.mark.parametrize("layout,dt,tiles", [(lay, dt, None) for lay in D16 for dt in ("bf16", "f16")
+                                             if dt == "bf16" or D16[lay][2] <= 256 * 128]
+                         + [("nn", "bf16", "256x128"), ("tt", "bf16", "256x128"), ("tn", "f16", "256x128")])
+def test_d16_tiles_within_band(ex, layout, dt, tiles, monkeypatch):
     from oracle import kernel_text as kt
     mk, form, tile = D16[layout]
     low = mk(dt)
-    print(f"[gemm] d16 {layout} {dt}", flush=True)
+    if tiles:
+        monkeypatch.setenv("PRESK_HIP_GEMM_TILE", tiles)
+    print(f"[gemm] d16 {layout} {dt} {tiles or ''}", flush=True)
     k = kt.parse_kernel(low.text)
     rng = np.random.default_rng(5)
     vals = [fmt.roundtrip(rng.standard_normal(b.dims, dtype=np.float32), dt) for b in k.inputs]
