@@ -188,8 +188,8 @@ PK_DEV float pk_erf_quot(float a, float b) { return pk_expf_quot(a, b); }
 
 // fdlibm's expf, its branches written as selects (the same operations on
 // every path, so the same bits): k = 0 is the general reduction with k = 0
-// (x - 0 * ln2_hi is x, 0 * ln2_lo is 0), scalbnf's one pre-scaling step is
-// a select of the factor, and the special inputs are chosen last.
+// (x - 0 * ln2_hi is x, 0 * ln2_lo is 0), scalbnf is one ldexp, and the
+// special inputs are chosen last.
 PK_DEV float pk_expf(float x) {
     const float ln2_hi = 6.9314575195e-1f, ln2_lo = 1.4286067653e-6f, inv_ln2 = 1.4426950216e+0f;
     const float p1 = 1.6666625440e-1f, p2 = -2.7667332906e-3f;
@@ -207,12 +207,11 @@ PK_DEV float pk_expf(float x) {
     const float rr = r * r;
     const float c = r - rr * (p1 + rr * p2);
     const float y = 1.0f + (pk_expf_quot(r * c, 2.0f - c) - lo + hi);
-    // y * 2^k as scalbnf computes it (k lies in [-150, 150])
-    const bool up = k > 127, down = k < -126;
-    const float s = up ? 0x1p127f : down ? 0x1p-102f : 1.0f;
-    const int kk = up ? k - 127 : down ? k + 102 : k;
-    const float scaled = (y * s) * pk_float((unsigned)(0x7f + kk) << 23);
-    float res = k == 0 ? y : scaled;
+    // y * 2^k as scalbnf computes it (k lies in [-150, 150]): its
+    // pre-scaling by 2^127 or 2^-102 is exact, so the one rounding is that of
+    // y * 2^k, which v_ldexp_f32 gives directly (denormals and overflow
+    // included; k = 0 leaves y)
+    float res = __builtin_amdgcn_ldexpf(y, k);
     res = ax <= 0x39000000u ? 1.0f + x : res;
     res = neg && ax >= 0x42cff1b5u ? 0.0f : res;
     res = !neg && ax >= 0x42b17218u ? x * 0x1p127f : res;
@@ -238,7 +237,7 @@ PK_DEV float pk_expf_le0(float x) {
     const float rr = r * r;
     const float c = r - rr * (p1 + rr * p2);
     const float y = 1.0f + (pk_expf_quot(r * c, 2.0f - c) - lo + hi);
-    const float res = k == 0 ? y : y * pk_float((unsigned)(0x7f + k) << 23);
+    const float res = __builtin_amdgcn_ldexpf(y, k);   // y * 2^k, k in [-126, 0]
     return ax <= 0x39000000u ? 1.0f + x : res;
 }
 
