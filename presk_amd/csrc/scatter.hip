@@ -8,11 +8,13 @@
 // collide), leaving 16K dependent steps per thread.
 //
 // Here one workgroup owns one table row v and 256 of its columns.  Its four
-// waves scan the indices together, 2048 tokens a round (eight coalesced loads
-// per lane in flight), and compact the positions of the tokens naming v into
-// an LDS list in token order (a ballot per 64 tokens, counts shared through
-// LDS).  Then each lane adds its column of those tokens' rows in list order
-// -- the nest's order, bit for bit -- with sixteen row loads in flight.  An
+// waves scan the indices together, 4096 tokens a round (sixteen coalesced
+// loads per lane in flight), and compact the positions of the tokens naming v
+// into an LDS list in token order (a ballot per 64 tokens, counts shared
+// through LDS).  Then each lane adds its column of those tokens' rows in list
+// order -- the nest's order, bit for bit -- the next 64 rows' loads in flight
+// while 64 are added (the rows lie anywhere in the cotangent, so each load
+// waits on HBM: 128 in flight a lane).  An
 // index outside [0, vocab) names no row here and is never added.
 #include <hip/hip_runtime.h>
 
@@ -24,9 +26,9 @@ namespace presk {
 namespace {
 
 constexpr int WAVES = 4;
-constexpr int PER = 8;                        // indices per lane per round
+constexpr int PER = 16;                       // indices per lane per round
 constexpr int ROUND = PER * WAVES * 64;       // tokens scanned per round
-constexpr int BATCH = 16;                     // row loads in flight
+constexpr int BATCH = 64;                     // row loads a batch, one list entry a lane (two batches in flight)
 
 template <int ST>
 __device__ __forceinline__ float ld(const void* p, long long i) {
@@ -83,20 +85,39 @@ __global__ void __launch_bounds__(WAVES * 64) embed_vjp_kernel(ScatterArgs a) {
         }
         total = before;
         __syncthreads();
-        if (live) {
-            for (int i0 = 0; i0 < total; i0 += BATCH) {
-                float x[BATCH];
-#pragma unroll
-                for (int q = 0; q < BATCH; ++q)
-                    x[q] = i0 + q < total ? ld<ST>(a.ct, (base + list[i0 + q]) * a.d + col) : 0.f;
+        // BATCH list entries at a time, one a lane (read once per wave, then
+        // handed out uniform by readlane: no LDS wait per row); the next
+        // batch's row loads in flight while this one is added.  Entries past
+        // the list repeat its last and are not added; a column past the row
+        // loads a live one and is never stored -- no lane diverges.
+        {
+            const long long colc = live ? col : a.d - 1;
+            float xa[BATCH], xb[BATCH];
+            auto fetch = [&](float (&x)[BATCH], int i0) {
+                const int n = total - i0 < BATCH ? total - i0 : BATCH;
+                const int mine = list[i0 + (lane < n ? lane : n - 1)];
 #pragma unroll
                 for (int q = 0; q < BATCH; ++q) {
-                    if (i0 + q < total) {
-                        const float s = acc + x[q];
-                        if (ST == 2) ovf |= pk_overflows_f16(s);
-                        acc = stored<ST>(s);
-                    }
+                    const long long t = base + __builtin_amdgcn_readlane(mine, q);
+                    x[q] = ld<ST>(a.ct, t * a.d + colc);
                 }
+            };
+            auto add = [&](const float (&x)[BATCH], int i0) {
+                const int n = total - i0 < BATCH ? total - i0 : BATCH;
+#pragma unroll
+                for (int q = 0; q < BATCH; ++q) {
+                    const float s = acc + x[q];
+                    if (ST == 2) ovf |= q < n && pk_overflows_f16(s);
+                    acc = q < n ? stored<ST>(s) : acc;
+                }
+            };
+            if (total > 0) fetch(xa, 0);
+            for (int i0 = 0; i0 < total; i0 += 2 * BATCH) {
+                if (i0 + BATCH < total) fetch(xb, i0 + BATCH);
+                add(xa, i0);
+                if (i0 + BATCH >= total) break;
+                if (i0 + 2 * BATCH < total) fetch(xa, i0 + 2 * BATCH);
+                add(xb, i0 + BATCH);
             }
         }
         __syncthreads();  // the list is rewritten next round

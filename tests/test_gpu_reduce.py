@@ -129,9 +129,10 @@ def test_rows_class_exact_at_size(dt):
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("ids", ["spread", "one_row"])
 def test_scatter_class_exact_at_size(dt, ids):
-    """embed_vjp over 4500 tokens (three scan rounds of 2048) into a 7 x 300
-    table (a partial column block); with every token naming one row, a round's
-    whole list is that row's."""
+    """embed_vjp over 4500 tokens (two scan rounds of 4096, the second
+    partial) into a 7 x 300 table (a partial column block); with every token
+    naming one row, a round's whole list is that row's (32 double batches of
+    64 row loads, then a ragged 404)."""
     B, T, V, D = 3, 1500, 7, 300
     tok = O(A(("vocab", V), ("model", D)))
     idx = O(A(("batch", B), ("seq", T)), "idx")
