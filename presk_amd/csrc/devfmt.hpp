@@ -60,28 +60,31 @@ PK_DEV float pk_float(unsigned b) { return __builtin_bit_cast(float, b); }
 PK_DEV float pk_bf16_to_f32(unsigned short h) { return pk_float((unsigned)h << 16); }
 // Round to nearest even; a NaN keeps its sign and top payload bits and is
 // quieted (bit 6 set).  gfx950's v_cvt_pk_bf16_f32 computes exactly this,
-// denormals included (pinned by the all-f32 digest of the conversion), in
-// one instruction for two values, against six for the integer form
-// (b + 0x7fff + ((b >> 16) & 1)) >> 16 with a select for a NaN.
-PK_DEV unsigned short pk_f32_to_bf16(float x) { return __builtin_bit_cast(unsigned short, (__bf16)x); }
+// denormals included (pinned by the all-f32 digest of the conversion): one
+// instruction against six for the integer form (b + 0x7fff + ((b >> 16) &
+// 1)) >> 16 with a select for a NaN.  Written as assembly so that the
+// compiler cannot fold the rounding into the operation that produced x (a
+// product and its rounding to 16 bits as one mixed-precision FMA rounds
+// once where the interpreter rounds twice).
+PK_DEV unsigned short pk_f32_to_bf16(float x) {
+    unsigned r;
+    asm("v_cvt_pk_bf16_f32 %0, %1, 0" : "=v"(r) : "v"(x));
+    return (unsigned short)r;
+}
 
 // ---- binary16 -----------------------------------------------------------------
-PK_DEV float pk_f16_to_f32(unsigned short c) {
-    const unsigned sign = (unsigned)(c & 0x8000u) << 16, field = (c >> 10) & 0x1fu, frac = c & 0x3ffu;
-    const unsigned special = frac == 0 ? 0x7f800000u : (0x7fc00000u | (frac << 13));
-    const unsigned sub = pk_bits((float)frac * 5.9604644775390625e-8f);   // frac * 2^-24, exact
-    const unsigned normal = ((field + 112u) << 23) | (frac << 13);
-    return pk_float(sign | (field == 0x1fu ? special : field == 0 ? sub : normal));
-}
+// Exact; a NaN is quieted with its payload kept (v_cvt_f32_f16: pinned by the
+// digest over every code)
+PK_DEV float pk_f16_to_f32(unsigned short c) { return (float)__builtin_bit_cast(_Float16, c); }
+// Round to nearest even, overflow to infinity, subnormals kept; a NaN keeps
+// its sign and top payload bits and is quieted.  v_cvt_f16_f32 computes
+// exactly this (pinned by the all-f32 digest of the conversion); assembly,
+// as for bf16, so that no product is rounded to binary16 in one step by a
+// mixed-precision FMA (v_fma_mixlo_f16), which the interpreter rounds twice.
 PK_DEV unsigned short pk_f32_to_f16(float x) {
-    const unsigned b = pk_bits(x), sign = (b >> 16) & 0x8000u, a = b & 0x7fffffffu;
-    const unsigned nan = 0x7e00u | ((a >> 13) & 0x1ffu);                  // NaN, quiet
-    const unsigned r = a - 0x38000000u;                                   // normal binary16: rebias 127 -> 15
-    const unsigned normal = (r + 0xfffu + ((r >> 13) & 1u)) >> 13;
-    // subnormal or zero: |x| / 2^-24 rounded to even (computed on 0 otherwise)
-    const unsigned sub = (unsigned)__builtin_rintf(pk_float(a < 0x38800000u ? a : 0u) * 16777216.0f);
-    const unsigned code = a > 0x7f800000u ? nan : a >= 0x477ff000u ? 0x7c00u : a >= 0x38800000u ? normal : sub;
-    return (unsigned short)(sign | code);
+    unsigned r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(x));
+    return (unsigned short)r;
 }
 PK_DEV bool pk_overflows_f16(float x) {
     unsigned a = pk_bits(x) & 0x7fffffffu;
@@ -364,7 +367,12 @@ PK_DEV float pk_erf_mid(float x) {
 PK_DEV float pk_erfc_tail(unsigned ax, float x) {
     if (ax < 0x3fa00000u) return pk_erf_mid(x);
     x = __builtin_fabsf(x);
-    const float s = 1.0f / (x * x);
+    // the quotients by the refined-reciprocal step (their operands lie in
+    // the normal range here: x^2 in [1.56, 36], q >= 1, the product of the
+    // exponentials above 2^-60), the first exponential's argument in
+    // (-37, -2] (expf's fast path): erff's bits on every f32, pinned by its
+    // all-f32 digest
+    const float s = pk_erf_quot(1.0f, x * x);
     float r, q;
     if (ax < 0x4036db6du) {
         r = -9.8649440333e-03f + s * (-6.9385856390e-01f + s * (-1.0558626175e+01f + s * (-6.2375331879e+01f +
@@ -378,7 +386,7 @@ PK_DEV float pk_erfc_tail(unsigned ax, float x) {
             s * (2.5530502930e+03f + s * (4.7452853394e+02f + s * -2.2440952301e+01f))))));
     }
     const float z = pk_float(pk_bits(x) & 0xffffe000u);
-    return pk_expf(-z * z - 0.5625f) * pk_expf((z - x) * (z + x) + r / q) / x;
+    return pk_erf_quot(pk_expf_le0(-z * z - 0.5625f) * pk_expf((z - x) * (z + x) + pk_erf_quot(r, q)), x);
 }
 
 PK_DEV float pk_erff(float x) {
