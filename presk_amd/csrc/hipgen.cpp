@@ -674,11 +674,17 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
         // stores of the unrolled iterations merge into 16-byte accesses.
         // The iterations are independent, so running them in one thread in
         // order changes nothing.
+        // A nest too small to fill the CUs a thread an iteration (under 64 K
+        // iterations a VEC, e.g. RoPE's sin and cos over 2 048 x 64) is
+        // latency-bound, not bandwidth-bound: it keeps a thread an iteration.
         int vec = 1;
         if (!loops.empty() && serial.empty() && !(loops.size() == 1 && ph.split)) {
             const int want = k.output.ty == Ty::F32 ? 4 : (k.output.ty == Ty::BF16 || k.output.ty == Ty::F16) ? 8 : 1;
             const Stmt* inner = loops.back();
-            if (want > 1 && inner->bound % want == 0 && output_unit_stride(k, *level, inner->var)) vec = want;
+            double iters = 1;
+            for (auto l : loops) iters *= (double)l->bound;
+            if (want > 1 && iters >= 65536.0 * want && inner->bound % want == 0 && output_unit_stride(k, *level, inner->var))
+                vec = want;
         }
         for (auto l : loops) ph.bounds.push_back(l->bound);
         if (vec > 1) ph.bounds.back() /= vec;

@@ -74,3 +74,34 @@ def test_overflow_guard(ex, dt):
     _, flag = cexec.run(low.text, dt, ins)
     assert not flag
     ex.run(low.text, dt, [hip.DeviceBuffer.of(a) for a in ins], hip.DeviceBuffer(4 * 8 * hip.STORAGE_BYTES[dt]))
+
+
+def _wide_cases():
+    """Elementwise nests of 2 048 x 512 (a million iterations: the printer's
+    16-byte form, each thread VEC consecutive outputs; smaller nests keep a
+    thread an iteration): a unary, a broadcast binary and the LayerNorm tail's
+    six-step chain."""
+    from presk_amd import lower as L
+    A, O = L.ax, L.Operand
+    x = O(A(("batch", 8), ("seq", 256), ("model", 512)))
+    r = O(A(("batch", 8), ("seq", 256)))
+    b = O(A(("model", 512)))
+    for dt in ("f32", "bf16", "f16"):
+        yield f"gelu-{dt}", L.unary("gelu", [x], dt)
+        yield f"sub-{dt}", L.elementwise_binary("sub", [x, r], dt)
+        yield f"layernorm_tail-{dt}", L.fused(
+            [("sub", [("in", 0), ("in", 1)]), ("add", [("in", 2), ("in", 3)]), ("sqrt", [("step", 1)]),
+             ("div", [("step", 0), ("step", 2)]), ("mul", [("step", 3), ("in", 4)]), ("add", [("step", 4), ("in", 5)])],
+            [x, r, r, O([]), b, b], x.axes, dt)
+
+
+@pytest.mark.parametrize("case", list(_wide_cases()), ids=lambda c: c[0])
+def test_exact_bits_vectorized(ex, case):
+    name, low = case
+    print(f"[parity] wide {name}", flush=True)
+    ins = zoo.inputs(low, seed=4)
+    want, want_flag = cexec.run(low.text, low.dtype, ins, lanes=low.lanes, threads=8)
+    got, got_flag = run_device(ex, low, ins)
+    assert got_flag == want_flag
+    w = want.view(np.uint8)
+    assert got.tobytes() == w.tobytes(), f"{name}: {np.count_nonzero(got != w)} bytes differ"
