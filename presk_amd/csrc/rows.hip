@@ -359,6 +359,31 @@ __global__ void __launch_bounds__(256) pack_mask_kernel(const long long* mask, u
     if (lane < 2) bits[r * words + c0 / 32 + lane] = (unsigned)(lane == 0 ? b : b >> 32);
 }
 
+// The same bits a byte a thread: eight columns from four 16-byte loads (a
+// wave reads 4 KB of the mask at once, against 512 bytes above), for rows of
+// a multiple of 8 columns on a 16-byte-aligned mask.  Byte k of word w holds
+// columns 32 w + 8 k .. + 7 (little-endian), as the ballot form lays them;
+// columns past the row are zeros.
+__global__ void __launch_bounds__(256) pack_mask8_kernel(const long long* mask, unsigned char* bytes, long long n,
+                                                         long long row_bytes) {
+    typedef long long ll2 __attribute__((ext_vector_type(2)));
+    const long long r = blockIdx.y;
+    const long long byte = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (byte >= row_bytes) return;
+    const long long c = 8 * byte;
+    unsigned v = 0;
+    if (c < n) {   // n % 8 == 0: the eight columns lie in the row
+        const ll2* p = (const ll2*)(mask + r * n + c);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const ll2 w = p[q];
+            v |= (w.x > 0 ? 1u : 0u) << (2 * q);
+            v |= (w.y > 0 ? 1u : 0u) << (2 * q + 1);
+        }
+    }
+    bytes[r * row_bytes + byte] = (unsigned char)v;
+}
+
 template <int ST>
 struct Raw {
     // storage elements per 16-byte vector
@@ -1032,8 +1057,13 @@ hipError_t launch_walk(const RowArgs& a, hipStream_t stream) {
     if (OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2) {
         if (!a.mbits) return hipErrorInvalidValue;
         const long long words = mask_words(a.n);
-        const dim3 grid((unsigned)((a.n + 255) / 256), (unsigned)a.mask_rows);
-        pack_mask_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, a.mbits, a.n, words);
+        if (a.n % 8 == 0 && (uintptr_t)a.mask % 16 == 0) {
+            const dim3 grid((unsigned)((words * 4 + 255) / 256), (unsigned)a.mask_rows);
+            pack_mask8_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, (unsigned char*)a.mbits, a.n, words * 4);
+        } else {
+            const dim3 grid((unsigned)((a.n + 255) / 256), (unsigned)a.mask_rows);
+            pack_mask_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, a.mbits, a.n, words);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
