@@ -391,17 +391,19 @@ struct Raw {
 };
 
 template <int OP, int ST, int R, int VEC>
-__global__ void __launch_bounds__(64) rows_walk_kernel(RowArgs a) {
+__global__ void __launch_bounds__(128) rows_walk_kernel(RowArgs a) {
     constexpr int CW = WE / R, TS = CW + 4;     // TS = 4 (mod 32): a b128 walk read is conflict-free
     constexpr int NV = WE / 64 / VEC;            // vectors per lane per chunk
     constexpr int ESZ = ST == 0 ? 4 : 2;
     static_assert(CW % 64 == 0 && CW % VEC == 0, "chunk geometry");
-    __shared__ __attribute__((aligned(16))) float tile[R * TS];
-    const int lane = threadIdx.x;
+    // two waves: wave 1 loads and converts the chunks into one of two tiles
+    // while wave 0's lanes walk the other
+    __shared__ __attribute__((aligned(16))) float tiles[2][R * TS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long long row0 = (long long)blockIdx.x * R;
     const long long n = a.n;
     const int nr = (int)(a.rows - row0 < R ? a.rows - row0 : R);
-    const bool walker = lane < nr;
+    const bool walker = wave == 0 && lane < nr;
     bool ovf = false;
     const long long nch = (n + CW - 1) / CW;
     using W = unsigned __attribute__((ext_vector_type(VEC * ESZ / 4 > 0 ? VEC * ESZ / 4 : 1)));
@@ -428,7 +430,7 @@ __global__ void __launch_bounds__(64) rows_walk_kernel(RowArgs a) {
             else hv[q] = ((const H*)a.x)[off];
         }
     };
-    auto put = [&]() {
+    auto put = [&](float* tile) {
 #pragma unroll
         for (int q = 0; q < NV; ++q) {
             int row, col;
@@ -452,17 +454,24 @@ __global__ void __launch_bounds__(64) rows_walk_kernel(RowArgs a) {
             for (int u = 0; u < VEC; ++u) tile[row * TS + col + u] = f[u];
         }
     };
-    // the row in index order: visit(x) in the walking lane
+    // the row in index order: visit(x) in the walking lane.  Wave 1 puts
+    // chunk ch + 1 (loaded a step earlier) into the other tile and starts
+    // chunk ch + 2's loads while wave 0 walks chunk ch; a barrier a step.
+    auto width = [&](long long ch) { return (int)(n - ch * CW < CW ? n - ch * CW : CW); };
     auto pass = [&](auto&& visit) {
-        int cw = (int)(n < CW ? n : CW);
-        fetch(0, cw);
+        if (wave == 1) {
+            fetch(0, width(0));
+            put(tiles[0]);
+            if (nch > 1) fetch(CW, width(1));
+        }
+        __syncthreads();
         for (long long ch = 0; ch < nch; ++ch) {
-            const long long c0 = ch * CW;
-            cw = (int)(n - c0 < CW ? n - c0 : CW);
-            __syncthreads();
-            put();
-            __syncthreads();
-            if (ch + 1 < nch) fetch(c0 + CW, (int)(n - c0 - CW < CW ? n - c0 - CW : CW));
+            const int cw = width(ch);
+            const float* const tile = tiles[ch & 1];
+            if (wave == 1 && ch + 1 < nch) {
+                put(tiles[(ch + 1) & 1]);
+                if (ch + 2 < nch) fetch((ch + 2) * CW, width(ch + 2));
+            }
             if (walker && cw == CW) {
                 const float* t = &tile[lane * TS];
                 if constexpr (OP == kRowMean || OP == kRowSum || (OP == kSumToRows && ST == 0)) {
@@ -514,6 +523,7 @@ __global__ void __launch_bounds__(64) rows_walk_kernel(RowArgs a) {
                 }
                 for (; j < cw; ++j) visit(t[j]);
             }
+            __syncthreads();   // this tile walked, the other filled
         }
     };
     const long long r = row0 + lane;
@@ -539,8 +549,8 @@ hipError_t launch_walk_v(const RowArgs& a, hipStream_t stream) {
     const unsigned grid = (unsigned)((a.rows + R - 1) / R);
     const int esz = ST == 0 ? 4 : 2;
     const bool vec = (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.out % 16 == 0 && (a.n * esz) % 16 == 0;
-    if (vec) rows_walk_kernel<OP, ST, R, V><<<grid, 64, 0, stream>>>(a);
-    else rows_walk_kernel<OP, ST, R, 1><<<grid, 64, 0, stream>>>(a);
+    if (vec) rows_walk_kernel<OP, ST, R, V><<<grid, 128, 0, stream>>>(a);
+    else rows_walk_kernel<OP, ST, R, 1><<<grid, 128, 0, stream>>>(a);
     return hipGetLastError();
 }
 
