@@ -208,6 +208,14 @@ int presk_hip_batch_add_convert(presk_hip_batch *b, const void *src, const char 
 int presk_hip_batch_add_dropout(presk_hip_batch *b, const void *key, double rate, const char *type, int64_t n,
                                 void *dst);
 int presk_hip_batch_graph(presk_hip_batch *b);
+/* presk_hip_batch_graph with independent steps on up to `branches` (1-8)
+ * parallel branches of the graph: a step follows every earlier step that
+ * writes bytes it reads or writes, or reads bytes it writes (the overflow
+ * flag aside: its stores commute), and every earlier launch of the same
+ * compiled kernel (one workspace a kernel).  1 is presk_hip_batch_graph.
+ * More than one branch is switched off in this build (E10001): a branched
+ * capture ended in a host segmentation fault whose cause is not found. */
+int presk_hip_batch_graph_branches(presk_hip_batch *b, int branches);
 int presk_hip_batch_run(presk_hip_batch *b, void *stream);
 void presk_hip_batch_release(presk_hip_batch *b);
 

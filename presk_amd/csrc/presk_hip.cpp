@@ -514,24 +514,119 @@ struct presk_hip_batch {
         exec = nullptr;
         graph = nullptr;
     }
-    int run_each(hipStream_t s) const {
-        for (const Item& it : items) {
-            if (!it.k && it.rate >= 0.0) {
-                hipError_t e = dropout_launch(it.bufs[0], it.rate, it.to, it.n, it.bufs[1], s);
-                if (e != hipSuccess) return hip_fail(e, "dropout mask");
-                continue;
-            }
-            if (!it.k) {
-                hipError_t e = convert_launch(it.bufs[0], it.from, it.bufs[1], it.to, it.n, (unsigned*)it.bufs[2], s);
-                if (e != hipSuccess) return hip_fail(e, "edge conversion");
-                continue;
-            }
-            if (int rc = presk_hip_run(it.k, it.bufs.data(), it.lo, it.hi, s)) return rc;
+    static int run_one(const Item& it, hipStream_t s) {
+        if (!it.k && it.rate >= 0.0) {
+            hipError_t e = dropout_launch(it.bufs[0], it.rate, it.to, it.n, it.bufs[1], s);
+            return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "dropout mask");
         }
+        if (!it.k) {
+            hipError_t e = convert_launch(it.bufs[0], it.from, it.bufs[1], it.to, it.n, (unsigned*)it.bufs[2], s);
+            return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "edge conversion");
+        }
+        return presk_hip_run(it.k, it.bufs.data(), it.lo, it.hi, s);
+    }
+    int run_each(hipStream_t s) const {
+        for (const Item& it : items)
+            if (int rc = run_one(it, s)) return rc;
         return PRESK_HIP_OK;
     }
     ~presk_hip_batch() { drop_graph(); }
 };
+
+namespace {
+
+constexpr int kMaxBranches = 8;
+constexpr bool kBranchesOn = false;
+
+// The byte ranges a step reads and writes.  The overflow flag is left out:
+// every store into it writes the same nonzero word and only the host reads
+// it, after the sequence, so steps that share it commute.
+struct Span {
+    uintptr_t lo, hi;
+};
+
+size_t spec_bytes(const BufSpec& s) {
+    return s.ty == Ty::Q4 ? (size_t)((s.numel() + 1) / 2) : (size_t)s.numel() * (size_t)ty_bytes(s.ty);
+}
+
+size_t code_bytes(int t) { return t == 0 ? 8 : t == 1 ? 4 : t == 5 ? 3 : 2; }
+
+void step_spans(const presk_hip_batch::Item& it, std::vector<Span>* rd, std::vector<Span>* wr) {
+    auto add = [](std::vector<Span>* v, const void* p, size_t bytes) {
+        if (p && bytes) v->push_back({(uintptr_t)p, (uintptr_t)p + bytes});
+    };
+    if (it.k) {
+        const Kernel& k = *it.k->k;
+        for (int b = 0; b < k.out_buf(); ++b) {
+            add(rd, it.bufs[b], spec_bytes(k.inputs[b]));
+            const int s = k.scale_slot(b);
+            if (s >= 0) add(rd, it.bufs[s], (size_t)k.inputs[b].scale_count() * sizeof(float));
+        }
+        add(wr, it.bufs[k.out_buf()], spec_bytes(k.output));
+    } else if (it.rate >= 0.0) {
+        add(rd, it.bufs[0], 32);   // the ChaCha20 key
+        add(wr, it.bufs[1], (size_t)it.n * code_bytes(it.to));
+    } else {
+        add(rd, it.bufs[0], (size_t)it.n * code_bytes(it.from));
+        add(wr, it.bufs[1], (size_t)it.n * code_bytes(it.to));
+    }
+}
+
+bool meet(const std::vector<Span>& a, const std::vector<Span>& b) {
+    for (const Span& x : a)
+        for (const Span& y : b)
+            if (x.lo < y.hi && y.lo < x.hi) return true;
+    return false;
+}
+
+// Streams for a branched capture of the sequence.  Step j depends on an
+// earlier step i when one writes bytes the other reads or writes, or when
+// both launch the same compiled kernel (its workspace is one per handle).
+// Each step goes on the stream whose last step it depends on (no wait), else
+// on an idle stream, else behind the oldest stream's last step; it then waits
+// for the latest step it depends on on each other stream, unless that stream
+// is already known to be done up to there.  One stream: program order.
+void plan_branches(const presk_hip_batch& b, int branches, std::vector<int>* lane,
+                   std::vector<std::vector<std::pair<int, int>>>* waits) {
+    const int n = (int)b.items.size();
+    lane->assign(n, 0);
+    waits->assign(n, {});
+    if (branches <= 1) return;
+    std::vector<std::vector<Span>> rd(n), wr(n);
+    for (int i = 0; i < n; ++i) step_spans(b.items[i], &rd[i], &wr[i]);
+    std::vector<int> last(branches, -1);                                  // each stream's last step
+    std::vector<std::vector<int>> known(branches, std::vector<int>(branches, -1));   // known[s][t]: t done up to this step before s's end
+    for (int j = 0; j < n; ++j) {
+        std::vector<int> dep(branches, -1);   // the latest step j depends on, per stream
+        for (int i = j - 1; i >= 0; --i) {
+            const int t = (*lane)[i];
+            if (dep[t] >= i) continue;
+            const bool same = b.items[i].k && b.items[i].k == b.items[j].k;
+            if (same || meet(wr[i], rd[j]) || meet(wr[i], wr[j]) || meet(rd[i], wr[j])) dep[t] = i;
+        }
+        int s = -1;
+        for (int t = 0; t < branches; ++t)   // continue the chain of the latest dependency
+            if (last[t] >= 0 && last[t] == dep[t] && (s < 0 || dep[t] > dep[s])) s = t;
+        if (s < 0)
+            for (int t = 0; t < branches && s < 0; ++t)
+                if (last[t] < 0) s = t;
+        if (s < 0) {
+            s = 0;
+            for (int t = 1; t < branches; ++t)
+                if (last[t] < last[s]) s = t;
+        }
+        (*lane)[j] = s;
+        for (int t = 0; t < branches; ++t) {
+            if (t == s || dep[t] < 0 || known[s][t] >= dep[t]) continue;
+            (*waits)[j].push_back({t, dep[t]});
+            known[s][t] = dep[t];
+        }
+        last[s] = j;
+        known[s][s] = j;
+    }
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -596,28 +691,81 @@ int presk_hip_batch_add_convert(presk_hip_batch* b, const void* src, const char*
     return PRESK_HIP_OK;
 }
 
-int presk_hip_batch_graph(presk_hip_batch* b) {
+int presk_hip_batch_graph(presk_hip_batch* b) { return presk_hip_batch_graph_branches(b, 1); }
+
+int presk_hip_batch_graph_branches(presk_hip_batch* b, int branches) {
     if (!b) return fail(PRESK_HIP_ERR, "E10001: null argument");
+    if (branches < 1 || branches > kMaxBranches)
+        return fail(PRESK_HIP_ERR, "E10001: branches " + std::to_string(branches) + " not in 1.." + std::to_string(kMaxBranches));
+    // switched off: the one branched capture run on the device (the course
+    // step, four branches) ended in a host segmentation fault inside this
+    // call whose cause is not found; one branch is the tested sequence
+    if (branches > 1 && !kBranchesOn)
+        return fail(PRESK_HIP_ERR, "E10001: parallel graph branches are switched off in this build; use 1");
     b->drop_graph();
     for (const auto& it : b->items)
         if (it.k)
             if (int rc = prepare_kernel(it.k)) return rc;
-    hipStream_t cs = nullptr;
-    hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
-    if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
-    e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    const int n = (int)b->items.size();
+    std::vector<int> lane;       // each step's capture stream
+    std::vector<std::vector<std::pair<int, int>>> waits;   // (stream, step) events each step waits for
+    plan_branches(*b, branches, &lane, &waits);
+    int used = 1;
+    for (int s : lane) used = std::max(used, s + 1);
+    std::vector<hipStream_t> cs(used, nullptr);
+    std::vector<hipEvent_t> ev;   // one a step when there are branches, then the fork
+    hipError_t e = hipSuccess;
+    auto cleanup = [&]() {
+        for (hipEvent_t x : ev)
+            if (x) hipEventDestroy(x);
+        for (hipStream_t s : cs)
+            if (s) hipStreamDestroy(s);
+    };
+    for (int s = 0; s < used && e == hipSuccess; ++s) e = hipStreamCreateWithFlags(&cs[s], hipStreamNonBlocking);
+    if (used > 1)
+        for (int i = 0; i <= n && e == hipSuccess; ++i) {
+            ev.push_back(nullptr);
+            e = hipEventCreateWithFlags(&ev.back(), hipEventDisableTiming);
+        }
     if (e != hipSuccess) {
-        hipStreamDestroy(cs);
+        cleanup();
+        return hip_fail(e, "graph streams and events");
+    }
+    e = hipStreamBeginCapture(cs[0], hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        cleanup();
         return hip_fail(e, "hipStreamBeginCapture");
     }
-    const int rc = b->run_each(cs);
-    hipGraph_t g = nullptr;
-    e = hipStreamEndCapture(cs, &g);  // ended whatever the launches returned
-    hipStreamDestroy(cs);
-    if (rc) {
-        if (g) hipGraphDestroy(g);
-        return rc;
+    int rc = PRESK_HIP_OK;
+    if (used == 1) {
+        rc = b->run_each(cs[0]);
+    } else {
+        // the other streams join the capture from the first one, then each
+        // step waits for the last step of every other stream it depends on,
+        // runs, and marks its end; the first stream finally waits for all
+        e = hipEventRecord(ev[n], cs[0]);
+        for (int s = 1; s < used && e == hipSuccess; ++s) e = hipStreamWaitEvent(cs[s], ev[n], 0);
+        for (int i = 0; i < n && e == hipSuccess && !rc; ++i) {
+            hipStream_t s = cs[lane[i]];
+            for (const auto& w : waits[i])
+                if (e == hipSuccess) e = hipStreamWaitEvent(s, ev[w.second], 0);
+            if (e != hipSuccess) break;
+            rc = b->run_one(b->items[i], s);
+            if (!rc) e = hipEventRecord(ev[i], s);
+        }
+        for (int s = 1; s < used && e == hipSuccess && !rc; ++s) {
+            e = hipEventRecord(ev[n], cs[s]);
+            if (e == hipSuccess) e = hipStreamWaitEvent(cs[0], ev[n], 0);
+        }
     }
+    hipGraph_t g = nullptr;
+    const hipError_t ee = hipStreamEndCapture(cs[0], &g);  // ended whatever the launches returned
+    cleanup();
+    if (rc || e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return rc ? rc : hip_fail(e, "branched capture");
+    }
+    e = ee;
     if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
     hipGraphExec_t x = nullptr;
     e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);

@@ -25,7 +25,7 @@ SYMBOLS = ["presk_hip_init", "presk_hip_last_error", "presk_hip_compile", "presk
            "presk_hip_kernel_info",
            "presk_hip_release", "presk_hip_kernel_text", "presk_hip_alloc", "presk_hip_free", "presk_hip_h2d", "presk_hip_d2h", "presk_hip_memset",
            "presk_hip_sync", "presk_hip_stream_create", "presk_hip_stream_destroy", "presk_hip_time",
-           "presk_hip_scalar_digest", "presk_hip_batch_create", "presk_hip_batch_add", "presk_hip_batch_graph",
+           "presk_hip_scalar_digest", "presk_hip_batch_create", "presk_hip_batch_add", "presk_hip_batch_graph", "presk_hip_batch_graph_branches",
            "presk_hip_batch_run", "presk_hip_batch_release", "presk_hip_convert", "presk_hip_batch_add_convert",
            "presk_hip_fill_normal", "presk_hip_dropout_mask", "presk_hip_batch_add_dropout",
            "presk_hip_pskd_decode", "presk_hip_pskd_decode_idx"]
@@ -81,6 +81,7 @@ def lib():
         L.presk_hip_batch_create.argtypes = [ctypes.POINTER(vp)]
         L.presk_hip_batch_add.argtypes = [vp, vp, ctypes.POINTER(vp), i64, i64]
         L.presk_hip_batch_graph.argtypes = [vp]
+        L.presk_hip_batch_graph_branches.argtypes = [vp, i32]
         L.presk_hip_batch_run.argtypes = [vp, vp]
         L.presk_hip_batch_release.argtypes = [vp]
         L.presk_hip_batch_release.restype = None

@@ -226,9 +226,10 @@ class Program:
         hip.check(hip.lib().presk_hip_convert(self.bufs.dev[src].ptr, frm.encode(), self.bufs.dev[dst].ptr, to.encode(),
                                               n, self._flag.ptr, stream))
 
-    def record(self, graph: bool = True):
+    def record(self, graph: bool = True, branches: int = 1):
         """Hands the prepared launch sequence to the executor: `run` then
-        issues it from one C call, and with `graph` as one HIP graph launch."""
+        issues it from one C call, and with `graph` as one HIP graph launch
+        whose independent launches lie on up to `branches` parallel branches."""
         lib = hip.lib()
         self.release_batch()
         b = ctypes.c_void_p()
@@ -248,7 +249,7 @@ class Program:
             c = st[1].compiled
             hip.check(lib.presk_hip_batch_add(b, c.handle, st[1].table, 0, max(c.split_bound, 0)))
         if graph:
-            hip.check(lib.presk_hip_batch_graph(b))
+            hip.check(lib.presk_hip_batch_graph_branches(b, branches))
         return self
 
     def release_batch(self):

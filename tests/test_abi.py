@@ -79,3 +79,19 @@ def test_noalloc_refuses_before_touching_the_device():
     assert cg.kind == "generic"
     rc = hip.lib().presk_hip_run_noalloc(cg.handle, (ctypes.c_void_p * 2)(None, None), 0, 4, None)
     assert rc == hip.ERR and "no code object loaded" in hip.lib().presk_hip_last_error().decode()
+
+
+def test_graph_branches_checked_before_any_device_work():
+    """presk_hip_batch_graph_branches takes 1-8 branches, and more than one is
+    refused in this build (E10001), before any capture."""
+    import ctypes
+    L = hip.lib()
+    b = ctypes.c_void_p()
+    assert L.presk_hip_batch_create(ctypes.byref(b)) == hip.OK
+    try:
+        for n, text in ((0, "not in 1..8"), (9, "not in 1..8"), (4, "switched off")):
+            assert L.presk_hip_batch_graph_branches(b, n) == hip.ERR
+            msg = L.presk_hip_last_error().decode()
+            assert msg.startswith("E10001") and text in msg, msg
+    finally:
+        L.presk_hip_batch_release(b)
