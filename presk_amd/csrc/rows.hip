@@ -921,12 +921,14 @@ __global__ void __launch_bounds__(64) softmax_short_kernel(RowArgs a) {
         return (mrow[q][col >> 5] >> (col & 31)) & live;
     };
 
-    // 1. the max (as the streamed kernel: lane partials joined over the row)
+    // 1. the max (as the streamed kernel: lane partials joined over the row),
+    //    the first allowed element's value joined beside its column (no
+    //    second read of x, whose latency nothing here would hide)
     const int BIG = 0x7fffffff;
     float mq[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-        float m = -__builtin_inff();
+        float m = -__builtin_inff(), fv = 0.f;
         int f = BIG;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -935,17 +937,19 @@ __global__ void __launch_bounds__(64) softmax_short_kernel(RowArgs a) {
             for (int u = 0; u < VEC; ++u) {
                 const bool ok = ((al >> u) & 1u) != 0;
                 m = ok && v[c][q][u] > m ? v[c][q][u] : m;
-                f = ok && f == BIG ? c * SCW + lc + u : f;
+                const bool first = ok && f == BIG;
+                fv = first ? v[c][q][u] : fv;
+                f = first ? c * SCW + lc + u : f;
             }
         }
         for (int off = LPR / 2; off > 0; off >>= 1) {
-            const float o = __shfl_xor(m, off, 64);
+            const float o = __shfl_xor(m, off, 64), ov = __shfl_xor(fv, off, 64);
             const int g = __shfl_xor(f, off, 64);
             m = o > m ? o : m;
+            fv = g < f ? ov : fv;
             f = g < f ? g : f;
         }
-        const float first = f == BIG ? 0.f : ld<ST>(a.x, (row0 + myrow[q]) * n + f);
-        mq[q] = f == BIG ? 0.f : first != first ? first : m;
+        mq[q] = f == BIG ? 0.f : fv != fv ? fv : m;
     }
 
     // 2. the exponentials, in place; z by lane i walking row i through the tile
