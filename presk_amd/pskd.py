@@ -30,7 +30,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import hip, keys
+from . import hip
 
 MAGIC = b"PSKD"
 VERSION, VERSION_ENCODED, VERSION_FORMATS = 1, 2, 3
@@ -615,37 +615,3 @@ def write(path: str, sample_ty: str, layout: Layout, samples: list, encs: list |
         f.write(out)
     return len(samples)
 
-
-# ---- the training data pipeline (lib.rs:860-905) ----------------------------------
-
-def shuffle_indices(n: int, seed: int, epoch: int) -> list:
-    """shuffle_indices (lib.rs:889-902): ChaCha20Rng::seed_from_u64(seed)
-    fills a 32-byte key max(epoch, 1) times (consecutive stream bytes), and
-    ChaCha20Rng::from_seed(that key) draws next_u64 (stream bytes 8k..8k+8,
-    little-endian) for a Fisher-Yates shuffle from the end, j = draw % (i + 1)."""
-    key = keys.stream(keys.seed_key(seed), 32 * max(epoch, 1))[-32:]
-    v = list(range(n))
-    draws = keys.stream(key, 8 * max(n - 1, 0))
-    for k, i in enumerate(range(n - 1, 0, -1)):
-        j = struct.unpack_from("<Q", draws, 8 * k)[0] % (i + 1)
-        v[i], v[j] = v[j], v[i]
-    return v
-
-
-@dataclass
-class Pipeline:
-    """Pipeline (lib.rs:860-887): whole batches of `batch` sample indices,
-    shuffled per epoch when a seed is given, at most `take` of them."""
-    shuffle: int | None
-    batch: int
-    take: int | None = None
-
-    def batches(self, count: int, epoch: int) -> list:
-        order = shuffle_indices(count, self.shuffle, epoch) if self.shuffle is not None else list(range(count))
-        b = max(self.batch, 1)
-        out = [order[i:i + b] for i in range(0, len(order) - b + 1, b)]
-        return out[:self.take] if self.take is not None else out
-
-    def batches_per_epoch(self, count: int) -> int:
-        n = count // max(self.batch, 1)
-        return min(n, self.take) if self.take is not None else n

@@ -1,8 +1,8 @@
 """The .psk.d container's host logic (presk_amd/pskd.py) on the reference's
 own cases (crates/presk-data/tests/data.rs) and data files: layouts from
 types, idx widths, the headers of versions 1-3 and their byte counts, values
-refused at write time, malformed files, `params` files that need the
-program's layout, and the data pipeline.  Leaf values are read back with the
+refused at write time, malformed files, and `params` files that need the
+program's layout.  Leaf values are read back with the
 oracle's decode (the device path is tests/test_gpu_pskd.py).
 
 Data files (tests/golden/pskd/) are the reference's examples, copied as data:
@@ -192,16 +192,3 @@ def test_params_files_need_a_layout(tmp_path, oracle_lib):
     small = Layout.record([("w", Leaf((1, 1))), ("b", Leaf((1,)))])
     assert code_of(lambda: pskd.Reader(p).with_layout(small)) == "E9005"
 
-
-def test_pipeline():
-    p = pskd.Pipeline(1234, 4)
-    b1 = p.batches(10, 1)
-    assert len(b1) == 2, "incomplete last batch dropped"
-    seen = sorted(i for b in b1 for i in b)
-    assert len(seen) == 8 and len(set(seen)) == 8
-    assert p.batches(10, 1) == b1, "deterministic"
-    assert p.batches(10, 2) != b1, "re-keyed per epoch"
-    assert sorted(pskd.shuffle_indices(50, 7, 3)) == list(range(50))
-    q = pskd.Pipeline(None, 3, 2)
-    assert q.batches(10, 1) == [[0, 1, 2], [3, 4, 5]] and q.batches_per_epoch(10) == 2
-    assert pskd.Pipeline(None, 32).batches_per_epoch(100) == 3
