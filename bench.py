@@ -278,6 +278,36 @@ def measure(name, dtype, steps, warmup, realize=None, dropout=0.0, adamw=False, 
     return rec, p, (ln, c)
 
 
+def per_launch_table(p, path):
+    """Each distinct launch of the step (by kernel text) timed alone with HIP
+    events on its stream (10 repetitions): its count, mean time, algorithmic
+    bytes (inputs and output once) and flops, and the rates they give against
+    the HBM and MFMA peaks; written to `path` as markdown rows, slowest total
+    first."""
+    from presk_amd import hip
+    hip.sync()
+    agg = {}
+    for ln, ms in p.kernel_times(reps=10):
+        head = ln.low.text.split("{")[0].strip()
+        e = agg.setdefault(head, [0, 0.0, ln])
+        e[0] += 1
+        e[1] += ms
+    total = sum(e[1] for e in agg.values())
+    rows = ["| launch (kernel text's head) | class, order | launches | us each | us a step | MB | GB/s | % of HBM | TFLOP/s | % of MFMA |",
+            "|---|---|---|---|---|---|---|---|---|---|"]
+    for head, (n, ms, ln) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        c = ln.compiled
+        each = ms / n * 1e-3
+        gbs = c.bytes / each / 1e9
+        tf = c.flops / each / 1e12 if c.flops else 0.0
+        peak = PEAK_TFLOPS.get(ln.low.dtype, PEAK_TFLOPS["f32"])
+        rows.append(f"| `{head[:160]}` | {c.kind}, {c.order} | {n} | {each * 1e6:.2f} | {ms * 1e3:.1f} | {c.bytes / 1e6:.1f} | "
+                    f"{gbs:.0f} | {100 * gbs / HBM_GBS:.0f} | " + (f"{tf:.1f} | {100 * tf / peak:.0f} |" if c.flops else "| |"))
+    rows.append(f"| (all {sum(e[0] for e in agg.values())} launches) | | | | {total * 1e3:.1f} | | | | | |")
+    with open(path, "w") as f:
+        f.write("\n".join(rows) + "\n")
+
+
 # the other configurations, timed after the headline (rows of the same line)
 SUPPLEMENTARY = [("gpt-step", "bf16", None), ("gpt-forward", "f32", "@" + os.path.join(ROOT, "presk_amd", "realizations", "course_gpt_mixed.json")),
                  ("linear", "f32", None), ("mlp", "bf16", None), ("llama", "bf16", None)]
@@ -307,6 +337,8 @@ def main():
                          "the timings the choice is made on)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain copy-like nest (neg over 64 Mi f32) 3 times and exit: the counters' calibration")
+    ap.add_argument("--per-launch", default=None, metavar="FILE",
+                    help="also time each distinct launch alone and write a markdown table of them to FILE")
     ap.add_argument("--cpu-rows", type=int, default=None)
     ap.add_argument("--cpu-child", nargs=3, type=int, default=None, metavar=("ROWS", "THREADS", "CORE"),
                     help=argparse.SUPPRESS)
@@ -336,6 +368,8 @@ def main():
         return
     rec, p, (ln, c) = measure(args.workload, dtype, args.steps, args.warmup, args.realize, args.dropout, args.adamw,
                               args.eager, args.dominant_match)
+    if args.per_launch:
+        per_launch_table(p, args.per_launch)
     if args.dominant_only:
         hip.sync()
         for _ in range(args.dominant_only):
