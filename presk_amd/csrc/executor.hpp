@@ -31,11 +31,14 @@ struct ClassPlan {
     int64_t nest = -1, split = -1;
 
     // (first, count) of the split loop's iterations a launch covers, count
-    // -1 for the whole call; false when [lo, hi) is not a range the plan runs
+    // -1 for the whole call; false when [lo, hi) is not a range the plan runs.
+    // A plan that computes only whole calls (split -1, which the kernel's
+    // info reports as its split bound) takes (0, 0) as the whole call, as the
+    // ABI states, whatever the nest's own bound.
     bool range(int64_t lo, int64_t hi, int64_t* first, int64_t* count) const {
         *first = 0;
         *count = -1;
-        if (lo == 0 && (hi == nest || (nest < 0 && hi == 0))) return true;
+        if (lo == 0 && (hi == nest || ((nest < 0 || split < 0) && hi == 0))) return true;
         if (split < 0 || lo < 0 || hi > split || lo > hi) return false;
         *first = lo;
         *count = hi - lo;

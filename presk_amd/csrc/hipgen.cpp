@@ -700,8 +700,9 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
             body += "    long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;\n";
             // the outermost loop runs over [lo, hi) when split, else its bound
             const int vec0 = loops.size() == 1 ? vec : 1;  // the outermost loop is also the innermost
-            body += "    const long long n0 = " + std::string(ph.split ? "a.hi - a.lo" : std::to_string(loops[0]->bound / vec0) + "LL") + ";\n";
-            std::string total = "n0";
+            // (named apart from the nest's own integer scalars n<k>)
+            body += "    const long long grid_n0 = " + std::string(ph.split ? "a.hi - a.lo" : std::to_string(loops[0]->bound / vec0) + "LL") + ";\n";
+            std::string total = "grid_n0";
             for (size_t d = 1; d < loops.size(); ++d)
                 total += " * " + std::to_string(d + 1 == loops.size() ? loops[d]->bound / vec : loops[d]->bound) + "LL";
             body += "    if (t >= " + total + ") return;\n";

@@ -276,6 +276,18 @@ class Builder:
     def slice(self, x, axis, lo, hi, name=None):
         return self._prim(lambda dt: L.slice_(axis, lo, hi, [self.op(x)], dt), [x], name)
 
+    def slice_vjp(self, tmpl, ct, axis, lo, hi, name=None):
+        return self._prim(lambda dt: L.slice_vjp(axis, lo, hi, [self.op(tmpl), self.op(ct)], dt), [tmpl, ct], name)
+
+    def index(self, x, axis, i, name=None):
+        return self._prim(lambda dt: L.index_const(axis, i, [self.op(x)], dt), [x], name)
+
+    def scatter_index(self, tmpl, ct, axis, i, name=None):
+        return self._prim(lambda dt: L.scatter_index(axis, i, [self.op(tmpl), self.op(ct)], dt), [tmpl, ct], name)
+
+    def argmax(self, x, name=None):
+        return self._prim(lambda dt: L.argmax([self.op(x)], dt), [x], name)
+
     def concat(self, x, y, axis, name=None):
         return self._prim(lambda dt: L.concat(axis, [self.op(x), self.op(y)], dt), [x, y], name)
 

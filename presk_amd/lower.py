@@ -1012,10 +1012,149 @@ def slice_(axis, lo, hi, ins, dtype) -> Lowered:
     ov = bd.loops(dims(out))
     src = ivs(ov)
     src[p] = bin_("+", iv(ov[p]), str(lo))
-    if t.kind != "real":
-        raise ValueError("slice: an index operand (the reference's StoreI form) is not restated")
+    # an index operand is copied as indices (StoreI of LoadI: the same text)
+    kind = "idx" if t.kind == "idx" else "real"
     body = [Store(1, ivs(ov), load(0, src))]
-    return kernel(f"slice {axis}: {lo}..{hi}", dtype, ins, out, "real", bd, nest(ov, dims(out), body))
+    return kernel(f"slice {axis}: {lo}..{hi}", dtype, ins, out, kind, bd, nest(ov, dims(out), body))
+
+
+def slice_vjp(axis, lo, hi, ins, dtype) -> Lowered:
+    """lower.rs:1574-1590: zeros of the template's shape, the cotangent at
+    the elements lo..hi of the axis."""
+    tmpl, ct = ins
+    p = _axis_pos(tmpl.axes, axis)
+    if len(ct.axes) != len(tmpl.axes) or ct.axes[p].len != hi - lo:
+        raise ValueError(f"slice_vjp {axis}: {lo}..{hi}: a cotangent of {show(ct.axes)} into {show(tmpl.axes)}")
+    bd = B()
+    body = _zero_fill(bd, 2, tmpl.axes)
+    cv = bd.loops(dims(ct.axes))
+    dst = ivs(cv)
+    dst[p] = bin_("+", iv(cv[p]), str(lo))
+    body += nest(cv, dims(ct.axes), [Store(2, dst, load(1, ivs(cv)))])
+    return kernel(f"slice_vjp {axis}: {lo}..{hi}", dtype, ins, tmpl.axes, "real", bd, body)
+
+
+def _zero_fill(bd, buf, axes):
+    """`zero_fill` (lower.rs:1439-1442)."""
+    v = bd.loops(dims(axes))
+    return nest(v, dims(axes), [Store(buf, ivs(v), num(0))])
+
+
+def show(axes) -> str:
+    """`show` (lower.rs:1754-1760): `[name: len, len]`."""
+    return "[" + ", ".join(f"{a.name}: {a.len}" if a.name is not None else str(a.len) for a in axes) + "]"
+
+
+def argmax(ins, dtype) -> Lowered:
+    """lower.rs:1490-1516: the position of the largest element along the
+    last axis, seeded from element 0 and moved on `>=`, so that the last of
+    equal maxima wins (the interpreter's `max_by`); a NaN never compares, so
+    a later NaN is passed over and a NaN at element 0 keeps position 0."""
+    t = ins[0]
+    if not t.axes:
+        raise ValueError("argmax: scalar argument")
+    p = len(t.axes) - 1
+    v = t.axes[p].len
+    out = list(t.axes[:p])
+    bd = B()
+    ov = bd.loops(dims(out))
+    k = bd.iv()
+    m = bd.sv()
+    best = bd.si()
+    full = ivs(ov) + [iv(k)]
+    first = ivs(ov) + ["0"]
+    body = [Set(m, load(0, first)), SetI(best, "0"),
+            For(k, v, [If(cmp(">=", load(0, full), sv(m)), [Set(m, load(0, full)), SetI(best, iv(k))])]),
+            Store(1, ivs(ov), f"n{best}")]
+    return kernel("argmax", dtype, ins, out, "idx", bd, nest(ov, dims(out), body))
+
+
+def index_const(axis, index, ins, dtype) -> Lowered:
+    """lower.rs:1518-1535: `t[axis: index]` (a negative index counts from the
+    end), which drops the axis; for a real and an index tensor."""
+    t = ins[0]
+    p = _axis_pos(t.axes, axis)
+    n = t.axes[p].len
+    i = n + index if index < 0 else index
+    if i < 0 or i >= n:
+        raise ValueError(f"index {index} out of range for axis `{axis}` of length {n}")
+    out = list(t.axes[:p]) + list(t.axes[p + 1:])
+    bd = B()
+    ov = bd.loops(dims(out))
+    full = ivs(ov)
+    full.insert(p, str(i))
+    kind = "idx" if t.kind == "idx" else "real"
+    body = [Store(1, ivs(ov), load(0, full))]
+    return kernel(f"index {axis}: {index}", dtype, ins, out, kind, bd, nest(ov, dims(out), body))
+
+
+def scatter_index(axis, index, ins, dtype) -> Lowered:
+    """lower.rs:1537-1552: the cotangent of `index`: zeros of the template's
+    shape, the cotangent at position `index` of the axis."""
+    tmpl, ct = ins
+    p = _axis_pos(tmpl.axes, axis)
+    n = tmpl.axes[p].len
+    i = n + index if index < 0 else index
+    bd = B()
+    body = _zero_fill(bd, 2, tmpl.axes)
+    cv = bd.loops(dims(ct.axes))
+    full = ivs(cv)
+    full.insert(p, str(i))
+    body += nest(cv, dims(ct.axes), [Store(2, full, load(1, ivs(cv)))])
+    return kernel(f"scatter_index {axis}: {index}", dtype, ins, tmpl.axes, "real", bd, body)
+
+
+def one_hot(out, dtype) -> Lowered:
+    """lower.rs:1728-1744: 1 where the index equals the position on the new
+    trailing axis; `out` is the result's axes, the indices carry all but the
+    last."""
+    k = len(out) - 1
+    idx_axes, v = list(out[:k]), out[k].len
+    ins = [Operand(idx_axes, "idx")]
+    bd = B()
+    lv = bd.loops(dims(idx_axes))
+    j = bd.iv()
+    hit = cmp("==", f"real({load(0, ivs(lv))})", f"real({iv(j)})")
+    body = nest(lv, dims(idx_axes), [For(j, v, [Store(1, ivs(lv) + [iv(j)], select(hit, num(1), num(0)))])])
+    return kernel("one_hot", dtype, ins, out, "real", bd, body)
+
+
+def fill(name, axes, value, dtype) -> Lowered:
+    """lower.rs:1746-1752: a constant fill (`zeros`, `ones`)."""
+    bd = B()
+    v = bd.loops(dims(axes))
+    return kernel(name, dtype, [], axes, "real", bd, nest(v, dims(axes), [Store(0, ivs(v), num(value))]))
+
+
+def pack_panel(c: Contraction, dtype, w: Operand) -> Lowered:
+    """lower.rs:1155-1182: operand 1 of an NT contraction copied, in its own
+    type, to a panel of axes (the outer axes it carries..., K, J), which the
+    contraction then reads as NN; written along J."""
+    if len(c.ks) > 1:
+        raise ValueError(f"{c.name}: a pack of a sum over several axes")
+    carried = [o for o in range(len(c.outer)) if ("o", o) in c.w_index]
+
+    def at(slot):
+        return w.axes[c.w_index.index(slot)]
+
+    axes = [at(("o", o)) for o in carried] + [at("K"), at("J")]
+    bd = B()
+    lv = bd.loops(dims(axes))
+    ov = [0] * len(c.outer)
+    for n, o in enumerate(carried):
+        ov[o] = lv[n]
+    p = len(carried)
+    src = _slots(c.w_index, ov, "0", iv(lv[p + 1]), [iv(lv[p])])
+    body = [Store(1, ivs(lv), load(0, src))]
+    return kernel("pack", dtype, [w], axes, "real", bd, nest(lv, dims(axes), body))
+
+
+def packed(c: Contraction) -> Contraction:
+    """`Contraction::packed` (lower.rs:804-809): the same contraction reading
+    operand 1 from its NN panel."""
+    import dataclasses
+    carried = [("o", o) for o in range(len(c.outer)) if ("o", o) in c.w_index]
+    return dataclasses.replace(c, w_index=carried + ["K", "J"], nt=False)
 
 
 def concat(axis, ins, dtype) -> Lowered:

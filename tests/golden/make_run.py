@@ -99,6 +99,49 @@ def main():
     out["mlp.w2"] = {"dims": [16, 4], "f64": hexes(w2)}
     out["mlp.x"] = {"dims": [2, 4], "f64": hexes(K.normals(keys[1], 8))}
     out["mlp.y"] = {"dims": [2, 4], "f64": hexes(K.normals(keys[2], 8))}
+    # attention2 / attention3(θ : params Attention, x) (rope.psk): Attention's
+    # four params, each normal(std = 0.02) from its key (init.rs: the key split
+    # over the module's params in order); x N(0, 1) [batch 2, seq 8, model 16]
+    keys = K.split(master, 2)
+    kp = K.split(keys[0], 4)
+    for name, k, dims in (("wq", kp[0], [16, 2, 8]), ("wk", kp[1], [16, 2, 8]), ("wv", kp[2], [16, 2, 8]),
+                          ("wo", kp[3], [2, 8, 16])):
+        out["rope." + name] = {"dims": dims, "f64": hexes([v * 0.02 for v in K.normals(k, int(np.prod(dims)))])}
+    out["rope.x"] = {"dims": [2, 8, 16], "f64": hexes(K.normals(keys[1], 256))}
+    # loss / loss_grad(θ : params Toy, w : Window) (concat.psk): Toy's params
+    # tok, head, then its use qkv (QKV's wq, wk, wv), each normal(std = 0.02);
+    # the window idx[64][batch 2, seq 9], each index floor(u * 64) of the key's
+    # uniform draws (run.rs:325-331)
+    keys = K.split(master, 2)
+    kt = K.split(keys[0], 3)
+    out["concat.tok"] = {"dims": [64, 16], "f64": hexes([v * 0.02 for v in K.normals(kt[0], 64 * 16)])}
+    out["concat.head"] = {"dims": [16, 64], "f64": hexes([v * 0.02 for v in K.normals(kt[1], 16 * 64)])}
+    kq = K.split(kt[2], 3)
+    for name, k in zip(("wq", "wk", "wv"), kq):
+        out["concat." + name] = {"dims": [16, 16], "f64": hexes([v * 0.02 for v in K.normals(k, 256)])}
+    out["concat.w"] = {"dims": [2, 9], "f64": hexes([float(math.floor(u * 64)) for u in K.uniforms(keys[1], 18)])}
+    # loss_grad(θ : params Tower, x, scale) (stack_grad.psk): Tower's one use,
+    # stack{3}(Block), its key split over the 3 layers, each Block's w
+    # xavier_uniform [3, 3] and b normal(std = 0.5) [3]; x N(0, 1) [batch 2,
+    # model 3]; scale a real of no axes, one normal draw
+    keys = K.split(master, 3)
+    kb = K.split(K.split(keys[0], 1)[0], 3)
+    ws, bs = [], []
+    for kl in kb:
+        k2 = K.split(kl, 2)
+        ws += K.xavier(k2[0], 3, 3)
+        bs += [v * 0.5 for v in K.normals(k2[1], 3)]
+    out["stack.w"] = {"dims": [3, 3, 3], "f64": hexes(ws)}
+    out["stack.b"] = {"dims": [3, 3], "f64": hexes(bs)}
+    out["stack.x"] = {"dims": [2, 3], "f64": hexes(K.normals(keys[1], 6))}
+    out["stack.scale"] = {"dims": [1], "f64": hexes(K.normals(keys[2], 1))}
+    # next_token(θ, key, ctx, temperature = 0.8) (serve_minigpt.psk): the
+    # key argument is the second of the master's four; sample draws one
+    # uniform of it a batch row (host.rs:1659-1688); ctx idx[64][batch 2,
+    # seq 8] from the third
+    keys = K.split(master, 4)
+    out["next.u"] = {"dims": [2], "f64": hexes(K.uniforms(keys[1], 2))}
+    out["next.ctx"] = {"dims": [2, 8], "f64": hexes([float(math.floor(u * 64)) for u in K.uniforms(keys[2], 16)])}
     with open(os.path.join(HERE, "run", "inputs.json"), "w") as f:
         json.dump(out, f, indent=0)
     print("wrote", os.path.join(HERE, "run", "inputs.json"))

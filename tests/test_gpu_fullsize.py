@@ -1,0 +1,275 @@
+"""The measured programs at the sizes bench.py times them, under checks.
+
+Config 4 (the course-GPT training step, B 64 x T 256): in EXACT mode the
+loss, the logits and every parameter gradient equal the oracle's run of the
+same program byte for byte (their digests, computed once by the oracle in
+tests/golden/make_fullsize.py, since the oracle takes minutes at this size);
+in FAST mode the loss and every gradient lie within the bands the TINY step
+is held to, of the EXACT run.  At this size the weight gradients' K is
+16 384 (split across workgroups), the masked softmax's rows are 256 long,
+and every contraction fills many MFMA tiles -- the plans the TINY program
+never reaches.
+
+Config 5 (the Llama-7B-shaped forward, bf16 storage, B 1 x T 2048, FAST):
+the logits are finite, and on 16 sampled rows each stage of the first and
+the last layer, and the head, is recomputed in float64 from that stage's own
+device inputs: contractions within 2 gamma_K sum|x w| plus one bf16 unit of
+the sum and the result, the masked softmax within a few bf16 units of the
+float64 softmax (rows summing to 1, zeros past the diagonal), RMSNorm's
+mean square within the band of its 4 096-term sum, and the elementwise
+stages (residual adds, the SwiGLU product, RoPE's rotation, the scale) bit
+for bit from their f32 arithmetic rounded once to bf16."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from presk_amd import configs, gpt, hip, llama
+from tests import fmt
+
+pytestmark = pytest.mark.gpu
+
+
+# ---- config 4 --------------------------------------------------------------------
+
+FULLSIZE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fullsize_c4.json")
+
+
+def _course_step(dt, mode):
+    s = gpt.COURSE
+    p, b, names = gpt.build(s, dt, train=True, mode=mode)
+    p.compile()
+    configs.load_inputs(p, gpt.host_inputs(s))
+    p.prepare()
+    p.record(graph=True)
+    p.run()
+    hip.sync()
+    p.check_overflow()
+    return p, names
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_course_step_full_size(dt):
+    """EXACT: the loss, the logits and every gradient byte-equal to the
+    oracle's run of the same program (their sha256, tests/golden/
+    make_fullsize.py); FAST: the loss and every gradient within the TINY
+    step's bands of the EXACT run."""
+    table = json.load(open(FULLSIZE))[dt]
+    print(f"[fullsize] config 4 {dt}: EXACT", flush=True)
+    p, names = _course_step(dt, hip.EXACT)
+    got = {"loss": p.bufs.download(names["loss"]), "logits": p.bufs.download(names["logits"])}
+    got.update({"d." + n: p.bufs.download(buf) for n, buf in names["grads"].items()})
+    exact = {k: fmt.decode(v, dt).astype(np.float64) for k, v in got.items() if k != "logits"}
+    bad = [k for k, v in got.items() if hashlib.sha256(np.ascontiguousarray(v).tobytes()).hexdigest() != table["sha256"][k]]
+    assert not bad, f"{len(bad)} of {len(got)} buffers differ from the oracle's: {bad[:6]}"
+    assert float(exact["loss"][0]) == table["loss_value"]
+    # the loss of uniform targets under a near-uniform head sits at ln V
+    assert abs(table["loss_value"] - np.log(gpt.COURSE.V)) < 0.05
+    del p, got
+    print(f"[fullsize] config 4 {dt}: FAST", flush=True)
+    q, names = _course_step(dt, hip.FAST)
+    splits = sorted({ln.compiled.order for ln in q.launches if "-split" in ln.compiled.order})
+    assert splits, "no weight gradient took a k-split at full size"
+    loss = float(fmt.decode(q.bufs.download(names["loss"]), dt)[0])
+    want = float(exact["loss"][0])
+    tol = 1e-5 if dt == "f32" else 2e-2
+    assert abs(loss - want) <= tol * abs(want), (loss, want)
+    floor = 1e-3 * max(np.max(np.abs(v)) for k, v in exact.items() if k != "loss")
+    worst = []
+    for n, buf in names["grads"].items():
+        g = fmt.decode(q.bufs.download(buf), dt).astype(np.float64)
+        ref = exact["d." + n]
+        assert np.all(np.isfinite(g)), n
+        err = np.max(np.abs(g - ref)) / max(np.max(np.abs(ref)), floor)
+        worst.append((err, n))
+        assert err < (1e-4 if dt == "f32" else 6e-2), (n, err)
+    print(f"[fullsize] config 4 {dt}: loss {loss} (EXACT {want}); worst gradient {max(worst)}; {splits}", flush=True)
+
+
+# ---- config 5 --------------------------------------------------------------------
+
+U = 2.0 ** -24
+BF = 2.0 ** -7        # one bf16 unit, relative
+
+
+def within(got, exact, S, K, what, rel=BF):
+    """|got - exact| <= gamma_K S + one unit of the sum and of the result."""
+    gamma = K * U / (1 - K * U)
+    bound = gamma * S + rel * (S + 2 * np.maximum(np.abs(exact), np.abs(got))) + 1e-30
+    err = np.abs(got - exact)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite"
+    assert np.all(err <= bound), f"{what}: {np.count_nonzero(err > bound)} of {err.size} outside the band"
+    assert np.median(err / bound) < 1 / 4, f"{what}: median error {np.median(err / bound):.3g} of the band"
+
+
+def bf16(x):
+    """float64 -> the f32 value rounded once to bf16 (as a store does)."""
+    return fmt.roundtrip(np.asarray(x, np.float32), "bf16").astype(np.float64)
+
+
+class Dev:
+    """The program's buffers on the host, as float64 arrays of their axes."""
+
+    def __init__(self, p, b):
+        self.p, self.b = p, b
+
+    def __call__(self, name):
+        base = self.b.base.get(name, name)
+        ty, _ = self.p.bufs.meta[base]
+        a = fmt.decode(self.p.bufs.download(base), ty).astype(np.float64)
+        return a.reshape([ax.len for ax in self.b.axes[name]])
+
+
+@pytest.fixture(scope="module")
+def llama_run():
+    s = llama.LLAMA_7B
+    print("[fullsize] config 5: build and run", flush=True)
+    p, b, names = llama.build(s, "bf16", mode=hip.FAST)
+    p.compile()
+    llama.load_device_inputs(p, s)
+    p.prepare()
+    p.record(graph=True)
+    p.run()
+    hip.sync()
+    p.check_overflow()
+    yield s, p, b, names
+    p.release_batch()
+
+
+ROWS = np.array([0, 1, 17, 255, 256, 511, 700, 1023, 1024, 1290, 1536, 1777, 1900, 2000, 2046, 2047])
+
+
+def test_llama_logits_finite(llama_run):
+    s, p, b, names = llama_run
+    lg = Dev(p, b)(names["logits"])
+    assert lg.shape == (1, s.T, s.V)
+    assert np.all(np.isfinite(lg))
+    assert np.std(lg) > 0
+
+
+def _rmsnorm_check(d, x, tag, eps, K):
+    """x * x bit-exact; ms within its K-term sum's band; sd and y bit-exact
+    from the device's own ms and sd (f32 arithmetic, one rounding)."""
+    xr = x[0, ROWS]
+    xx = d(f"{tag}.xx")[0, ROWS]
+    assert np.array_equal(xx, bf16(xr.astype(np.float32) * xr.astype(np.float32))), f"{tag}.xx"
+    ms = d(f"{tag}.ms")[0, ROWS]
+    exact = xx.mean(axis=1)
+    within(ms, exact, np.abs(xx).mean(axis=1), K, f"{tag}.ms")
+    sd = d(f"{tag}.sd")[0, ROWS]
+    assert np.array_equal(sd, bf16(np.sqrt(ms.astype(np.float32) + np.float32(eps)))), f"{tag}.sd"
+    return d(f"{tag}.y")[0, ROWS], sd
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("layer", [0, 31])
+def test_llama_layer_stages_in_float64(llama_run, layer):
+    s, p, b, names = llama_run
+    d = Dev(p, b)
+    pr = f"b{layer}."
+    T, D, H, HD, FF = s.T, s.D, s.H, s.HD, s.FF
+    f32 = np.float32
+    print(f"[fullsize] config 5 layer {layer}", flush=True)
+    x = d("x0" if layer == 0 else f"b{layer - 1}.out")           # [1, T, D]
+    eps = float(bf16(s.eps))
+    # ---- RMSNorm 1
+    y, sd = _rmsnorm_check(d, x, pr + "n1", eps, D)
+    gain = d(pr + "n1.g")
+    want = bf16((x[0, ROWS].astype(f32) / sd[:, None].astype(f32)) * gain.astype(f32))
+    assert np.array_equal(y, want), "n1.y"
+    h = d(pr + "n1.y")[0]                                        # [T, D], every row (k, v need them)
+    # ---- projections q (sampled rows), k and v (every row: the scores read them)
+    wq = d(pr + "attn.wq")
+    wk = d(pr + "attn.wk")
+    wv = d(pr + "attn.wv")
+    qp = d(pr + "qp")[0, :, 0]                                   # [G, T, HD]
+    hq = h[ROWS]
+    exact = (hq @ wq).reshape(len(ROWS), H, HD).transpose(1, 0, 2)
+    S = (np.abs(hq) @ np.abs(wq)).reshape(len(ROWS), H, HD).transpose(1, 0, 2)
+    within(qp[:, ROWS], exact, S, D, "qp")
+    kp = d(pr + "kp")[0]                                         # [G, T, HD]
+    within(kp, (h @ wk).reshape(T, H, HD).transpose(1, 0, 2), (np.abs(h) @ np.abs(wk)).reshape(T, H, HD).transpose(1, 0, 2),
+           D, "kp")
+    vd = d(pr + "vd")[0]                                         # [T, G*HD]
+    within(vd[ROWS], hq @ wv, np.abs(hq) @ np.abs(wv), D, "vd")
+    # ---- RoPE: cos and sin of the device's angles within one bf16 unit;
+    # the rotation bit-exact from the device's halves and c, s
+    phi = d("phi")                                               # [T, HD/2]
+    for nm, fn in (("c", np.cos), ("s", np.sin)):
+        v = d(f"{pr}q.{nm}")
+        ref = fn(phi)
+        assert np.all(np.abs(v - ref) <= BF * np.abs(ref) + 2.0 ** -24), f"q.{nm}"
+    c, sn = d(f"{pr}q.c").astype(f32), d(f"{pr}q.s").astype(f32)
+    x0, x1 = qp[..., : HD // 2].astype(f32), qp[..., HD // 2:].astype(f32)
+    r0 = bf16(x0 * c - x1 * sn)
+    r1 = bf16(x1 * c + x0 * sn)
+    q = d(pr + "q.rot")[0, :, 0]                                 # [G, T, HD]
+    assert np.array_equal(q[:, ROWS], np.concatenate([r0, r1], axis=-1)[:, ROWS]), "rope(q)"
+    k = d(pr + "k.rot")[0]                                       # [G, T, HD]
+    # ---- scores, the scale, the masked softmax
+    sc = d(pr + "scores")[0, :, 0]                               # [G, T, T]
+    within(sc[:, ROWS], np.einsum("gtd,gsd->gts", q[:, ROWS], k, optimize=True),
+           np.einsum("gtd,gsd->gts", np.abs(q[:, ROWS]), np.abs(k), optimize=True),
+           HD, "scores")
+    sq = d(pr + "sqrt_hd")
+    assert np.array_equal(sq, bf16(np.sqrt(f32(HD)))), "sqrt_hd"
+    sc2 = d(pr + "scaled")[0, :, 0]
+    assert np.array_equal(sc2[:, ROWS], bf16(sc[:, ROWS].astype(f32) / sq.astype(f32))), "scaled"
+    pb = d(pr + "probs")[0, :, 0]                                # [G, T, T]
+    sub = pb[:, ROWS]
+    allowed = np.arange(T)[None, :] <= ROWS[:, None]             # [R, T]
+    assert np.all(sub[:, ~allowed] == 0), "probs past the diagonal"
+    z = sc2[:, ROWS]
+    z = np.where(allowed[None], z, -np.inf)
+    e = np.exp(z - z.max(axis=-1, keepdims=True))
+    ref = e / e.sum(axis=-1, keepdims=True)
+    assert np.all(np.abs(sub - ref) <= 2 * BF * ref + 1e-7), "masked softmax"
+    rs = sub.sum(axis=-1)
+    assert np.all(np.abs(rs - 1) <= 2.0 ** -7), f"probs rows sum to {rs.min()}..{rs.max()}"
+    # ---- values and the output projection
+    v = vd.reshape(T, H, HD)
+    o = d(pr + "o")[0]                                           # [T, G, 1, HD]
+    within(o[ROWS, :, 0], np.einsum("gts,sgd->tgd", pb[:, ROWS], v, optimize=True),
+           np.einsum("gts,sgd->tgd", np.abs(pb[:, ROWS]), np.abs(v), optimize=True),
+           T, "o")
+    wo = d(pr + "attn.wo")
+    orow = o[ROWS].reshape(len(ROWS), D)
+    ao = d(pr + "ao")[0]
+    within(ao[ROWS], orow @ wo, np.abs(orow) @ np.abs(wo), D, "ao")
+    x2 = d(pr + "x")[0]
+    assert np.array_equal(x2[ROWS], bf16(x[0, ROWS].astype(f32) + ao[ROWS].astype(f32))), "x + ao"
+    # ---- RMSNorm 2 and SwiGLU
+    y2, sd2 = _rmsnorm_check(d, x2[None], pr + "n2", eps, D)
+    g2 = d(pr + "n2.g")
+    assert np.array_equal(y2, bf16((x2[ROWS].astype(f32) / sd2[:, None].astype(f32)) * g2.astype(f32))), "n2.y"
+    h2 = y2
+    wg, wu, wd = d(pr + "ff.gate"), d(pr + "ff.up"), d(pr + "ff.down")
+    gt = d(pr + "gate")[0, ROWS]
+    within(gt, h2 @ wg, np.abs(h2) @ np.abs(wg), D, "gate")
+    up = d(pr + "up")[0, ROWS]
+    within(up, h2 @ wu, np.abs(h2) @ np.abs(wu), D, "up")
+    sl = d(pr + "silu")[0, ROWS]
+    ref = gt / (1 + np.exp(-gt))
+    assert np.all(np.abs(sl - ref) <= BF * np.abs(ref) + 2.0 ** -30), "silu"
+    gu = d(pr + "gu")[0, ROWS]
+    assert np.array_equal(gu, bf16(sl.astype(f32) * up.astype(f32))), "silu * up"
+    dn = d(pr + "down")[0, ROWS]
+    within(dn, gu @ wd, np.abs(gu) @ np.abs(wd), FF, "down")
+    out = d(pr + "out")[0, ROWS]
+    assert np.array_equal(out, bf16(x2[ROWS].astype(f32) + dn.astype(f32))), "x2 + down"
+
+
+def test_llama_head_in_float64(llama_run):
+    s, p, b, names = llama_run
+    d = Dev(p, b)
+    x = d(f"b{s.L - 1}.out")
+    eps = float(bf16(s.eps))
+    y, sd = _rmsnorm_check(d, x, "norm", eps, s.D)
+    g = d("norm.g")
+    assert np.array_equal(y, bf16((x[0, ROWS].astype(np.float32) / sd[:, None].astype(np.float32)) * g.astype(np.float32)))
+    w = d("head")
+    lg = d(names["logits"])[0, ROWS]
+    within(lg, y @ w, np.abs(y) @ np.abs(w), s.D, "logits")

@@ -61,3 +61,45 @@ def test_golden_minigpt_zero_head(mode):
     logits = read(p, names["logits"], "f32")
     assert logits.size == R.snapshot("minigpt_forward").size and np.all(logits == 0.0)
     assert np.all(R.within(read(p, names["loss"], "f32"), R.snapshot("minigpt_loss"), "f32"))
+
+
+@pytest.mark.parametrize("mode", [hip.EXACT, hip.FAST])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("entry", ["rope_attention2", "rope_attention3", "concat_loss_grad", "stack_grad",
+                                   "minigpt_next_token"])
+def test_newer_golden_entry(entry, dt, mode):
+    """Attention with RoPE (slices, concat, sin/cos, the masked softmax, the
+    projections' `ein`s), the concat toy's loss and gradient (slices of index
+    and real tensors, `slice_vjp`, min/max/clamp and their adjoints,
+    `embed_vjp`), the stacked fold's gradient, and next_token's `index` and
+    scale (the draw on the host): each within the conformance band of the
+    reference's exact output, and in EXACT mode byte-equal to the oracle."""
+    print(f"[golden] {entry} {dt} mode {mode}", flush=True)
+    if entry.startswith("rope"):
+        p, host, names = R.rope_attention(dt, int(entry[-1]), mode=mode)
+    elif entry == "concat_loss_grad":
+        p, host, names = R.concat_toy(dt, grad=True, mode=mode)
+    elif entry == "stack_grad":
+        p, host, names = R.stack_tower(dt, mode=mode)
+    else:
+        p, host, names = R.next_token(dt, mode=mode)
+    device(p, host)
+    if mode == hip.EXACT:
+        env = cpu_program.run(p, host)
+        bad = [ln.out for ln in p.launches if p.bufs.download(ln.out).tobytes() != np.ascontiguousarray(env[ln.out]).tobytes()]
+        assert not bad, bad[:5]
+    if entry.startswith("rope"):
+        assert np.all(R.within(read(p, names["out"], dt), R.snapshot(entry), dt))
+    elif entry == "concat_loss_grad":
+        assert np.all(R.within(read(p, names["loss"], dt), R.snapshot("concat_loss"), dt))
+        want = R.snapshot(entry)
+        for leaf in ("tok", "head", "qkv.wq", "qkv.wk", "qkv.wv"):
+            assert np.all(R.within(read(p, names[leaf], dt), want[leaf], dt)), leaf
+    elif entry == "stack_grad":
+        want = R.snapshot(entry)
+        for leaf in ("blocks.w", "blocks.b"):
+            got = np.concatenate([read(p, n, dt).ravel() for n in names[leaf]])
+            assert np.all(R.within(got, want[leaf], dt)), leaf
+    else:
+        scaled = read(p, names["scaled"], dt).reshape(2, 64)
+        assert np.array_equal(R.sample_rows(scaled, R.inputs()["next.u"]), R.snapshot(entry))

@@ -38,6 +38,9 @@ def pairs():
         out.append((f"masked_softmax_long-{dt}", hip.EXACT, "rows", masked(dt, 400), masked(dt, 300)))
         out.append((f"sum_to-{dt}", hip.FAST, "colsum", colsum(dt, 600), colsum(dt, 300)))
         out.append((f"gelu-{dt}", hip.EXACT, "generic", gelu(dt, 60), gelu(dt, 30)))
+    # e8m15: the operands' and the output's f32 widenings, then the split-K
+    # partials, at 256-byte-aligned offsets of the same scratch
+    out.append(("dot_vjp_r-split-e8m15", hip.FAST, "gemm", vjp_r("e8m15", 1200), vjp_r("e8m15", 600)))
     return out
 
 
@@ -66,6 +69,8 @@ def test_noalloc_equals_run(case):
     cb = ex.compiled(big.text, big.dtype, big.lanes)
     cs = ex.compiled(small.text, small.dtype, small.lanes)
     assert cb.kind == kind and cs.kind == kind
+    if kind == "gemm":
+        assert "-split" in cb.order and "-split" in cs.order, (cb.order, cs.order)
     want_b, _ = _launch(lib.presk_hip_run, cb, big, 1)
     want_s, _ = _launch(lib.presk_hip_run, cs, small, 2)
     got_b, _ = _launch(lib.presk_hip_run_noalloc, cb, big, 1)

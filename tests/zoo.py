@@ -93,6 +93,52 @@ def cases(dtypes=("f32", "bf16", "f16", "e8m15")):
         k = O(A(("heads", 2), ("seq2", 5), ("hd", 9)))
         out.append((f"ein_chunked4-{dt}", L.ein([q, k], [["heads", "seq", "hd"], ["heads", "seq2", "hd"]], ["heads", "seq", "seq2"], dt,
                                                order=("chunked", 4))))
+    out += _gather_cases()
+    return out
+
+
+def _gather_cases():
+    """The dispatch table's remaining nests (lower.rs:1155, 1490-1590,
+    1728-1752) and the unary/binary forms of min, max, clamp and their
+    derivatives (lower.rs:180-226; rules.rs:115-125: heaviside of a
+    difference), in every storage type."""
+    out = []
+    x = O(A(("batch", 3), ("seq", 5), ("vocab", 7)))
+    xi = O(A(("batch", 3), ("seq", 9)), "idx")
+    r = O(A(("batch", 3), ("seq", 5)))
+    for dt in ("f32", "bf16", "f16", "e8m15"):
+        out.append((f"argmax-{dt}", L.argmax([x], dt)))
+        out.append((f"index_last-{dt}", L.index_const("seq", -1, [x], dt)))
+        out.append((f"index_mid-{dt}", L.index_const("vocab", 3, [x], dt)))
+        out.append((f"scatter_index-{dt}", L.scatter_index("seq", -1, [x, O(A(("batch", 3), ("vocab", 7)))], dt)))
+        out.append((f"slice-{dt}", L.slice_("vocab", 2, 6, [x], dt)))
+        out.append((f"slice_vjp-{dt}", L.slice_vjp("vocab", 2, 6, [x, O(A(("batch", 3), ("seq", 5), ("vocab", 4)))], dt)))
+        out.append((f"one_hot-{dt}", L.one_hot(A(("batch", 3), ("seq", 5), ("vocab", 7)), dt)))
+        out.append((f"zeros-{dt}", L.fill("zeros", A(("batch", 3), 6), 0.0, dt)))
+        out.append((f"ones-{dt}", L.fill("ones", A(("batch", 3), 6), 1.0, dt)))
+        for op in ("relu", "heaviside", "sign", "abs"):
+            out.append((f"{op}-{dt}", L.unary(op, [x], dt)))
+        out.append((f"min-{dt}", L.elementwise_binary("min", [x, r], dt)))
+        # clamp(x, lo, hi) = min(max(x, lo), hi) (crates/presk-core/src/lower/expr.rs:540-545)
+        out.append((f"clamp-{dt}", L.fused([("max", [("in", 0), ("in", 1)]), ("min", [("step", 0), ("in", 2)])],
+                                           [x, O([]), O([])], x.axes, dt)))
+        # max's adjoints: heaviside(a - b) * ct and (1 - heaviside(a - b)) * ct
+        out.append((f"max_vjp_a-{dt}", L.fused([("sub", [("in", 0), ("in", 1)]), ("heaviside", [("step", 0)]),
+                                                ("mul", [("in", 2), ("step", 1)])], [x, x, x], x.axes, dt)))
+        out.append((f"max_vjp_b-{dt}", L.fused([("sub", [("in", 0), ("in", 1)]), ("heaviside", [("step", 0)]),
+                                                ("sub", [("in", 3), ("step", 1)]), ("mul", [("in", 2), ("step", 2)])],
+                                               [x, r, x, O([])], x.axes, dt)))
+        # the pack of an NT contraction's operand 1 (lower.rs:1155-1182):
+        # dot_vjp_l's matrix and the scores' keys
+        c = L.contraction_of("dot_vjp_l", [O(A(("batch", 3), ("seq", 5), 12)), O(A(10, 12))])
+        out.append((f"pack_vjp_l-{dt}", L.pack_panel(c, dt, O(A(10, 12)))))
+        q = O(A(("batch", 2), ("heads", 3), ("seq", 5), ("hd", 8)))
+        k = O(A(("batch", 2), ("heads", 3), ("seq2", 6), ("hd", 8)))
+        c = L.contraction_of("ein", [q, k], [["batch", "heads", "seq", "hd"], ["batch", "heads", "seq2", "hd"]],
+                             ["batch", "heads", "seq", "seq2"])
+        out.append((f"pack_scores-{dt}", L.pack_panel(c, dt, k)))
+    out.append(("slice_idx", L.slice_("seq", 1, 9, [xi], "f32")))
+    out.append(("index_idx", L.index_const("seq", 0, [xi], "f32")))
     return out
 
 
@@ -112,6 +158,14 @@ def inputs(low: L.Lowered, seed: int = 0, scale: float = 1.0):
             arrs.append(rng.integers(0, hi, size=b.numel, dtype=np.int64))
         else:
             v = (rng.standard_normal(b.dims) * scale).astype(np.float32)
+            if low.name in ("argmax", "fused 2 steps", "fused 3 steps", "fused 4 steps", "min"):
+                # a coarse grid, so that ties (max/min's second operand, the
+                # last of equal maxima) and zeros (heaviside's boundary) occur,
+                # and a NaN in a first and in a later position
+                v = np.round(v * 2).astype(np.float32) / 2
+                if low.name == "argmax" and v.size > 8:
+                    v.ravel()[0] = np.nan
+                    v.ravel()[9] = np.nan
             arrs.append(fmt.encode(v, b.ty))
     return arrs
 
@@ -124,4 +178,9 @@ def _index_bound(low, k, i):
         return k.inputs[0].dims[-1]
     if name.startswith("softmax"):
         return 2
+    if name == "one_hot":
+        # one index past the last position: a row with no hit
+        return k.output.dims[-1] + 1
+    if name.startswith(("slice", "index")):
+        return 1000
     return 2
