@@ -242,8 +242,12 @@ int presk_hip_fill_normal(void *dst, const char *type, int64_t n, uint64_t seed,
 
 /* Self-test of the device's scalar functions over a domain block: the digest
  * (sum of splitmix64 finalizers of (i << 32 | out_i)) of function `fn` over
- * inputs [lo, hi), as tests/golden/digests.json holds the reference's.  No
- * counterpart in the reference; for the exhaustive device checks. */
+ * inputs [lo, hi), as tests/golden/digests.json holds the reference's.  For
+ * fn 50 (expf) and 51 (erff) the result is instead the largest distance in
+ * units in the last place between FAST mode's function and the
+ * interpreter's over the inputs, and for fn 60 / 61 the count of inputs
+ * where the two differ.  No counterpart in the reference; for the
+ * exhaustive device checks. */
 int presk_hip_scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t *digest);
 
 #ifdef __cplusplus

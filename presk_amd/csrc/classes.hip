@@ -709,11 +709,23 @@ struct RowPlan : ClassPlan {
     bool guarded = false;
     long long rows_per_iter = 0;   // rows one iteration of the split loop covers
     bool row_out = false;          // one output element a row (a sum, a mean, a loss)
+    // FAST: the sums in the `lanes64-tree` order over blocks of `vec`
+    // elements and FAST mode's exponential (wrows.hip)
+    bool fast = false;
+    int vec = 1;
     const char* kind() const override { return "rows"; }
-    std::string order() const override { return "sequential"; }
-    // the mask as bits (masked softmax over long rows), [mask_rows][words]
+    std::string order() const override {
+        if (!fast) return "sequential";
+        const bool exps = a.op != kRowMean && a.op != kRowSum && a.op != kSumToRows;
+        return "lanes64x" + std::to_string(vec) + "-tree" + (exps ? "+fast-exp" : "");
+    }
+    bool masked() const { return a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2; }
+    // the mask as bits (masked softmax over long rows, and every masked
+    // softmax in FAST), [mask_rows][words]
     size_t workspace_bytes() const override {
-        return rows_need_mask_bits(a) ? (size_t)a.mask_rows * rows_mask_words(a.n) * sizeof(unsigned) : 0;
+        return rows_need_mask_bits(a) || (fast && masked() && a.rows > 0)
+                   ? (size_t)a.mask_rows * rows_mask_words(a.n) * sizeof(unsigned)
+                   : 0;
     }
     hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const override {
         int64_t first, count;
@@ -738,13 +750,18 @@ struct RowPlan : ClassPlan {
             if (x.ct) x.ct = (const char*)x.ct + r0 * esz;
             if (a.mask_rows > 0) x.mask_row0 = r0 % a.mask_rows;
         }
+        if (fast && wrows_fits(x)) {
+            x.mbits = masked() ? (unsigned*)work : nullptr;
+            if (masked() && !work) return hipErrorInvalidValue;
+            return wrows_launch(x, stream);
+        }
         x.mbits = rows_need_mask_bits(x) ? (unsigned*)work : nullptr;
         if (rows_need_mask_bits(x) && !work) return hipErrorInvalidValue;
         return rows_launch(x, stream);
     }
 };
 
-std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
+std::unique_ptr<ClassPlan> classify_rows(const Kernel& k, bool fast) {
     const int st = k.dtype == Ty::F32 ? 0 : k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : -1;
     if (st < 0 || k.inputs.empty() || k.inputs[0].ty != k.dtype || k.inputs[0].dims.empty()) return nullptr;
     const BufSpec& x = k.inputs[0];
@@ -812,6 +829,12 @@ std::unique_ptr<ClassPlan> classify_rows(const Kernel& k) {
     // the split loop runs over x's first axis (and the output's), each
     // iteration a run of whole rows
     p->row_out = p->a.op == kRowMean || p->a.op == kRowSum || p->a.op == kSumToRows || p->a.op == kCrossEntropy;
+    // FAST: one wave a row (rows of up to 16 blocks a lane); a single
+    // total (`mean`/`sum` of every element) stays ordered
+    if (fast && p->a.rows > 1 && wrows_ok(p->a)) {
+        p->fast = true;
+        p->vec = wrows_vec(p->a);
+    }
     p->nest = parallel_outer(k);
     if (p->nest > 0 && x.dims[0] == p->nest && !k.output.dims.empty() && k.output.dims[0] == p->nest &&
         p->a.rows % p->nest == 0) {
@@ -872,8 +895,8 @@ std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode) {
     // FAST: column sums and totals in the declared chunked order
     if (mode == PRESK_HIP_FAST)
         if (auto p = classify_sum_to(k)) return p;
-    // exact in every mode: the interpreter's order, row by row
-    if (auto p = classify_rows(k)) return p;
+    // row nests: the interpreter's order (EXACT), FAST's lane tree (FAST)
+    if (auto p = classify_rows(k, mode == PRESK_HIP_FAST)) return p;
     if (auto p = classify_scatter(k)) return p;
     if (mode == PRESK_HIP_FAST)
         if (auto p = classify_gemm(k)) return p;

@@ -409,6 +409,48 @@ PK_DEV float pk_erff(float x) {
     return neg ? -y : y;
 }
 
+// ---- FAST mode's functions ------------------------------------------------------
+// Not the interpreter's bits: FAST mode's exponential and error function, each
+// within a bound stated against musl's (the functions above) and measured on
+// the device over every f32 input (presk_hip_scalar_digest's ulp scans).
+
+// e^x: x = k ln2 + r by Cody-Waite in two fmas (ln2's high part has 16
+// significant bits, so k ln2_hi is exact for |k| < 2^8), |r| <= ln2 / 2;
+// e^r = 2^(r log2 e) by the hardware's v_exp_f32 (an argument within 1/2,
+// a normal result); then v_ldexp_f32 by k (one rounding where the result
+// is subnormal, overflow to infinity and underflow to zero as it
+// rounds).  The argument is clamped to [-104, 89] first (e^x rounds to 0
+// below and overflows above), a NaN passed through.
+PK_DEV float pk_expf_fast(float x) {
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 89.0f);
+    const float k = __builtin_rintf(xc * 1.44269502e+0f);
+    float r = __builtin_fmaf(-k, 6.93145751953125e-1f, xc);
+    r = __builtin_fmaf(-k, 1.42860677e-6f, r);
+    const float y = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(r * 1.44269502e+0f), (int)k);
+    return x != x ? x + x : y;
+}
+
+// erf(x): x P(x^2) below |x| = 1 (P of degree 5, a relative minimax fit of
+// erf(sqrt z)/sqrt z on [0, 1]), else 1 - e^(-x^2 + G(|x|)) with G of degree
+// 8 in |x| - 2.5 fitted to log(erfc(u)) + u^2 on [1, 4] (|x| clamped to 4,
+// where 1 - erfc already rounds to 1), the sign restored; both branches
+// evaluated and one chosen, so a wave runs no divergent paths.
+PK_DEV float pk_erff_fast(float x) {
+    const float u = __builtin_fabsf(x);
+    const float z = x * x;
+    const float p = 1.12837911e+0f + z * (-3.76123250e-1f + z * (1.12801798e-1f + z * (-2.67113112e-2f +
+                    z * (4.91755083e-3f + z * -5.63141890e-4f))));
+    const float small = x * p;
+    const float s = __builtin_fminf(u, 4.0f) - 2.5f;
+    const float g = -1.55681527e+0f + s * (-3.52680683e-1f + s * (5.61063923e-2f + s * (-1.08584873e-2f +
+                    s * (2.16508145e-3f + s * (-4.20173135e-4f + s * (7.74549189e-5f + s * (-1.33017093e-5f +
+                    s * 1.59981914e-6f)))))));
+    const float uc = __builtin_fminf(u, 4.0f);
+    const float large = __builtin_copysignf(1.0f - pk_expf_fast(__builtin_fmaf(-uc, uc, g)), x);
+    const float y = u < 1.0f ? small : large;
+    return x != x ? x + x : y;
+}
+
 // ---- sinf / cosf: fdlibm's method in f64 (presk_libm.c:672-746 the
 // kernels, 1372-1447 the reduction, 749-1189 its large-argument form,
 // 2054-2111 sinf, 2213-2272 cosf) ---------------------------------------------

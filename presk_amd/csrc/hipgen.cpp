@@ -44,6 +44,11 @@ struct Printer {
     // `post[u]`, written back after the iterations (key: its index text).
     std::map<std::string, int> pre;
     std::string post_key;
+    // FAST mode: f32 exponentials and error functions by pk_expf_fast and
+    // pk_erff_fast (within a stated bound of the interpreter's, not its
+    // bits); `used_fast` records whether the kernel called one
+    bool fast_fns = false;
+    bool used_fast = false;
 
     explicit Printer(const Kernel& k) : k(k) {
         A = k.dtype == Ty::F64 ? "double" : "float";
@@ -168,10 +173,14 @@ struct Printer {
                     case Un::Sqrt: return std::string(f ? "__builtin_sqrtf(" : "__builtin_sqrt(") + a + ")";
                     // f32 arithmetic: the f32 functions; f64: the double ones
                     // (exec.rs:115-130, musl's exp/log/tanh/erf/sin/cos)
-                    case Un::Exp: return std::string(f ? "pk_expf(" : "pk_exp(") + a + ")";
+                    case Un::Exp:
+                        if (f && fast_fns) return used_fast = true, "pk_expf_fast(" + a + ")";
+                        return std::string(f ? "pk_expf(" : "pk_exp(") + a + ")";
                     case Un::Log: return std::string(f ? "pk_logf(" : "pk_log(") + a + ")";
                     case Un::Tanh: return std::string(f ? "pk_tanhf(" : "pk_tanh(") + a + ")";
-                    case Un::Erf: return std::string(f ? "pk_erff(" : "pk_erf(") + a + ")";
+                    case Un::Erf:
+                        if (f && fast_fns) return used_fast = true, "pk_erff_fast(" + a + ")";
+                        return std::string(f ? "pk_erff(" : "pk_erf(") + a + ")";
                     case Un::Sin: return std::string(f ? "pk_sinf(" : "pk_sin(") + a + ")";
                     case Un::Cos: return std::string(f ? "pk_cosf(" : "pk_cos(") + a + ")";
                 }
@@ -582,7 +591,7 @@ bool owns_one_element(const Kernel& k, const std::vector<const Stmt*>& body, con
 
 }  // namespace
 
-bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
+bool generate_hip(const Kernel& k, Generated* out, std::string* err, bool fast_fns) {
     if (!k.arith.empty()) {
         *err = "E7005: the kernel `" + k.name + "` rounds to formats other than its storage type's arithmetic (" + k.arith +
                "); the kernel interpreter emulates those";
@@ -593,6 +602,7 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
         return false;
     }
     Printer P(k);
+    P.fast_fns = fast_fns;
     // The phases: each top-level statement its own launch when none reads a
     // variable an earlier one wrote; otherwise one sequential phase.
     std::vector<std::vector<const Stmt*>> groups;
@@ -839,6 +849,7 @@ bool generate_hip(const Kernel& k, Generated* out, std::string* err) {
         return false;
     }
     out->src = src;
+    out->fast_fns = P.used_fast;
     return true;
 }
 

@@ -34,10 +34,14 @@ struct Phase {
 struct Generated {
     std::string src;
     std::vector<Phase> phases;
+    bool fast_fns = false;            // an f32 exp or erf printed as FAST mode's function
 };
 
 // Prints `k`.  Returns false and sets `err` for a kernel the printer refuses.
-bool generate_hip(const Kernel& k, Generated* out, std::string* err);
+// `fast_fns` (FAST mode): f32 exp and erf as pk_expf_fast / pk_erff_fast,
+// whose results lie within a stated bound of the interpreter's, in place of
+// its bits.
+bool generate_hip(const Kernel& k, Generated* out, std::string* err, bool fast_fns = false);
 
 // The argument block every printed phase takes (by value).
 struct PhaseArgs {

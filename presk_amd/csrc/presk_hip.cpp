@@ -270,7 +270,7 @@ int presk_hip_compile(const char* text, const char* dtype, int lanes, int mode, 
     h->mode = mode;
     h->plan = classify(*k, mode);
     if (!h->plan) {
-        if (!generate_hip(*k, &h->gen, &err)) return fail(err.compare(0, 5, "E7005") == 0 ? PRESK_HIP_REFUSED : PRESK_HIP_ERR, err);
+        if (!generate_hip(*k, &h->gen, &err, mode == PRESK_HIP_FAST)) return fail(err.compare(0, 5, "E7005") == 0 ? PRESK_HIP_REFUSED : PRESK_HIP_ERR, err);
         // PRESK_HIP_DUMP=<dir>: keep each printed source, for inspection
         if (const char* dump = std::getenv("PRESK_HIP_DUMP")) {
             char name[40];
@@ -403,7 +403,8 @@ int presk_hip_kernel_info(const presk_hip_kernel* h, presk_hip_info* info) {
     if (!h || !info) return fail(PRESK_HIP_ERR, "E10001: null argument");
     std::memset(info, 0, sizeof *info);
     std::snprintf(info->kind, sizeof info->kind, "%s", h->plan ? h->plan->kind() : "generic");
-    std::snprintf(info->order, sizeof info->order, "%s", h->plan ? h->plan->order().c_str() : "sequential");
+    std::snprintf(info->order, sizeof info->order, "%s",
+                  h->plan ? h->plan->order().c_str() : h->gen.fast_fns ? "sequential+fast-exp-erf" : "sequential");
     info->guarded = h->k->guarded();
     info->n_inputs = (int32_t)h->k->inputs.size();
     info->split_bound = h->plan ? h->plan->split : parallel_outer(*h->k);

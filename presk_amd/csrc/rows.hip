@@ -1069,16 +1069,7 @@ template <int OP>
 hipError_t launch_walk(const RowArgs& a, hipStream_t stream) {
     constexpr bool SOFTMAX = OP == kSoftmax3 || OP == kSoftmax2 || OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2;
     if (OP == kMaskedSoftmax3 || OP == kMaskedSoftmax2) {
-        if (!a.mbits) return hipErrorInvalidValue;
-        const long long words = mask_words(a.n);
-        if (a.n % 8 == 0 && (uintptr_t)a.mask % 16 == 0) {
-            const dim3 grid((unsigned)((words * 4 + 255) / 256), (unsigned)a.mask_rows);
-            pack_mask8_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, (unsigned char*)a.mbits, a.n, words * 4);
-        } else {
-            const dim3 grid((unsigned)((a.n + 255) / 256), (unsigned)a.mask_rows);
-            pack_mask_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, a.mbits, a.n, words);
-        }
-        hipError_t e = hipGetLastError();
+        hipError_t e = rows_pack_mask(a, stream);
         if (e != hipSuccess) return e;
     }
     if constexpr (SOFTMAX) {
@@ -1145,6 +1136,19 @@ hipError_t launch_op(const RowArgs& a, hipStream_t stream) {
 }  // namespace
 
 long long rows_mask_words(long long n) { return mask_words(n); }
+
+hipError_t rows_pack_mask(const RowArgs& a, hipStream_t stream) {
+    if (!a.mbits || a.mask_rows <= 0) return hipErrorInvalidValue;
+    const long long words = mask_words(a.n);
+    if (a.n % 8 == 0 && (uintptr_t)a.mask % 16 == 0) {
+        const dim3 grid((unsigned)((words * 4 + 255) / 256), (unsigned)a.mask_rows);
+        pack_mask8_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, (unsigned char*)a.mbits, a.n, words * 4);
+    } else {
+        const dim3 grid((unsigned)((a.n + 255) / 256), (unsigned)a.mask_rows);
+        pack_mask_kernel<<<grid, 256, 0, stream>>>((const long long*)a.mask, a.mbits, a.n, words);
+    }
+    return hipGetLastError();
+}
 
 bool rows_need_mask_bits(const RowArgs& a) {
     return (a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2) && a.rows > 0 &&

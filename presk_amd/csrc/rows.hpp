@@ -26,6 +26,20 @@ struct RowArgs {
 
 hipError_t rows_launch(const RowArgs& a, hipStream_t stream);
 
+// The mask of a masked softmax packed to bits in `mbits` (rows_mask_words(n)
+// 32-bit words a mask row, bit c of a row its column c).
+hipError_t rows_pack_mask(const RowArgs& a, hipStream_t stream);
+
+// FAST mode's row nests (wrows.hip): the same nests with their sums in the
+// `lanes64-tree` order and FAST mode's exponential.  wrows_ok: the shape is
+// one it holds (the op, rows of at most 16 blocks a lane); wrows_vec: the
+// elements of a block (the order's block width); wrows_fits: also the
+// buffers' alignment for 16-byte blocks; a masked softmax needs `mbits`.
+bool wrows_ok(const RowArgs& a);
+int wrows_vec(const RowArgs& a);
+bool wrows_fits(const RowArgs& a);
+hipError_t wrows_launch(const RowArgs& a, hipStream_t stream);
+
 // Whether a launch of these arguments reads the mask as bits (a workspace
 // of mask_rows * mask_words(n) words the caller provides in `mbits`).
 bool rows_need_mask_bits(const RowArgs& a);

@@ -106,6 +106,62 @@ __device__ unsigned eval1(int fn, unsigned long long i) {
     }
 }
 
+// FAST mode's functions against the interpreter's (fn 50: expf, 51: erff):
+// the distance in units in the last place between the two results, the f32
+// bit patterns ordered as integers (-0 and +0 one point), two NaNs 0 apart
+// and a NaN from a number 2^32
+__device__ __forceinline__ long long ordered(unsigned b) {
+    const long long m = b & 0x7fffffffu;
+    return (b >> 31) ? -m : m;
+}
+__device__ unsigned long long ulp_distance(int fn, unsigned long long i) {
+    const float x = pk_float((unsigned)i);
+    float a, b;
+    if (fn == 50) {
+        a = pk_expf_fast(x);
+        b = pk_expf(x);
+    } else {
+        a = pk_erff_fast(x);
+        b = pk_erff(x);
+    }
+    if (a != a || b != b) return (a != a) == (b != b) ? 0ull : 1ull << 32;
+    const long long d = ordered(pk_bits(a)) - ordered(pk_bits(b));
+    return (unsigned long long)(d < 0 ? -d : d);
+}
+
+// the largest distance over [lo, lo + n) (fn 50, 51) or the count of inputs
+// at a nonzero distance (fn 60, 61)
+__global__ void __launch_bounds__(256) ulp_kernel(int fn, unsigned long long lo, unsigned long long n,
+                                                  unsigned long long per_thread, unsigned long long* out) {
+    const unsigned long long t = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool count = fn >= 60;
+    const int f = count ? fn - 10 : fn;
+    unsigned long long acc = 0;
+    const unsigned long long first = t * per_thread;
+    for (unsigned long long j = 0; j < per_thread; ++j) {
+        const unsigned long long k = first + j;
+        if (k >= n) break;
+        const unsigned long long d = ulp_distance(f, lo + k);
+        acc = count ? acc + (d != 0) : (d > acc ? d : acc);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_down(acc, off, 64);
+        acc = count ? acc + o : (o > acc ? o : acc);
+    }
+    __shared__ unsigned long long part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (count) {
+            atomicAdd(out, part[0] + part[1] + part[2] + part[3]);
+        } else {
+            unsigned long long m = part[0];
+            for (int q = 1; q < 4; ++q) m = part[q] > m ? part[q] : m;
+            atomicMax(out, m);
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long lo, unsigned long long n,
                                                      unsigned long long per_thread, unsigned long long* out) {
     const unsigned long long t = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -128,7 +184,8 @@ __global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long 
 }  // namespace
 
 hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
-    const int known[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33, 40, 41, 42, 43, 44, 45};
+    const int known[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33, 40, 41, 42, 43, 44, 45,
+                         50, 51, 60, 61};
     bool ok = false;
     for (int f : known) ok |= f == fn;
     if (!ok || hi < lo) return hipErrorInvalidValue;
@@ -140,7 +197,10 @@ hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
     const unsigned long long per_thread = 64, threads = (n + per_thread - 1) / per_thread;
     const unsigned long long blocks = (threads + 255) / 256;
     if (e == hipSuccess && n) {
-        digest_kernel<<<dim3((unsigned)blocks), dim3(256)>>>(fn, lo, n, per_thread, d);
+        if (fn >= 50)
+            ulp_kernel<<<dim3((unsigned)blocks), dim3(256)>>>(fn, lo, n, per_thread, d);
+        else
+            digest_kernel<<<dim3((unsigned)blocks), dim3(256)>>>(fn, lo, n, per_thread, d);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();

@@ -197,6 +197,14 @@ class Compiled:
         return buf.value.decode()
 
     def _table(self, ptrs):
+        # the KernelFn table has no length: every slot the kernel reads must
+        # be there (inputs, the output, the flag when guarded; scales of
+        # integer inputs come between), or the launch would read a pointer
+        # past the table's end
+        need = self.n_inputs + 1 + (1 if self.guarded else 0)
+        if len(ptrs) < need or any(not p for p in ptrs):
+            raise ValueError(f"a KernelFn table of {len(ptrs)} pointers for a kernel of {self.n_inputs} inputs"
+                             f"{' and a flag' if self.guarded else ''}: {need} or more non-null pointers needed")
         return (ctypes.c_void_p * len(ptrs))(*ptrs)
 
     def run(self, ptrs, lo=0, hi=None, stream=None):
@@ -261,6 +269,8 @@ class HipExec:
         """`KernelExec::run`: raises HipError E7007 when a narrowing store
         overflowed."""
         c = self.compiled(text, dtype, lanes)
+        if len(inputs) != c.n_inputs:
+            raise ValueError(f"{len(inputs)} input buffers for a kernel of {c.n_inputs} inputs")
         ptrs = [b.ptr for b in inputs] + [out.ptr]
         if c.guarded:
             self._flag.zero(stream)

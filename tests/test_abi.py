@@ -95,3 +95,27 @@ def test_graph_branches_checked_before_any_device_work():
             assert msg.startswith("E10001") and text in msg, msg
     finally:
         L.presk_hip_batch_release(b)
+
+
+def test_short_kernelfn_tables_refused_on_the_host():
+    """The KernelFn table carries no length (crates/presk-cranelift/src/
+    lib.rs:38-42), so the host binding checks it: a table missing an input
+    (a `sum_to` given no template operand) or holding a null pointer is
+    refused before any launch, instead of the plan reading its output slot
+    past the table's end."""
+    from presk_amd import lower as L
+    A, O = L.ax, L.Operand
+    low = L.sum_to([O(A(("batch", 64), ("seq", 256), ("model", 384))), O(A(("batch", 64), ("seq", 256)))], "f32")
+    c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+    assert c.kind == "rows" and c.n_inputs == 2 and c.order == "lanes64x4-tree"
+    with pytest.raises(ValueError, match="2 inputs"):
+        c.run([0x1000, 0x2000])
+    with pytest.raises(ValueError, match="non-null"):
+        c.run([0x1000, None, 0x3000])
+
+    class Buf:
+        ptr = 0x1000
+    ex = hip.HipExec.__new__(hip.HipExec)
+    ex.mode, ex._cache = hip.FAST, {}
+    with pytest.raises(ValueError, match="1 input buffers for a kernel of 2 inputs"):
+        ex.run(low.text, "f32", [Buf()], Buf())

@@ -66,8 +66,9 @@ def test_course_step_full_size(dt):
     bad = [k for k, v in got.items() if hashlib.sha256(np.ascontiguousarray(v).tobytes()).hexdigest() != table["sha256"][k]]
     assert not bad, f"{len(bad)} of {len(got)} buffers differ from the oracle's: {bad[:6]}"
     assert float(exact["loss"][0]) == table["loss_value"]
-    # the loss of uniform targets under a near-uniform head sits at ln V
-    assert abs(table["loss_value"] - np.log(gpt.COURSE.V)) < 0.05
+    # uniform targets under small logits (N(0, 0.02) weights): the loss sits
+    # near ln V, above it by about half the logits' variance
+    assert 0 <= table["loss_value"] - np.log(gpt.COURSE.V) < 0.2
     del p, got
     print(f"[fullsize] config 4 {dt}: FAST", flush=True)
     q, names = _course_step(dt, hip.FAST)

@@ -50,6 +50,10 @@ def cases():
         out.append((f"mean-{dt}", L.reduce_axis("mean", "vocab", [logits], dt), hip.EXACT, "rows"))
         out.append((f"cross_entropy-{dt}", L.cross_entropy([logits, ids], dt), hip.EXACT, "rows"))
         out.append((f"cross_entropy_vjp-{dt}", L.cross_entropy_vjp([logits, ids, rows], dt), hip.EXACT, "rows"))
+        # FAST's row nests (one wave a row, the lane-tree order)
+        out.append((f"masked_softmax_fast-{dt}", L.masked_softmax("seq2", [s, mask], dt), hip.FAST, "rows"))
+        out.append((f"mean_fast-{dt}", L.reduce_axis("mean", "vocab", [logits], dt), hip.FAST, "rows"))
+        out.append((f"cross_entropy_vjp_fast-{dt}", L.cross_entropy_vjp([logits, ids, rows], dt), hip.FAST, "rows"))
         xs = O(A(("batch", 7), ("seq", 60), ("model", 96)))
         out.append((f"sum_to-{dt}", L.sum_to([xs, O(A(("model", 96)))], dt), hip.FAST, "colsum"))
         out.append((f"embed_vjp-{dt}", L.embed_vjp([O(A(("vocab", 65), ("model", 96))), ids, xs], dt), hip.EXACT, "scatter"))

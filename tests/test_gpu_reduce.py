@@ -109,7 +109,7 @@ def test_rows_class_exact_long_and_many(dt):
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 def test_rows_class_exact_at_size(dt):
-    ex = hip.HipExec(0, mode=hip.FAST)
+    ex = hip.HipExec(0, mode=hip.EXACT)
     for name, low in _big_rows(dt):
         ins = zoo.inputs(low, seed=11, scale=3.0)
         if name == "masked_softmax" or name == "masked_softmax2":

@@ -108,3 +108,44 @@ def test_realization_order_reaches_every_contraction():
         llama.build(llama.TINY, "f32", mode=hip.EXACT, realize=r)
     with pytest.raises(ValueError, match="E7001"):
         Realization.of_json({"default": "f32", "order": {"kind": "spiral"}})
+
+
+def _lanes_tree_brute(row, vec):
+    """FAST's `lanes64xV-tree` from its definition, one row: lane l's
+    elements (blocks l, l + 64, ... of `vec` elements) summed in index order
+    from +0, then the 64 lane sums added by recursive halving of the lane
+    range [0, 64)."""
+    f = np.float32
+    lane = [f(0.0)] * 64
+    for e, x in enumerate(row):
+        l = (e // vec) % 64
+        lane[l] = f(lane[l] + f(x))
+
+    def tree(lo, hi):
+        if hi - lo == 1:
+            return lane[lo]
+        mid = (lo + hi) // 2
+        return f(tree(lo, mid) + tree(mid, hi))
+    return tree(0, 64)
+
+
+@pytest.mark.parametrize("vec,n", [(4, 384), (8, 768), (8, 4096), (1, 65), (4, 8), (8, 2048), (1, 200)])
+def test_lanes_tree_order_restatement(vec, n):
+    """oracle/lanes.py's vectorized butterfly = the order written from its
+    definition (a recursive tree over the lane sums), bit for bit, on rows
+    whose terms span 2^20 in magnitude (so that orders differ); and both
+    within n u sum|x| of the exact sum."""
+    import math
+    from oracle.lanes import lanes_tree_sum
+    rng = np.random.default_rng(n + vec)
+    x = (rng.standard_normal((6, n)) * np.exp2(rng.integers(-10, 10, (6, n)))).astype(np.float32)
+    got = lanes_tree_sum(x, vec)
+    for r in range(6):
+        assert got[r] == _lanes_tree_brute(x[r], vec), (r, got[r], _lanes_tree_brute(x[r], vec))
+        exact = math.fsum(float(v) for v in x[r])
+        assert abs(float(got[r]) - exact) <= (n + 64) * 2.0 ** -24 * float(np.abs(x[r].astype(np.float64)).sum())
+    # an order, not the sequential one: some row differs from the in-order sum
+    seq = np.zeros(6, np.float32)
+    for e in range(n):
+        seq = seq + x[:, e]
+    assert n <= 8 or np.any(seq != got)
