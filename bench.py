@@ -352,9 +352,10 @@ def per_launch_table(p, path, ring_mb: float = 768.0):
         head = ln.low.text.split("{")[0].strip()
         e = agg.setdefault(head, [0, 0.0, ln, 1])
         e[0] += 1
-    for head, e in agg.items():
+    for i, (head, e) in enumerate(agg.items()):
         ms, r = _rotated_ms(e[2], ring_mb * 1e6)
         e[1], e[3] = ms * e[0], r
+        print(f"[per-launch] {i + 1}/{len(agg)} {ms * 1e3:.1f} us over {r} copies: {head[:90]}", file=sys.stderr, flush=True)
     total = sum(e[1] for e in agg.values())
     rows = ["| launch (kernel text's head) | class, order | launches | copies | us each | us a step | MB | GB/s | % of HBM | TFLOP/s | % of MFMA |",
             "|---|---|---|---|---|---|---|---|---|---|---|"]
