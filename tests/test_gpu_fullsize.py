@@ -5,7 +5,10 @@ loss, the logits and every parameter gradient equal the oracle's run of the
 same program byte for byte (their digests, computed once by the oracle in
 tests/golden/make_fullsize.py, since the oracle takes minutes at this size);
 in FAST mode the loss and every gradient lie within the bands the TINY step
-is held to, of the EXACT run.  At this size the weight gradients' K is
+is held to, of the EXACT run -- except, in bf16, the gradients that are sums
+over the tokens (biases, gains), which the nest accumulates in its bf16
+output (rounded at every step) and FAST in f32 chunk sums: those against the
+float64 sum of the FAST run's own inputs.  At this size the weight gradients' K is
 16 384 (split across workgroups), the masked softmax's rows are 256 long,
 and every contraction fills many MFMA tiles -- the plans the TINY program
 never reaches.
@@ -79,15 +82,32 @@ def test_course_step_full_size(dt):
     tol = 1e-5 if dt == "f32" else 2e-2
     assert abs(loss - want) <= tol * abs(want), (loss, want)
     floor = 1e-3 * max(np.max(np.abs(v)) for k, v in exact.items() if k != "loss")
-    worst = []
+    producer = {ln.out: ln for ln in q.launches}
+    worst, sums = [], 0
     for n, buf in names["grads"].items():
         g = fmt.decode(q.bufs.download(buf), dt).astype(np.float64)
-        ref = exact["d." + n]
         assert np.all(np.isfinite(g)), n
+        ln = producer[buf]
+        if dt == "bf16" and ln.low.name == "sum_to":
+            # a bias's or a gain's gradient: a sum over the 16 384 tokens.  The
+            # nest's running sum lives in its bf16 output, rounded at every
+            # step (EXACT does that), which FAST's chunk sums in f32 do not,
+            # so these are held to the float64 sum of the FAST run's own
+            # input instead: within the chunked f32 order's band and one
+            # bf16 rounding
+            x = fmt.decode(q.bufs.download(ln.ins[0]), dt).astype(np.float64).reshape(-1, g.size)
+            ex_sum, S = x.sum(axis=0), np.abs(x).sum(axis=0)
+            bound = (64 + x.shape[0] // 64) * 2.0 ** -24 * S + 2.0 ** -8 * np.abs(ex_sum) + 1e-30
+            assert np.all(np.abs(g - ex_sum) <= bound), (n, np.max(np.abs(g - ex_sum) / bound))
+            sums += 1
+            continue
+        ref = exact["d." + n]
         err = np.max(np.abs(g - ref)) / max(np.max(np.abs(ref)), floor)
         worst.append((err, n))
         assert err < (1e-4 if dt == "f32" else 6e-2), (n, err)
-    print(f"[fullsize] config 4 {dt}: loss {loss} (EXACT {want}); worst gradient {max(worst)}; {splits}", flush=True)
+    assert dt == "f32" or sums > 20
+    print(f"[fullsize] config 4 {dt}: loss {loss} (EXACT {want}); worst gradient {max(worst)}; {sums} sums against "
+          f"float64; {splits}", flush=True)
 
 
 # ---- config 5 --------------------------------------------------------------------
