@@ -119,7 +119,16 @@ struct GemmPlan : ClassPlan {
     // (the first batch axis), rows_per_iter rows of M, or cols_per_iter
     // columns of N (an `ein` whose first output axis is J)
     bool split_on_batch = false;
-    bool e8 = false;               // e8m15 storage: f32 products of the exact widenings
+    // operands multiplied on the f32 kernel from f32 copies (e8m15 codes,
+    // integer weights, and the 16-bit operand beside an integer one): conv[i]
+    // the WidenArgs kind of operand i (0: used as it is), wq[i] its integer
+    // layout; `narrow` the output's storage when the f32 sums are stored
+    // into it afterwards (kBF16, kF16, or 3 for e8m15), else -1
+    int conv[2] = {0, 0};
+    WidenArgs wq[2] = {};
+    int scale_slot[2] = {-1, -1};
+    int narrow = -1;
+    int flag_slot = 0;
     long long numel_in[2] = {0, 0}, numel_out = 0;
     bool swapped = false;          // operand 1 is A (an `ein` whose operand 1 carries I)
     long long rows_per_iter = 0;
@@ -133,14 +142,15 @@ struct GemmPlan : ClassPlan {
         if (g.splits > 1) o += "-split" + std::to_string(g.splits);
         return o;
     }
-    // e8m15: the operands' and the output's f32 copies, each 256-byte
+    // the converted operands' and the output's f32 copies, each 256-byte
     // aligned; then the split-K partials, [splits][M][N] in f32
     static size_t up256(size_t n) { return (n + 255) / 256 * 256; }
-    size_t e8_bytes() const {
-        return e8 ? up256(4 * (size_t)numel_in[0]) + up256(4 * (size_t)numel_in[1]) + up256(4 * (size_t)numel_out) : 0;
+    size_t wide_bytes() const {
+        return (conv[0] ? up256(4 * (size_t)numel_in[0]) : 0) + (conv[1] ? up256(4 * (size_t)numel_in[1]) : 0) +
+               (narrow >= 0 ? up256(4 * (size_t)numel_out) : 0);
     }
     size_t workspace_bytes() const override {
-        return e8_bytes() + (g.splits > 1 ? (size_t)g.splits * (size_t)g.M * (size_t)g.N * sizeof(float) : 0);
+        return wide_bytes() + (g.splits > 1 ? (size_t)g.splits * (size_t)g.M * (size_t)g.N * sizeof(float) : 0);
     }
 
     hipError_t launch(void* const* bufs, int64_t lo, int64_t hi, void* work, hipStream_t stream) const override {
@@ -152,26 +162,37 @@ struct GemmPlan : ClassPlan {
         a.B = bufs[swapped ? 0 : 1];
         a.bias = epilogue ? bufs[2] : nullptr;
         a.C = bufs[n_in];
-        a.flag = guarded ? (unsigned*)bufs[n_in + 1] : nullptr;
-        // e8m15: the kernel multiplies exact f32 widenings of the operands
-        // into an f32 copy of the output, which is narrowed afterwards
-        unsigned char* e8_out = nullptr;
-        const unsigned char* e8_bias = nullptr;
-        if (e8) {
+        a.flag = guarded ? (unsigned*)bufs[flag_slot] : nullptr;
+        // operands of other types: f32 copies (exact widenings, or the
+        // integer weights' loads), the f32 kernel into an f32 copy of the
+        // output where its storage is narrower, narrowed afterwards
+        unsigned char* n_out = nullptr;
+        const unsigned char* n_bias = nullptr;
+        if (conv[0] || conv[1] || narrow >= 0) {
             if (!work) return hipErrorInvalidValue;
-            float* const w0 = (float*)work;
-            float* const w1 = (float*)((char*)work + up256(4 * (size_t)numel_in[0]));
-            float* const wc = (float*)((char*)w1 + up256(4 * (size_t)numel_in[1]));
-            hipError_t e = gemm_e8_widen(bufs[0], w0, numel_in[0], stream);
-            if (e == hipSuccess) e = gemm_e8_widen(bufs[1], w1, numel_in[1], stream);
-            if (e != hipSuccess) return e;
-            a.A = swapped ? w1 : w0;
-            a.B = swapped ? w0 : w1;
-            e8_out = (unsigned char*)a.C;
-            e8_bias = (const unsigned char*)a.bias;
-            a.C = wc;
-            a.bias = nullptr;
-            work = (char*)work + e8_bytes();
+            char* w = (char*)work;
+            const void* op[2] = {bufs[0], bufs[1]};
+            for (int i = 0; i < 2; ++i) {
+                if (!conv[i]) continue;
+                WidenArgs x = wq[i];
+                x.src = bufs[i];
+                x.dst = (float*)w;
+                x.n = numel_in[i];
+                x.kind = conv[i];
+                x.scales = conv[i] >= 4 ? (const float*)bufs[scale_slot[i]] : nullptr;
+                if (hipError_t e = gemm_widen(x, stream); e != hipSuccess) return e;
+                op[i] = w;
+                w += up256(4 * (size_t)numel_in[i]);
+            }
+            a.A = op[swapped ? 1 : 0];
+            a.B = op[swapped ? 0 : 1];
+            if (narrow >= 0) {
+                n_out = (unsigned char*)a.C;
+                n_bias = (const unsigned char*)a.bias;
+                a.C = w;
+                a.bias = nullptr;
+            }
+            work = (char*)work + wide_bytes();
         }
         const int esz = storage == kF32 ? 4 : 2;
         // a partial range: the same tiles, k-blocks and split of K as the
@@ -203,8 +224,9 @@ struct GemmPlan : ClassPlan {
             }
             a.C = (char*)a.C + c_off * esz;
             if (a.bias) a.bias = (const char*)a.bias + bias_off * esz;
-            if (e8_out) e8_out += 3 * c_off;
-            if (e8_bias) e8_bias += 3 * bias_off;
+            const int nsz = narrow == 3 ? 3 : 2;   // the narrowed output's element bytes
+            if (n_out) n_out += nsz * c_off;
+            if (n_bias) n_bias += nsz * bias_off;
         }
         // the clamped 16-byte loads need whole aligned vectors along the
         // loaded axis: k when it is contiguous, else the rows
@@ -223,13 +245,14 @@ struct GemmPlan : ClassPlan {
             if (!work) return hipErrorInvalidValue;
             a.work = (float*)work;
         }
-        if (!e8) return gemm_launch(a, stream);
+        if (narrow < 0) return gemm_launch(a, stream);
         unsigned* const flag = a.flag;
         a.flag = nullptr;
         hipError_t e = gemm_launch(a, stream);
         if (e != hipSuccess) return e;
         a.flag = flag;
-        return gemm_e8_narrow(a, e8_out, e8_bias, stream);
+        if (narrow == 3) return gemm_e8_narrow(a, n_out, n_bias, stream);
+        return gemm_narrow16(a, narrow, n_out, n_bias, stream);
     }
 };
 
@@ -392,17 +415,43 @@ std::unique_ptr<ClassPlan> classify_gemm(const Kernel& k) {
     const bool is_l = n == "dot_vjp_l", is_r = n == "dot_vjp_r";
     const bool is_ein = n.compare(0, 4, "ein[") == 0;
     if (!(is_dot || is_l || is_r || is_ein)) return nullptr;
-    // e8m15 storage runs as f32 on the exact widenings of its codes
+    // e8m15 storage runs as f32 on the exact widenings of its codes; an
+    // integer weight (a Quant operand) as f32 on its loads f32(q) * s, the
+    // other operand widened exactly
     const bool e8 = k.dtype == Ty::E8M15;
-    const int st = e8 ? kF32 : storage_of(k.dtype);
-    if (st < 0 || k.output.ty != k.dtype) return nullptr;
-    for (auto& b : k.inputs)
-        if (b.ty != k.dtype) return nullptr;       // indices or widened parameters: generic
+    const bool quant = k.n_quant() > 0;
+    const int own = e8 ? kF32 : storage_of(k.dtype);
+    if (own < 0 || k.output.ty != k.dtype) return nullptr;
     const bool epi = n == "dot+add";
     if ((int)k.inputs.size() != (epi ? 3 : 2)) return nullptr;
+    for (size_t i = 0; i < k.inputs.size(); ++i) {
+        const Ty t = k.inputs[i].ty;
+        // indices or widened parameters: generic; a Quant bias too
+        if (t != k.dtype && !(i < 2 && ty_quant(t))) return nullptr;
+        if (k.inputs[i].wide) return nullptr;
+    }
+    const bool wide = e8 || quant;
+    const int st = wide ? kF32 : own;
     const BufSpec &x = k.inputs[0], &w = k.inputs[1], &o = k.output;
     auto p = std::make_unique<GemmPlan>();
-    p->e8 = e8;
+    p->flag_slot = k.flag_slot();
+    for (int i = 0; i < 2; ++i) {
+        const BufSpec& b = k.inputs[i];
+        if (ty_quant(b.ty)) {
+            p->conv[i] = b.ty == Ty::Q8 ? 4 : 5;
+            p->scale_slot[i] = k.scale_slot(i);
+            const auto ss = b.scale_strides();
+            if (b.dims.empty() || b.dims.size() > 8 || ss.size() != b.dims.size()) return nullptr;
+            p->wq[i].ndims = (int)b.dims.size();
+            for (size_t d = 0; d < b.dims.size(); ++d) {
+                p->wq[i].dims[d] = b.dims[d];
+                p->wq[i].sstride[d] = ss[d];
+            }
+        } else if (wide) {
+            p->conv[i] = k.dtype == Ty::BF16 ? 1 : k.dtype == Ty::F16 ? 2 : k.dtype == Ty::E8M15 ? 3 : 0;
+        }
+    }
+    if (wide && k.dtype != Ty::F32) p->narrow = e8 ? 3 : own;
     p->numel_in[0] = x.numel();
     p->numel_in[1] = w.numel();
     p->numel_out = o.numel();
@@ -889,9 +938,10 @@ std::unique_ptr<ClassPlan> classify_scatter(const Kernel& k) {
 }
 
 std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode) {
-    // integer weights (their scales in the slots after the output): the
-    // generic printer's loads
-    if (k.n_quant() > 0) return nullptr;
+    // integer weights (their scales in the slots after the output): in
+    // FAST a contraction takes the f32 MFMA kernel on their loads, anything
+    // else the generic printer's loads
+    if (k.n_quant() > 0) return mode == PRESK_HIP_FAST ? classify_gemm(k) : nullptr;
     // FAST: column sums and totals in the declared chunked order
     if (mode == PRESK_HIP_FAST)
         if (auto p = classify_sum_to(k)) return p;

@@ -956,7 +956,75 @@ __global__ void __launch_bounds__(256) e8_narrow_kernel(GemmArgs g, unsigned cha
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
 
+__global__ void __launch_bounds__(256) widen_kernel(WidenArgs w) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= w.n) return;
+    float v;
+    if (w.kind == 1) {
+        v = pk_bf16_to_f32(((const unsigned short*)w.src)[i]);
+    } else if (w.kind == 2) {
+        v = pk_f16_to_f32(((const unsigned short*)w.src)[i]);
+    } else if (w.kind == 3) {
+        v = pk_e8m15_to_f32(pk_ld24((const unsigned char*)w.src, i));
+    } else {
+        // the element's scale: its index with the span axes' strides zero
+        long long rest = i, s = 0;
+        for (int d = w.ndims - 1; d >= 0; --d) {
+            const long long q = rest / w.dims[d];
+            s += (rest - q * w.dims[d]) * w.sstride[d];
+            rest = q;
+        }
+        const int q = w.kind == 4 ? (int)((const signed char*)w.src)[i] : pk_nibble((const unsigned char*)w.src, i);
+        v = (float)q * w.scales[s];
+    }
+    w.dst[i] = v;
+}
+
+template <int ST>
+__global__ void __launch_bounds__(256) narrow16_kernel(GemmArgs g, unsigned short* __restrict__ out,
+                                                       const unsigned short* __restrict__ bias) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= g.batch * g.M * g.N) return;
+    const long long n = idx % g.N, m = (idx / g.N) % g.M, b = idx / (g.N * g.M);
+    const long long off = batch_offset(g, b, g.sc_b) + m * g.sc_m + n;
+    const float sum = ((const float*)g.C)[off];
+    bool ovf = false;
+    auto narrow = [&](float v) -> unsigned short {
+        if (ST == kBF16) return pk_f32_to_bf16(v);
+        ovf |= pk_overflows_f16(v);
+        return pk_f32_to_f16(v);
+    };
+    auto widen = [](unsigned short h) { return ST == kBF16 ? pk_bf16_to_f32(h) : pk_f16_to_f32(h); };
+    unsigned short h = narrow(sum);
+    if (bias) {
+        const long long bo = g.bias_kind == 1 ? n : g.bias_kind == 2 ? m * g.N + n : 0;
+        h = narrow(widen(h) + widen(bias[bo]));
+    }
+    out[off] = h;
+    if (ovf && g.flag) atomicOr(g.flag, 1u);
+}
+
 }  // namespace
+
+hipError_t gemm_widen(const WidenArgs& w, hipStream_t stream) {
+    if (w.n <= 0) return hipSuccess;
+    if (w.kind < 1 || w.kind > 5 || (w.kind >= 4 && (!w.scales || w.ndims < 1 || w.ndims > 8))) return hipErrorInvalidValue;
+    widen_kernel<<<(unsigned)((w.n + 255) / 256), 256, 0, stream>>>(w);
+    return hipGetLastError();
+}
+
+hipError_t gemm_narrow16(const GemmArgs& g, int st, void* out, const void* bias, hipStream_t stream) {
+    const long long n = g.batch * g.M * g.N;
+    if (n <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (st == kBF16)
+        narrow16_kernel<kBF16><<<grid, 256, 0, stream>>>(g, (unsigned short*)out, (const unsigned short*)bias);
+    else if (st == kF16)
+        narrow16_kernel<kF16><<<grid, 256, 0, stream>>>(g, (unsigned short*)out, (const unsigned short*)bias);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
 
 hipError_t gemm_e8_widen(const void* src, float* dst, long long n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;

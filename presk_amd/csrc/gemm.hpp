@@ -41,6 +41,26 @@ hipError_t gemm_e8_widen(const void* src, float* dst, long long n, hipStream_t s
 // the f32 sum at g.C rounded (overflow guard at g.flag), then, with a bias,
 // read back, the bias added in f32 and rounded again (lower.rs:1053-1060)
 hipError_t gemm_e8_narrow(const GemmArgs& g, void* out, const void* bias, hipStream_t stream);
+// Operands multiplied on the f32 kernel from f32 copies: `kind` 1 bf16 and
+// 2 f16 values widened exactly, 3 e8m15 codes widened exactly, 4 int8 and 5
+// int4 integer weights loaded as a Quant input is (f32(q) * s, one f32
+// multiplication, crates/presk-rt/src/quant.rs:248-252), the scale of
+// element ix at sum ix_a * sstride_a over the buffer's `ndims` axes.
+struct WidenArgs {
+    const void* src;
+    float* dst;
+    long long n;
+    int kind;
+    const float* scales;
+    int ndims;
+    long long dims[8], sstride[8];
+};
+hipError_t gemm_widen(const WidenArgs& w, hipStream_t stream);
+// the bf16 or f16 (`st`) output of every element g's M, N and batch cover:
+// the f32 sum at g.C stored rounded (the guard at g.flag for f16), then,
+// with a bias, read back, the bias added in f32 and rounded again
+// (lower.rs:1053-1060)
+hipError_t gemm_narrow16(const GemmArgs& g, int st, void* out, const void* bias, hipStream_t stream);
 int gemm_block_k(int storage);
 int gemm_tile_m();
 int gemm_tile_m_of(const GemmArgs& g);

@@ -191,15 +191,21 @@ __global__ void __launch_bounds__(64 * WAVES) wrows_kernel(RowArgs a) {
             for (int i = 0; i < VEC; ++i)
                 if ((allow[j] >> i) & 1u) m = __builtin_fmaxf(m, v[j][i]);
         m = lanes_max(m);
-        // every allowed element's exponential, their sum in the declared order
+        // every allowed element's exponential, their sum in the declared
+        // order; a block with no allowed element holds zeros already, and
+        // adding them to a sum of nonnegative terms changes no bit, so its
+        // lanes skip it (a wave skips a block no lane's row allows: a causal
+        // mask's upper triangle)
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < CH; ++j)
+            if (allow[j]) {
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-                const float e = (allow[j] >> i) & 1u ? pk_expf_fast(v[j][i] - m) : 0.0f;
-                v[j][i] = e;
-                s = s + e;
+                for (int i = 0; i < VEC; ++i) {
+                    const float e = (allow[j] >> i) & 1u ? pk_expf_fast(v[j][i] - m) : 0.0f;
+                    v[j][i] = e;
+                    s = s + e;
+                }
             }
         const float z = lanes_sum(s);
         if constexpr (KIND == 1) {
@@ -210,10 +216,15 @@ __global__ void __launch_bounds__(64 * WAVES) wrows_kernel(RowArgs a) {
                 const long long b = (long long)j * 64 + lane;
                 if (b >= nb) continue;
                 float o[VEC];
+                if (allow[j]) {
 #pragma unroll
-                for (int i = 0; i < VEC; ++i)
-                    // the two-pass nest divides the stored exponential
-                    o[i] = (allow[j] >> i) & 1u ? q(two ? stored<ST>(v[j][i]) : v[j][i]) : 0.0f;
+                    for (int i = 0; i < VEC; ++i)
+                        // the two-pass nest divides the stored exponential
+                        o[i] = (allow[j] >> i) & 1u ? q(two ? stored<ST>(v[j][i]) : v[j][i]) : 0.0f;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i) o[i] = 0.0f;
+                }
                 stv<ST, VEC>(a.out, base + b * VEC, o, ovf);
             }
         } else if constexpr (KIND == 2) {

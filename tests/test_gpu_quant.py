@@ -2,8 +2,11 @@
 bit: a contraction reading int8 or int4 weights with one f32 scale per
 channel, the stored axis kept by the kernel's view or split into two axes
 (span 2), scalar loads and the tiled layout's vector loads (f32, 4 lanes),
-in every storage type's arithmetic, EXACT and FAST (the generic printer's
-loads either way).  The scales ride in the slot after the output, the
+in every storage type's arithmetic: EXACT through the generic printer's
+loads, bit for bit; FAST on the f32 MFMA kernel from the weights' loads
+(f32(q) * s into an f32 copy, the other operand widened exactly, the f32
+sums stored into the storage type afterwards with the epilogue), within the
+band of two f32 orders of the same sums.  The scales ride in the slot after the output, the
 overflow flag after them (crates/presk-cranelift/src/lib.rs:1609-1629)."""
 import ctypes
 
@@ -45,7 +48,7 @@ def test_integer_weights_exact(dt, bits, span, J, mode):
     print(f"[quant] {dt} int{bits} span {span} J {J} mode {mode} lanes {low.lanes}", flush=True)
     want, flag = cexec.run(text, dt, [x, (qt.data, qt.scales)], lanes=low.lanes)
     c = hip.Compiled(text, dt, low.lanes, mode)
-    assert c.kind == "generic"
+    assert c.kind == ("generic" if mode == hip.EXACT else "gemm"), c.kind
     bx, bq, bs = hip.DeviceBuffer.of(x), hip.DeviceBuffer.of(qt.data), hip.DeviceBuffer.of(qt.scales)
     out = hip.DeviceBuffer(want.nbytes)
     out.upload(np.full(want.nbytes, 0xFF, np.uint8))
@@ -54,9 +57,25 @@ def test_integer_weights_exact(dt, bits, span, J, mode):
     ptrs = [bx.ptr, bq.ptr, out.ptr, bs.ptr] + ([f.ptr] if c.guarded else [])
     c.run(ptrs)
     hip.sync()
-    assert out.download(want.dtype).tobytes() == want.tobytes()
+    got = out.download(want.dtype)
     if c.guarded:
         assert bool(f.download(np.uint32, 1)[0]) == flag
+    if mode == hip.EXACT:
+        assert got.tobytes() == want.tobytes()
+        return
+    assert c.order == "mfma-f32-k4", c.order
+    # two f32 orders of the same K products of the loads: 2 gamma_K S, plus
+    # one unit of the storage type for the sum and the result
+    xs = fmt.decode(x, dt).astype(np.float64).reshape(50, -1)
+    wv = qt.dequantize().astype(np.float64).reshape(xs.shape[1], -1)
+    K = xs.shape[1]
+    S = np.abs(xs) @ np.abs(wv)
+    g = fmt.decode(got, dt).astype(np.float64).reshape(S.shape)
+    r = fmt.decode(want, dt).astype(np.float64).reshape(S.shape)
+    unit = {"f32": 2.0 ** -23, "bf16": 2.0 ** -7, "f16": 2.0 ** -10, "e8m15": 2.0 ** -15}[dt]
+    gamma = K * 2.0 ** -24 / (1 - K * 2.0 ** -24)
+    bound = 2 * gamma * S + unit * (S + 2 * np.maximum(np.abs(r), np.abs(g))) + 1e-30
+    assert np.all(np.abs(g - r) <= bound), np.max(np.abs(g - r) / bound)
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
