@@ -246,8 +246,11 @@ int presk_hip_fill_normal(void *dst, const char *type, int64_t n, uint64_t seed,
  * fn 50 (expf) and 51 (erff) the result is instead the largest distance in
  * units in the last place between FAST mode's function and the
  * interpreter's over the inputs, and for fn 60 / 61 the count of inputs
- * where the two differ.  No counterpart in the reference; for the
- * exhaustive device checks. */
+ * where the two differ; fn 70-77 count the f32 dividends (the inputs' bit
+ * patterns) whose quotient by one of eight fixed divisors through the
+ * printed nests' division by a constant differs from the correctly rounded
+ * division.  No counterpart in the reference; for the exhaustive device
+ * checks. */
 int presk_hip_scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t *digest);
 
 #ifdef __cplusplus

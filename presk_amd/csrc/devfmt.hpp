@@ -409,6 +409,20 @@ PK_DEV float pk_erff(float x) {
     return neg ? -y : y;
 }
 
+// ---- division by a constant ------------------------------------------------------
+// a / c for f32 a and a finite nonzero f32 constant c, given rc = RN64(1/c):
+// the f64 product a * rc rounded to f32.  It is the correctly rounded f32
+// quotient for every a: the product is within 2^-52 of a/c relative (two
+// f64 roundings); a quotient that is not a midpoint of the f32 grid
+// (subnormal grid included) lies more than 2^-49 relative from every
+// midpoint (a - m c is a nonzero multiple of the grid of a or of m c), so
+// the product rounds to the same f32; a quotient that is a midpoint has at
+// most 25 significant bits, so the product, within half an f64 ulp of it,
+// is it exactly and rounds as it does.  Pinned on the device against the
+// division over every f32 dividend for a set of divisors
+// (presk_hip_scalar_digest fn 70-77).
+PK_DEV float pk_div_rc(float a, double rc) { return (float)((double)a * rc); }
+
 // ---- FAST mode's functions ------------------------------------------------------
 // Not the interpreter's bits: FAST mode's exponential and error function, each
 // within a bound stated against musl's (the functions above) and measured on
@@ -431,24 +445,36 @@ PK_DEV float pk_expf_fast(float x) {
 }
 
 // erf(x): x P(x^2) below |x| = 1 (P of degree 5, a relative minimax fit of
-// erf(sqrt z)/sqrt z on [0, 1]), else 1 - e^(-x^2 + G(|x|)) with G of degree
-// 8 in |x| - 2.5 fitted to log(erfc(u)) + u^2 on [1, 4] (|x| clamped to 4,
-// where 1 - erfc already rounds to 1), the sign restored; both branches
-// evaluated and one chosen, so a wave runs no divergent paths.
+// erf(sqrt z)/sqrt z on [0, 1]), else 1 - 2^t, t = -u^2 log2 e + G2(u), with
+// G2 of degree 8 in u - 2.5 (log2 e times a fit of log(erfc(u)) + u^2 on
+// [1, 4]) and u = |x| clamped to 4, where 1 - erfc already rounds to 1; the
+// sign restored.  Both polynomials by fma Horner steps; 2^t by v_exp_f32
+// alone (t in [-24, -2.6], a normal result below 0.16, so its error moves
+// 1 - 2^t by well under an ulp).  Both branches are evaluated and one
+// chosen, so a wave runs no divergent paths; a NaN takes the first
+// branch, which returns it quieted.
 PK_DEV float pk_erff_fast(float x) {
     const float u = __builtin_fabsf(x);
     const float z = x * x;
-    const float p = 1.12837911e+0f + z * (-3.76123250e-1f + z * (1.12801798e-1f + z * (-2.67113112e-2f +
-                    z * (4.91755083e-3f + z * -5.63141890e-4f))));
+    float p = __builtin_fmaf(z, -5.63141890e-4f, 4.91755083e-3f);
+    p = __builtin_fmaf(z, p, -2.67113112e-2f);
+    p = __builtin_fmaf(z, p, 1.12801798e-1f);
+    p = __builtin_fmaf(z, p, -3.76123250e-1f);
+    p = __builtin_fmaf(z, p, 1.12837911e+0f);
     const float small = x * p;
-    const float s = __builtin_fminf(u, 4.0f) - 2.5f;
-    const float g = -1.55681527e+0f + s * (-3.52680683e-1f + s * (5.61063923e-2f + s * (-1.08584873e-2f +
-                    s * (2.16508145e-3f + s * (-4.20173135e-4f + s * (7.74549189e-5f + s * (-1.33017093e-5f +
-                    s * 1.59981914e-6f)))))));
     const float uc = __builtin_fminf(u, 4.0f);
-    const float large = __builtin_copysignf(1.0f - pk_expf_fast(__builtin_fmaf(-uc, uc, g)), x);
-    const float y = u < 1.0f ? small : large;
-    return x != x ? x + x : y;
+    const float s = uc - 2.5f;
+    float g = __builtin_fmaf(s, 2.308051080e-06f, -1.919030910e-05f);
+    g = __builtin_fmaf(s, g, 1.117438296e-04f);
+    g = __builtin_fmaf(s, g, -6.061816821e-04f);
+    g = __builtin_fmaf(s, g, 3.123552306e-03f);
+    g = __builtin_fmaf(s, g, -1.566548645e-02f);
+    g = __builtin_fmaf(s, g, 8.094441146e-02f);
+    g = __builtin_fmaf(s, g, -5.088106990e-01f);
+    g = __builtin_fmaf(s, g, -2.246009588e+00f);
+    const float t = __builtin_fmaf(-(uc * 1.44269502e+0f), uc, g);
+    const float large = __builtin_copysignf(1.0f - __builtin_amdgcn_exp2f(t), x);
+    return u >= 1.0f ? large : small;
 }
 
 // ---- sinf / cosf: fdlibm's method in f64 (presk_libm.c:672-746 the

@@ -143,6 +143,24 @@ struct Printer {
         return it == pre.end() ? "" : "pre" + std::to_string(it->second) + "[u]";
     }
 
+    // a / c in f32 arithmetic, c a finite nonzero constant: the quotient
+    // rounded once from the f64 product a * RN64(1/c), which equals the
+    // correctly rounded f32 quotient for every a (the product is within
+    // 2^-52 of a/c relative, a quotient that is not a midpoint of the f32
+    // grid lies at least 2^-49 relative from the nearest one, and one that
+    // is, a double of at most 25 bits, is the product's rounding exactly);
+    // pk_div_rc's three full-rate instructions in place of the division's
+    // sequence.  "" where the form does not apply, and for a power of two,
+    // whose exact product the compiler makes itself.
+    std::string div_by_const(const Expr* e, const std::string& a, const Expr* den = nullptr) const {
+        if (!den) den = e->kids[1];
+        if (e->op != Op::Div || A != "float" || den->kind != Expr::Num) return "";
+        const float c = (float)den->num;
+        int ex = 0;
+        if (!std::isfinite(c) || c == 0.0f || std::fabs(std::frexp(c, &ex)) == 0.5f) return "";
+        return "pk_div_rc(" + a + ", " + hexlit(1.0 / (double)c) + ")";
+    }
+
     std::string real(const Expr* e) {
         switch (e->kind) {
             case Expr::Num: return "((" + A + ")" + hexlit(e->num) + ")";
@@ -162,7 +180,9 @@ struct Printer {
             case Expr::Iv: case Expr::Si: return "((" + A + ")(double)(" + intx(e) + "))";
             case Expr::Bin: {
                 static const char* ops[] = {"+", "-", "*", "/"};
-                return "(" + real(e->kids[0]) + " " + ops[(int)e->op] + " " + real(e->kids[1]) + ")";
+                const std::string a = real(e->kids[0]);
+                if (const std::string d = div_by_const(e, a); !d.empty()) return d;
+                return "(" + a + " " + ops[(int)e->op] + " " + real(e->kids[1]) + ")";
             }
             case Expr::Unary: {
                 std::string a = real(e->kids[0]);
@@ -246,7 +266,10 @@ struct Printer {
             case Expr::Splat: return real(e->kids[0]);
             case Expr::VBin: {
                 static const char* ops[] = {"+", "-", "*", "/"};
-                return "(" + vec(e->kids[0]) + " " + ops[(int)e->op] + " " + vec(e->kids[1]) + ")";
+                const Expr* den = e->kids[1]->kind == Expr::Splat ? e->kids[1]->kids[0] : e->kids[1];
+                const std::string a = vec(e->kids[0]);
+                if (const std::string d = div_by_const(e, a, den); !d.empty()) return d;
+                return "(" + a + " " + ops[(int)e->op] + " " + vec(e->kids[1]) + ")";
             }
             default: return real(e);
         }

@@ -114,8 +114,31 @@ __device__ __forceinline__ long long ordered(unsigned b) {
     const long long m = b & 0x7fffffffu;
     return (b >> 31) ? -m : m;
 }
+// the divisors of the division scans (fn 70-77): sqrt 2 and sqrt(2 pi) as
+// GELU and its derivative divide by them, small odd parts, a significand of
+// all ones, a subnormal, a large and a small magnitude
+__device__ float scan_divisor(int k) {
+    switch (k) {
+        case 0: return 0x1.6a09e6p+0f;
+        case 1: return 0x1.40d932p+1f;
+        case 2: return 3.0f;
+        case 3: return 0x1.99999ap-4f;
+        case 4: return 0x1.fffffep+0f;
+        case 5: return 0x1.16c2p-133f;
+        case 6: return 0x1.2eec2ep+101f;
+        default: return -6.0f;
+    }
+}
 __device__ unsigned long long ulp_distance(int fn, unsigned long long i) {
     const float x = pk_float((unsigned)i);
+    if (fn >= 70) {
+        // pk_div_rc against the correctly rounded division: 1 where the bits
+        // differ (two NaNs agree)
+        const float c = scan_divisor(fn - 70);
+        const float a = pk_div_rc(x, 1.0 / (double)c), b = x / c;
+        if (a != a || b != b) return (a != a) == (b != b) ? 0ull : 1ull;
+        return pk_bits(a) != pk_bits(b) ? 1ull : 0ull;
+    }
     float a, b;
     if (fn == 50) {
         a = pk_expf_fast(x);
@@ -130,12 +153,13 @@ __device__ unsigned long long ulp_distance(int fn, unsigned long long i) {
 }
 
 // the largest distance over [lo, lo + n) (fn 50, 51) or the count of inputs
-// at a nonzero distance (fn 60, 61)
+// at a nonzero distance (fn 60, 61; fn 70-77 the count of dividends whose
+// quotients differ)
 __global__ void __launch_bounds__(256) ulp_kernel(int fn, unsigned long long lo, unsigned long long n,
                                                   unsigned long long per_thread, unsigned long long* out) {
     const unsigned long long t = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
     const bool count = fn >= 60;
-    const int f = count ? fn - 10 : fn;
+    const int f = fn >= 70 ? fn : count ? fn - 10 : fn;
     unsigned long long acc = 0;
     const unsigned long long first = t * per_thread;
     for (unsigned long long j = 0; j < per_thread; ++j) {
@@ -185,7 +209,7 @@ __global__ void __launch_bounds__(256) digest_kernel(int fn, unsigned long long 
 
 hipError_t scalar_digest(int fn, uint64_t lo, uint64_t hi, uint64_t* digest) {
     const int known[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 20, 21, 22, 30, 31, 32, 33, 40, 41, 42, 43, 44, 45,
-                         50, 51, 60, 61};
+                         50, 51, 60, 61, 70, 71, 72, 73, 74, 75, 76, 77};
     bool ok = false;
     for (int f : known) ok |= f == fn;
     if (!ok || hi < lo) return hipErrorInvalidValue;

@@ -58,6 +58,20 @@ def test_softmax_quotient_is_the_division():
         assert a.value == b.value, hex(lo)
 
 
+@pytest.mark.parametrize("k", range(8))
+def test_division_by_a_constant_is_the_division(k):
+    """the printed nests' division by a constant, pk_div_rc (the f64 product
+    with RN64(1/c), rounded to f32), equals the correctly rounded division
+    for every f32 dividend, for each of eight divisors (selftest.hip's
+    scan_divisor: sqrt 2, sqrt(2 pi), 3, 0.1, 2 - 2^-23, a subnormal,
+    3e30, -6)"""
+    hip.init(0)
+    d = ctypes.c_uint64()
+    hip.check(hip.lib().presk_hip_scalar_digest(70 + k, 0, 1 << 32, ctypes.byref(d)))
+    print(f"[div] divisor {k}: {d.value} of 2^32 dividends differ", flush=True)
+    assert d.value == 0, d.value
+
+
 @pytest.mark.parametrize("name", list(spec.F64))
 def test_device_f64_function_sample(name, golden):
     hip.init(0)
