@@ -372,6 +372,95 @@ def per_launch_table(p, path, ring_mb: float = 768.0):
         f.write("\n".join(rows) + "\n")
 
 
+# the contractions of the configurations, [M x K] . [K x N]: Llama's
+# projections and head, the MLP block's two, the course step's three
+YARDSTICK_SHAPES = [(2048, 4096, 4096), (2048, 11008, 4096), (2048, 4096, 11008), (2048, 32000, 4096),
+                    (8192, 3072, 768), (8192, 768, 3072), (16384, 384, 384), (16384, 1536, 384), (16384, 384, 1536)]
+
+
+def yardstick(path, ring_mb: float = 600.0):
+    """The vendor library beside this executor on the same contractions: each
+    shape of YARDSTICK_SHAPES in bf16 and f32 (row-major [M x K] . [K x N],
+    a `dot`), timed as torch.matmul (hipBLASLt on this image) and as this
+    executor's contraction, both over rings of operand copies larger than
+    the Infinity Cache: the library's 30 back-to-back calls after 3 untimed
+    ones between HIP events, the executor's ring recorded as one graph and
+    replayed 8 times under the host clock; written to `path` as a markdown
+    table.  A yardstick of
+    what the hardware gives a tuned library on these shapes, not a path of
+    this executor."""
+    import ctypes
+
+    import torch
+
+    from presk_amd import hip, lower as L
+    hip.init(0)
+    dev = torch.device("cuda:0")
+    rows = ["| shape M x N x K | type | hipBLASLt (torch.matmul) us | TFLOP/s | % of peak | this executor us | TFLOP/s | % of peak | order |",
+            "|---|---|---|---|---|---|---|---|---|"]
+    for dt in ("bf16", "f32"):
+        tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+        esz = 2 if dt == "bf16" else 4
+        peak = PEAK_TFLOPS[dt]
+        for (M, N, K) in YARDSTICK_SHAPES:
+            per = (M * K + K * N + M * N) * esz
+            nrot = max(2, int(ring_mb * 1e6 // per) + 1)
+            flop = 2.0 * M * N * K
+            # the library
+            As = [torch.randn(M, K, device=dev, dtype=tdt) for _ in range(nrot)]
+            Bs = [torch.randn(K, N, device=dev, dtype=tdt) for _ in range(nrot)]
+            Cs = [torch.empty(M, N, device=dev, dtype=tdt) for _ in range(nrot)]
+            for i in range(3):
+                torch.matmul(As[i % nrot], Bs[i % nrot], out=Cs[i % nrot])
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(30):
+                torch.matmul(As[i % nrot], Bs[i % nrot], out=Cs[i % nrot])
+            e1.record()
+            torch.cuda.synchronize()
+            lib_us = e0.elapsed_time(e1) / 30 * 1e3
+            del As, Bs, Cs
+            torch.cuda.empty_cache()
+            # this executor: the same product as a `dot`, on its own stream
+            x = L.Operand(L.ax(("batch", M), ("model", K)))
+            w = L.Operand(L.ax(K, N))
+            low = L.dot([x, w], dt)
+            c = hip.Compiled(low.text, dt, low.lanes, hip.FAST)
+            bufs = [[hip.DeviceBuffer(M * K * esz), hip.DeviceBuffer(K * N * esz), hip.DeviceBuffer(M * N * esz)]
+                    for _ in range(nrot)]
+            for bb in bufs:
+                bb[0].zero()
+                bb[1].zero()
+            # the ring as one recorded sequence (no host launch cost), repeated
+            lib = hip.lib()
+            tables = [(ctypes.c_void_p * 3)(*[b_.ptr for b_ in bb]) for bb in bufs]
+            bt = ctypes.c_void_p()
+            hip.check(lib.presk_hip_batch_create(ctypes.byref(bt)))
+            try:
+                for t in tables:
+                    hip.check(lib.presk_hip_batch_add(bt, c.handle, t, 0, max(c.split_bound, 0)))
+                hip.check(lib.presk_hip_batch_graph_branches(bt, 1))
+                for _ in range(2):
+                    hip.check(lib.presk_hip_batch_run(bt, None))
+                hip.sync()
+                reps = 8
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    hip.check(lib.presk_hip_batch_run(bt, None))
+                hip.sync()
+                own_us = (time.perf_counter() - t0) / (reps * nrot) * 1e6
+            finally:
+                lib.presk_hip_batch_release(bt)
+            del bufs
+            lt, ot = flop / lib_us / 1e6, flop / own_us / 1e6
+            rows.append(f"| {M} x {N} x {K} | {dt} | {lib_us:.1f} | {lt:.1f} | {100 * lt / peak:.1f} | {own_us:.1f} | {ot:.1f} | "
+                        f"{100 * ot / peak:.1f} | {c.order} |")
+            print(f"[yardstick] {dt} {M}x{N}x{K}: library {lib_us:.1f} us, executor {own_us:.1f} us", file=sys.stderr, flush=True)
+    with open(path, "w") as f:
+        f.write("\n".join(rows) + "\n")
+
+
 # the other configurations, timed after the headline (rows of the same line)
 SUPPLEMENTARY = [("gpt-step", "bf16", None), ("gpt-forward", "f32", "@" + os.path.join(ROOT, "presk_amd", "realizations", "course_gpt_mixed.json")),
                  ("linear", "f32", None), ("mlp", "bf16", None), ("llama", "bf16", None)]
@@ -403,6 +492,9 @@ def main():
                     help="run a plain copy-like nest (neg over 64 Mi f32) 3 times and exit: the counters' calibration")
     ap.add_argument("--per-launch", default=None, metavar="FILE",
                     help="also time each distinct launch alone and write a markdown table of them to FILE")
+    ap.add_argument("--yardstick", default=None, metavar="FILE",
+                    help="time torch.matmul (the vendor library) beside this executor's contraction on the "
+                         "configurations' GEMM shapes, write a markdown table to FILE and exit")
     ap.add_argument("--cpu-rows", type=int, default=None)
     ap.add_argument("--cpu-child", nargs=3, type=int, default=None, metavar=("ROWS", "THREADS", "CORE"),
                     help=argparse.SUPPRESS)
@@ -418,7 +510,7 @@ def main():
         return
     # the CPU baseline first, in child processes, before the GPU is touched
     cpu = None
-    if not args.no_cpu and not args.copy_probe and not args.dominant_only:
+    if not args.no_cpu and not args.copy_probe and not args.dominant_only and not args.yardstick:
         # gpt-step: B 16 x T 256, the batch of the reference's own published rows
         rows_all = args.cpu_rows or {"mlp": 2048, "linear": 512, "gpt-step": 4096, "gpt-forward": 4096}.get(args.workload)
         rows_one = {"mlp": 256, "linear": 64, "gpt-step": 256, "gpt-forward": 256}.get(args.workload)
@@ -429,6 +521,9 @@ def main():
 
     if args.copy_probe:
         copy_probe()
+        return
+    if args.yardstick:
+        yardstick(args.yardstick)
         return
     rec, p, (ln, c) = measure(args.workload, dtype, args.steps, args.warmup, args.realize, args.dropout, args.adamw,
                               args.eager, args.dominant_match)

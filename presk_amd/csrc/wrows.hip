@@ -4,8 +4,10 @@
 // order of the executor's own and the exponentials by pk_expf_fast.
 //
 // One wave owns a row.  The row is cut into blocks of VEC elements (one
-// 16-byte load: 4 f32 or 8 bf16/f16; VEC 1 where rows are not whole
-// 16-byte vectors), block b held by lane b mod 64.  The order of a sum,
+// 16-byte load: 4 f32 or 8 bf16/f16; 8 bytes, 4 bf16/f16, for 16-bit rows
+// of at most 256; VEC 1 where rows are not whole vectors), block b held by
+// lane b mod 64; the cross-lane steps are register moves (DPP and gfx950's
+// lane swaps), not LDS round trips.  The order of a sum,
 // `lanes64-tree`: each lane adds its own elements in index order (block by
 // block, element by element, from zero), then the 64 lane sums are added by
 // a balanced pairwise tree over the lane index ((s0 + s1) + (s2 + s3)) + ...,
@@ -52,7 +54,8 @@ __device__ __forceinline__ float stored(float v) {
     return pk_f16_to_f32(pk_f32_to_f16(v));
 }
 
-// VEC elements from element e (e a multiple of VEC; 16-byte aligned when VEC > 1)
+// VEC elements from element e (e a multiple of VEC; VEC elements aligned
+// to their size when VEC > 1: 16 bytes, or 8 for 16-bit rows in blocks of 4)
 template <int ST, int VEC>
 __device__ __forceinline__ void ldv(const void* p, long long e, float (&v)[VEC]) {
     if constexpr (VEC == 1) {
@@ -63,6 +66,19 @@ __device__ __forceinline__ void ldv(const void* p, long long e, float (&v)[VEC])
         v[1] = q.y;
         v[2] = q.z;
         v[3] = q.w;
+    } else if constexpr (VEC == 4) {
+        const uint2 q = *(const uint2*)((const unsigned short*)p + e);
+        const unsigned w[2] = {q.x, q.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (ST == 1) {
+                v[2 * i] = pk_bf16_to_f32((unsigned short)(w[i] & 0xffffu));
+                v[2 * i + 1] = pk_bf16_to_f32((unsigned short)(w[i] >> 16));
+            } else {
+                v[2 * i] = pk_f16_to_f32((unsigned short)(w[i] & 0xffffu));
+                v[2 * i + 1] = pk_f16_to_f32((unsigned short)(w[i] >> 16));
+            }
+        }
     } else {
         const uint4 q = *(const uint4*)((const unsigned short*)p + e);
         const unsigned w[4] = {q.x, q.y, q.z, q.w};
@@ -87,6 +103,12 @@ __device__ __forceinline__ void stv(void* p, long long e, const float (&v)[VEC],
         else ((unsigned short*)p)[e] = narrow16<ST>(v[0], ovf);
     } else if constexpr (ST == 0) {
         *(float4*)((float*)p + e) = make_float4(v[0], v[1], v[2], v[3]);
+    } else if constexpr (VEC == 4) {
+        unsigned w[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            w[i] = (unsigned)narrow16<ST>(v[2 * i], ovf) | ((unsigned)narrow16<ST>(v[2 * i + 1], ovf) << 16);
+        *(uint2*)((unsigned short*)p + e) = make_uint2(w[0], w[1]);
     } else {
         unsigned w[4];
 #pragma unroll
@@ -96,18 +118,57 @@ __device__ __forceinline__ void stv(void* p, long long e, const float (&v)[VEC],
     }
 }
 
+// lane l ^ D's value (the whole wave active), by register moves instead of
+// the LDS crossbar: DPP quad permutations for 1 and 2, a half-row mirror of
+// a quad reversal for 4 ((l & ~7) + 7 - (l & 7) of (l & ~3) + 3 - (l & 3)
+// is l ^ 4), a row rotation by 8 for 8, and gfx950's row and half-wave
+// swaps for 16 and 32: swapping a value with itself leaves each lane's
+// partner in one of the two results (the odd rows' partners in the first),
+// chosen by the lane's row or half
+template <int D>
+__device__ __forceinline__ float xor_lane(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (D == 1) {
+        r = __builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
+    } else if constexpr (D == 2) {
+        r = __builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, false);       // quad_perm [2,3,0,1]
+    } else if constexpr (D == 4) {
+        const int q = __builtin_amdgcn_update_dpp(0, b, 0x1B, 0xF, 0xF, false);   // quad_perm [3,2,1,0]
+        r = __builtin_amdgcn_update_dpp(0, q, 0x141, 0xF, 0xF, false);            // row_half_mirror
+    } else if constexpr (D == 8) {
+        r = __builtin_amdgcn_update_dpp(0, b, 0x128, 0xF, 0xF, false);      // row_ror:8
+    } else if constexpr (D == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap((unsigned)b, (unsigned)b, false, false);
+        r = (int)(((threadIdx.x >> 4) & 1) ? p[0] : p[1]);
+    } else {
+        static_assert(D == 32, "a lane distance of the wave");
+        const auto p = __builtin_amdgcn_permlane32_swap((unsigned)b, (unsigned)b, false, false);
+        r = (int)(((threadIdx.x >> 5) & 1) ? p[0] : p[1]);
+    }
+    return __builtin_bit_cast(float, r);
+}
+
 // the 64 lanes' sums by the balanced pairwise tree over lane index: at
 // distance d lane l adds lane l ^ d's value, and since a + b = b + a both
 // lanes of a pair hold the same sum, so every lane ends with the tree's
 // total
 __device__ __forceinline__ float lanes_sum(float s) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) s = s + __shfl_xor(s, d, 64);
+    s = s + xor_lane<1>(s);
+    s = s + xor_lane<2>(s);
+    s = s + xor_lane<4>(s);
+    s = s + xor_lane<8>(s);
+    s = s + xor_lane<16>(s);
+    s = s + xor_lane<32>(s);
     return s;
 }
 __device__ __forceinline__ float lanes_max(float m) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) m = __builtin_fmaxf(m, __shfl_xor(m, d, 64));
+    m = __builtin_fmaxf(m, xor_lane<1>(m));
+    m = __builtin_fmaxf(m, xor_lane<2>(m));
+    m = __builtin_fmaxf(m, xor_lane<4>(m));
+    m = __builtin_fmaxf(m, xor_lane<8>(m));
+    m = __builtin_fmaxf(m, xor_lane<16>(m));
+    m = __builtin_fmaxf(m, xor_lane<32>(m));
     return m;
 }
 
@@ -183,13 +244,29 @@ __global__ void __launch_bounds__(64 * WAVES) wrows_kernel(RowArgs a) {
             stv<ST, 1>(a.out, row, o, ovf);
         }
     } else {
-        // the row's max over its allowed elements
+        // the row's max over its allowed elements.  Where each lane's block j
+        // is wholly allowed or wholly not (every block of an unmasked row,
+        // all but the diagonal's of a causal one), the wave takes a path
+        // without the per-element test; elsewhere every lane tests (one path,
+        // not both)
+        constexpr unsigned FULL = (1u << VEC) - 1;
+        bool whole[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) whole[j] = __all(allow[j] == FULL || allow[j] == 0);
         float m = -__builtin_inff();
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
+        for (int j = 0; j < CH; ++j) {
+            if (whole[j]) {
+                if (allow[j]) {
 #pragma unroll
-            for (int i = 0; i < VEC; ++i)
-                if ((allow[j] >> i) & 1u) m = __builtin_fmaxf(m, v[j][i]);
+                    for (int i = 0; i < VEC; ++i) m = __builtin_fmaxf(m, v[j][i]);
+                }
+            } else if (allow[j]) {
+#pragma unroll
+                for (int i = 0; i < VEC; ++i)
+                    if ((allow[j] >> i) & 1u) m = __builtin_fmaxf(m, v[j][i]);
+            }
+        }
         m = lanes_max(m);
         // every allowed element's exponential, their sum in the declared
         // order; a block with no allowed element holds zeros already, and
@@ -198,8 +275,17 @@ __global__ void __launch_bounds__(64 * WAVES) wrows_kernel(RowArgs a) {
         // mask's upper triangle)
         float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
-            if (allow[j]) {
+        for (int j = 0; j < CH; ++j) {
+            if (whole[j]) {
+                if (allow[j]) {
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i) {
+                        const float e = pk_expf_fast(v[j][i] - m);
+                        v[j][i] = e;
+                        s = s + e;
+                    }
+                }
+            } else if (allow[j]) {
 #pragma unroll
                 for (int i = 0; i < VEC; ++i) {
                     const float e = (allow[j] >> i) & 1u ? pk_expf_fast(v[j][i] - m) : 0.0f;
@@ -207,6 +293,7 @@ __global__ void __launch_bounds__(64 * WAVES) wrows_kernel(RowArgs a) {
                     s = s + e;
                 }
             }
+        }
         const float z = lanes_sum(s);
         if constexpr (KIND == 1) {
             const Quot q(z);
@@ -216,10 +303,14 @@ __global__ void __launch_bounds__(64 * WAVES) wrows_kernel(RowArgs a) {
                 const long long b = (long long)j * 64 + lane;
                 if (b >= nb) continue;
                 float o[VEC];
-                if (allow[j]) {
+                if (whole[j] && allow[j]) {
 #pragma unroll
                     for (int i = 0; i < VEC; ++i)
                         // the two-pass nest divides the stored exponential
+                        o[i] = q(two ? stored<ST>(v[j][i]) : v[j][i]);
+                } else if (allow[j]) {
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i)
                         o[i] = (allow[j] >> i) & 1u ? q(two ? stored<ST>(v[j][i]) : v[j][i]) : 0.0f;
                 } else {
 #pragma unroll
@@ -274,6 +365,8 @@ hipError_t launch_ch(const RowArgs& a, int ch, hipStream_t stream) {
 template <int KIND, int ST>
 hipError_t launch_st(const RowArgs& a, int vec, int ch, hipStream_t stream) {
     if (vec == 1) return launch_ch<KIND, ST, 1>(a, ch, stream);
+    if constexpr (ST != 0)
+        if (vec == 4) return launch_ch<KIND, ST, 4>(a, ch, stream);
     return launch_ch<KIND, ST, ST == 0 ? 4 : 8>(a, ch, stream);
 }
 
@@ -298,10 +391,13 @@ int kind_of(int op) {
 }
 
 // 16-byte blocks when every row is whole vectors, else single elements;
-// the blocks a lane holds, a power of two up to 16.  0 when the rows are
-// too long to hold.
+// 16-bit rows of at most 256 elements in 8-byte blocks (4 elements), so
+// that all 64 lanes hold a part of the row (the course's attention rows:
+// 64 blocks of 4, not 32 of 8 with half the wave idle); the blocks a lane
+// holds, a power of two up to 16.  0 when the rows are too long to hold.
 int vec_of(const RowArgs& a) {
     const int esz = a.storage == 0 ? 4 : 2;
+    if (esz == 2 && a.n <= 256 && a.n % 4 == 0) return 4;
     return (a.n * esz) % 16 == 0 ? 16 / esz : 1;
 }
 int ch_of(long long n, int vec) {

@@ -73,6 +73,9 @@ SUMS = [
     ("sum-vocab65", lambda dt: L.reduce_axis("sum", "vocab", [O(A(("batch", 7), ("seq", 60), ("vocab", 65)))], dt), "f32"),
     ("sum_to-rows", lambda dt: L.sum_to([O(A(("batch", 64), ("seq", 256), ("model", 384))), O(A(("batch", 64), ("seq", 256)))], dt), "f32"),
     ("mean-f16", lambda dt: L.reduce_axis("mean", "model", [O(A(("batch", 300), ("model", 1000)))], dt), "f16"),
+    # 16-bit rows of at most 256 elements: blocks of 4 (8-byte loads)
+    ("sum-bf16-256", lambda dt: L.reduce_axis("sum", "seq2", [O(A(("batch", 64), ("heads", 6), ("seq", 256), ("seq2", 256)))], dt), "bf16"),
+    ("mean-f16-100", lambda dt: L.reduce_axis("mean", "model", [O(A(("batch", 300), ("model", 100)))], dt), "f16"),
 ]
 
 
@@ -91,7 +94,9 @@ def test_fast_row_sums_are_the_declared_order(ex, name, mk, dt):
     c, got = run(ex, low, ins)
     vec = int(c.order.split("x")[1].split("-")[0])
     assert c.order == f"lanes64x{vec}-tree", c.order
-    assert vec == (1 if (n * (4 if dt == "f32" else 2)) % 16 else 16 // (4 if dt == "f32" else 2))
+    esz = 4 if dt == "f32" else 2
+    # 16-byte blocks, 8-byte ones for 16-bit rows of at most 256, else single elements
+    assert vec == (4 if esz == 2 and n <= 256 and n % 4 == 0 else 1 if (n * esz) % 16 else 16 // esz)
     s = lanes_tree_sum(x, vec)
     if low.name.startswith("mean"):
         s = (s / np.float32(n)).astype(np.float32)
@@ -185,13 +190,14 @@ def test_fast_softmax_special_rows(ex, dt):
     ins = [fmt.encode(x, dt), mask.ravel()]
     want, _ = cexec.run(low.text, dt, ins, lanes=low.lanes)
     c, raw = run(ex, low, ins)
+    vec = int(c.order.split("x")[1].split("-")[0])
     got = fmt.decode(raw, dt).astype(np.float64)
     ref = fmt.decode(want, dt).astype(np.float64)
     assert np.array_equal(np.isnan(got), np.isnan(ref))
     allowed = np.broadcast_to(mask > 0, (3, T, T)).ravel()
     assert np.all(got[~allowed] == 0) and np.all(got[20 * T:21 * T] == 0)
     fin = np.isfinite(ref)
-    assert np.all(np.abs(got[fin] - ref[fin]) <= band(T, 1) * np.abs(ref[fin]) + 4 * HALF[dt] * np.abs(ref[fin]) + 2.0 ** -126)
+    assert np.all(np.abs(got[fin] - ref[fin]) <= band(T, vec) * np.abs(ref[fin]) + 4 * HALF[dt] * np.abs(ref[fin]) + 2.0 ** -126)
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
