@@ -372,6 +372,120 @@ def per_launch_table(p, path, ring_mb: float = 768.0):
         f.write("\n".join(rows) + "\n")
 
 
+# the workloads whose distinct launches the traffic table covers
+TRAFFIC_WORKLOADS = [("gpt-step", "f32", None), ("gpt-step", "bf16", None),
+                     ("gpt-forward", "f32", "@" + os.path.join(ROOT, "presk_amd", "realizations", "course_gpt_mixed.json")),
+                     ("linear", "f32", None), ("mlp", "bf16", None), ("llama", "bf16", None)]
+
+
+def traffic_run(keys_path):
+    """The counter runs' program (under rocprofv3 --pmc FETCH_SIZE, then
+    WRITE_SIZE): the copy probe (neg over 64 Mi f32), then every distinct
+    launch of TRAFFIC_WORKLOADS, each group of 3 calls after a 4 KiB
+    presk_hip_memset whose fill kernel delimits the group in the counter
+    table; the groups' launch keys, in order, and the device sources' sha go
+    to `keys_path` for traffic_table."""
+    from presk_amd import configs, hip, llama, lower as L
+    lib = hip.lib()
+    hip.init(0)
+    keys = []
+    delim = hip.DeviceBuffer(4096)
+    x = L.Operand(L.ax(("rows", 16384), ("cols", 4096)))
+    low = L.unary("neg", [x], "f32")
+    cp = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+    a, b = hip.DeviceBuffer(4 << 26), hip.DeviceBuffer(4 << 26)
+    a.zero()
+    hip.check(lib.presk_hip_memset(delim.ptr, 0, 4096, None))
+    for _ in range(3):
+        cp.run([a.ptr, b.ptr])
+    keys.append("__copy_probe__")
+    hip.sync()
+    del a, b
+    for name, dt, real in TRAFFIC_WORKLOADS:
+        p, host, _, _, _ = workload(name, dt, realize=real)
+        p.compile()
+        if host is None:
+            llama.load_device_inputs(p, llama.LLAMA_7B)
+        else:
+            configs.load_inputs(p, host)
+        p.prepare()
+        p.run()
+        hip.sync()
+        seen = set()
+        for ln in p.launches:
+            k = launch_key(ln)
+            if k in seen:
+                continue
+            seen.add(k)
+            c = ln.compiled
+            hip.check(lib.presk_hip_memset(delim.ptr, 0, 4096, None))
+            for _ in range(3):
+                hip.check(lib.presk_hip_run(c.handle, ln.table, 0, max(c.split_bound, 0), None))
+            keys.append(k)
+        hip.sync()
+        print(f"[traffic] {name} {dt}: {len(seen)} distinct launches", file=sys.stderr, flush=True)
+        del p
+        gc.collect()
+    hip.check(lib.presk_hip_memset(delim.ptr, 0, 4096, None))
+    hip.sync()
+    with open(keys_path, "w") as f:
+        json.dump({"keys": keys, "src_sha": source_sha()}, f)
+    print(f"[traffic] {len(keys)} groups", file=sys.stderr, flush=True)
+
+
+def traffic_table(keys_path, fetch_glob, write_glob, out_path):
+    """profiles/traffic.json from the two counter runs of traffic_run: the
+    per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) split into groups at the
+    fill kernels, each group's 3 calls averaged, every KiB scaled by the
+    bytes the copy probe moves per KiB its group counts."""
+    import csv
+    import glob
+
+    with open(keys_path) as f:
+        keys = json.load(f)
+
+    def groups(pattern, counter):
+        rows = []
+        for path in glob.glob(pattern, recursive=True):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    if r.get("Counter_Name") == counter:
+                        rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+        rows.sort()
+        segs, cur = [], None
+        for _, kname, v in rows:
+            if "fill" in kname.lower() or "memset" in kname.lower():
+                if cur is not None:
+                    segs.append(cur)
+                cur = []
+            elif cur is not None:
+                cur.append(v)
+        if cur:
+            segs.append(cur)
+        return segs
+
+    fetch, write = groups(fetch_glob, "FETCH_SIZE"), groups(write_glob, "WRITE_SIZE")
+    k = keys["keys"]
+    if len(fetch) < len(k) or len(write) < len(k):
+        raise SystemExit(f"traffic_table: {len(k)} groups expected, {len(fetch)} / {len(write)} found")
+    probe = 4 << 26
+    ff = probe / (sum(fetch[0]) / 3 * 1024)
+    wf = probe / (sum(write[0]) / 3 * 1024)
+    out = []
+    for i, key in enumerate(k[1:], 1):
+        fb = sum(fetch[i]) / 3 * 1024 * ff
+        wb = sum(write[i]) / 3 * 1024 * wf
+        out.append({"key": key, "bytes_per_launch": round(fb + wb), "fetch_bytes": round(fb), "write_bytes": round(wb),
+                    "dispatches": len(fetch[i]) // 3})
+    with open(out_path, "w") as f:
+        json.dump({"src_sha": keys["src_sha"],
+                   "method": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over bench.py --traffic-run (every distinct "
+                             "launch of the workloads 3 times after a 4 KiB memset delimiter), each KiB scaled by the "
+                             f"copy probe's reading (neg over 64 Mi f32: FETCH x {ff:.3f}, WRITE x {wf:.3f})",
+                   "launches": out}, f, indent=1)
+    print(f"[traffic] wrote {out_path}: {len(out)} launches; copy probe factors {ff:.3f} {wf:.3f}", file=sys.stderr)
+
+
 # the contractions of the configurations, [M x K] . [K x N]: Llama's
 # projections and head, the MLP block's two, the course step's three
 YARDSTICK_SHAPES = [(2048, 4096, 4096), (2048, 11008, 4096), (2048, 4096, 11008), (2048, 32000, 4096),
@@ -495,6 +609,11 @@ def main():
     ap.add_argument("--yardstick", default=None, metavar="FILE",
                     help="time torch.matmul (the vendor library) beside this executor's contraction on the "
                          "configurations' GEMM shapes, write a markdown table to FILE and exit")
+    ap.add_argument("--traffic-run", default=None, metavar="KEYS_JSON",
+                    help="the counter runs' program: every distinct launch 3 times after a memset delimiter (run "
+                         "under rocprofv3 --pmc), the launch keys written to KEYS_JSON; exits")
+    ap.add_argument("--traffic-table", nargs=4, default=None, metavar=("KEYS_JSON", "FETCH_GLOB", "WRITE_GLOB", "OUT"),
+                    help="profiles/traffic.json from the FETCH_SIZE and WRITE_SIZE runs of --traffic-run; exits")
     ap.add_argument("--cpu-rows", type=int, default=None)
     ap.add_argument("--cpu-child", nargs=3, type=int, default=None, metavar=("ROWS", "THREADS", "CORE"),
                     help=argparse.SUPPRESS)
@@ -504,13 +623,16 @@ def main():
               "multi-GPU sharding is a design (DESIGN.md), not a run.", file=sys.stderr)
         sys.exit(2)
     dtype = args.dtype or ("bf16" if args.workload in ("mlp", "llama") else "f32")
+    if args.traffic_table:
+        traffic_table(*args.traffic_table)
+        return
     if args.cpu_child:
         rows, th, core = args.cpu_child
         cpu_child(args.workload, dtype, rows, th, core, args.realize, args.dropout, args.adamw)
         return
     # the CPU baseline first, in child processes, before the GPU is touched
     cpu = None
-    if not args.no_cpu and not args.copy_probe and not args.dominant_only and not args.yardstick:
+    if not args.no_cpu and not args.copy_probe and not args.dominant_only and not args.yardstick and not args.traffic_run:
         # gpt-step: B 16 x T 256, the batch of the reference's own published rows
         rows_all = args.cpu_rows or {"mlp": 2048, "linear": 512, "gpt-step": 4096, "gpt-forward": 4096}.get(args.workload)
         rows_one = {"mlp": 256, "linear": 64, "gpt-step": 256, "gpt-forward": 256}.get(args.workload)
@@ -524,6 +646,9 @@ def main():
         return
     if args.yardstick:
         yardstick(args.yardstick)
+        return
+    if args.traffic_run:
+        traffic_run(args.traffic_run)
         return
     rec, p, (ln, c) = measure(args.workload, dtype, args.steps, args.warmup, args.realize, args.dropout, args.adamw,
                               args.eager, args.dominant_match)
