@@ -381,27 +381,35 @@ TRAFFIC_WORKLOADS = [("gpt-step", "f32", None), ("gpt-step", "bf16", None),
 def traffic_run(keys_path):
     """The counter runs' program (under rocprofv3 --pmc FETCH_SIZE, then
     WRITE_SIZE): the copy probe (neg over 64 Mi f32), then every distinct
-    launch of TRAFFIC_WORKLOADS, each group of 3 calls after a 4 KiB
-    presk_hip_memset whose fill kernel delimits the group in the counter
-    table; the groups' launch keys, in order, and the device sources' sha go
-    to `keys_path` for traffic_table."""
+    launch of TRAFFIC_WORKLOADS 3 times.  Each region of dispatches follows
+    one launch of a marker nest (a one-element copy named `traffic_mark`,
+    found by name in the counter table): the probe's, each workload's set-up
+    and first run (key `__setup__`, left out of the table) and each launch's
+    group; the keys, in order, and the device sources' sha go to
+    `keys_path` for traffic_table."""
     from presk_amd import configs, hip, llama, lower as L
     lib = hip.lib()
     hip.init(0)
     keys = []
-    delim = hip.DeviceBuffer(4096)
+    one = L.unary("neg", [L.Operand(L.ax(("one", 1)))], "f32")
+    mark = hip.Compiled(one.text.replace("kernel neg ", "kernel traffic_mark ", 1), "f32", one.lanes, hip.FAST)
+    mbuf = [hip.DeviceBuffer(256), hip.DeviceBuffer(256)]
+
+    def marker(key):
+        mark.run([mbuf[0].ptr, mbuf[1].ptr])
+        keys.append(key)
+
     x = L.Operand(L.ax(("rows", 16384), ("cols", 4096)))
     low = L.unary("neg", [x], "f32")
     cp = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
-    a, b = hip.DeviceBuffer(4 << 26), hip.DeviceBuffer(4 << 26)
-    a.zero()
-    hip.check(lib.presk_hip_memset(delim.ptr, 0, 4096, None))
+    a, b = hip.DeviceBuffer(4 << 26), hip.DeviceBuffer(4 << 26)   # contents as allocated: neg moves them all
+    marker("__copy_probe__")
     for _ in range(3):
         cp.run([a.ptr, b.ptr])
-    keys.append("__copy_probe__")
     hip.sync()
     del a, b
     for name, dt, real in TRAFFIC_WORKLOADS:
+        marker("__setup__")
         p, host, _, _, _ = workload(name, dt, realize=real)
         p.compile()
         if host is None:
@@ -418,26 +426,25 @@ def traffic_run(keys_path):
                 continue
             seen.add(k)
             c = ln.compiled
-            hip.check(lib.presk_hip_memset(delim.ptr, 0, 4096, None))
+            marker(k)
             for _ in range(3):
                 hip.check(lib.presk_hip_run(c.handle, ln.table, 0, max(c.split_bound, 0), None))
-            keys.append(k)
         hip.sync()
         print(f"[traffic] {name} {dt}: {len(seen)} distinct launches", file=sys.stderr, flush=True)
         del p
         gc.collect()
-    hip.check(lib.presk_hip_memset(delim.ptr, 0, 4096, None))
+    marker("__end__")
     hip.sync()
     with open(keys_path, "w") as f:
         json.dump({"keys": keys, "src_sha": source_sha()}, f)
-    print(f"[traffic] {len(keys)} groups", file=sys.stderr, flush=True)
+    print(f"[traffic] {len(keys)} regions", file=sys.stderr, flush=True)
 
 
 def traffic_table(keys_path, fetch_glob, write_glob, out_path):
     """profiles/traffic.json from the two counter runs of traffic_run: the
-    per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) split into groups at the
-    fill kernels, each group's 3 calls averaged, every KiB scaled by the
-    bytes the copy probe moves per KiB its group counts."""
+    per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) split into regions at the
+    marker launches, each launch's 3 calls averaged, every KiB scaled by the
+    bytes the copy probe moves per KiB its region counts."""
     import csv
     import glob
 
@@ -452,27 +459,27 @@ def traffic_table(keys_path, fetch_glob, write_glob, out_path):
                     if r.get("Counter_Name") == counter:
                         rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
         rows.sort()
-        segs, cur = [], None
+        # a region: the dispatches after one marker launch, up to the next
+        # (the runtime's own copy and fill kernels left out)
+        segs = []
         for _, kname, v in rows:
-            if "fill" in kname.lower() or "memset" in kname.lower():
-                if cur is not None:
-                    segs.append(cur)
-                cur = []
-            elif cur is not None:
-                cur.append(v)
-        if cur:
-            segs.append(cur)
+            if kname.startswith("pk_traffic_mark"):
+                segs.append([])
+            elif segs and not kname.startswith("__amd_rocclr"):
+                segs[-1].append(v)
         return segs
 
     fetch, write = groups(fetch_glob, "FETCH_SIZE"), groups(write_glob, "WRITE_SIZE")
     k = keys["keys"]
-    if len(fetch) < len(k) or len(write) < len(k):
-        raise SystemExit(f"traffic_table: {len(k)} groups expected, {len(fetch)} / {len(write)} found")
+    if len(fetch) != len(k) or len(write) != len(k):
+        raise SystemExit(f"traffic_table: {len(k)} regions expected, {len(fetch)} / {len(write)} found")
     probe = 4 << 26
     ff = probe / (sum(fetch[0]) / 3 * 1024)
     wf = probe / (sum(write[0]) / 3 * 1024)
     out = []
-    for i, key in enumerate(k[1:], 1):
+    for i, key in enumerate(k):
+        if key.startswith("__"):
+            continue
         fb = sum(fetch[i]) / 3 * 1024 * ff
         wb = sum(write[i]) / 3 * 1024 * wf
         out.append({"key": key, "bytes_per_launch": round(fb + wb), "fetch_bytes": round(fb), "write_bytes": round(wb),
@@ -480,8 +487,8 @@ def traffic_table(keys_path, fetch_glob, write_glob, out_path):
     with open(out_path, "w") as f:
         json.dump({"src_sha": keys["src_sha"],
                    "method": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over bench.py --traffic-run (every distinct "
-                             "launch of the workloads 3 times after a 4 KiB memset delimiter), each KiB scaled by the "
-                             f"copy probe's reading (neg over 64 Mi f32: FETCH x {ff:.3f}, WRITE x {wf:.3f})",
+                             "launch of the workloads 3 times after a marker launch), each KiB scaled by the copy "
+                             f"probe's reading (neg over 64 Mi f32: FETCH x {ff:.3f}, WRITE x {wf:.3f})",
                    "launches": out}, f, indent=1)
     print(f"[traffic] wrote {out_path}: {len(out)} launches; copy probe factors {ff:.3f} {wf:.3f}", file=sys.stderr)
 

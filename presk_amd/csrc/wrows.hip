@@ -207,8 +207,15 @@ __global__ void __launch_bounds__(64 * WAVES) wrows_kernel(RowArgs a) {
     const bool masked = a.op == kMaskedSoftmax3 || a.op == kMaskedSoftmax2;
     const unsigned char* mrow = nullptr;
     // the packed mask's rows: (n + 63) / 64 * 2 words each (rows.hip's layout)
-    if (KIND == 1 && masked)
-        mrow = (const unsigned char*)(a.mbits + ((row + a.mask_row0) % a.mask_rows) * ((n + 63) / 64 * 2));
+    if (KIND == 1 && masked) {
+        // the mask's row, in 32-bit arithmetic where the operands fit (a
+        // 64-bit remainder is a long scalar sequence ahead of the loads)
+        const unsigned long long r = (unsigned long long)(row + a.mask_row0);
+        const unsigned long long mr = (r >> 32) == 0 && ((unsigned long long)a.mask_rows >> 32) == 0
+                                          ? (unsigned long long)((unsigned)r % (unsigned)a.mask_rows)
+                                          : r % (unsigned long long)a.mask_rows;
+        mrow = (const unsigned char*)(a.mbits + (long long)mr * ((n + 63) / 64 * 2));
+    }
     bool ovf = false;
 
     // the lane's blocks, loaded once (a block past the row or wholly masked
