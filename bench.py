@@ -180,6 +180,10 @@ def cpu_baseline(name, dtype, rows_all, rows_one, realize=None, dropout=0.0, ada
             out.append(json.loads(text.strip().splitlines()[-1]))
         return out
 
+    # one untimed process first: the first of a run has measured twice as
+    # long as those after it (the host's first touch of its memory and
+    # caches), which a three-process median would otherwise carry
+    warm = collect([child(rows_all, threads, -1)])[0]
     every = [collect([child(rows_all, threads, -1)])[0] for _ in range(repeats)]
     one = collect([child(rows_one, 1, cores[(i * 2) % len(cores)]) for i in range(repeats)])
 
@@ -198,7 +202,7 @@ def cpu_baseline(name, dtype, rows_all, rows_one, realize=None, dropout=0.0, ada
     return {"value": round(med, 1), "best": round(best, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "cpu_model": model, "repeats": repeats,
             "sample": f"{toks} tokens of the same workload (B {max(toks // 256, 1)} x T 256), {repeats} processes "
-                      f"({secs} s a call): the oracle's C restatement of the same nests (-O3 -march=native, "
+                      f"({secs} s a call) after an untimed one ({round(warm['secs'], 3)} s): the oracle's C restatement of the same nests (-O3 -march=native, "
                       f"-ffp-contract=off, sequential sums, the outermost parallel loop split over {threads} OpenMP "
                       f"threads); value = the median, best = the fastest",
             "one_core": {"value": round(med1, 2), "best": round(best1, 2), "unit": "tokens/s", "cores": 1,

@@ -185,6 +185,10 @@ class Compiled:
         self.order = info.order.decode()
         self.guarded = bool(info.guarded)
         self.n_inputs = info.n_inputs
+        # integer (Quant) inputs, `int8/..` or `int4/..` in the header: each
+        # has its scales' slot after the output
+        head = text.split("->", 1)[0]
+        self.n_quant = head.count(": int8/") + head.count(": int4/")
         self.split_bound = info.split_bound
         self.flops = info.flops
         self.bytes = info.bytes
@@ -198,12 +202,13 @@ class Compiled:
 
     def _table(self, ptrs):
         # the KernelFn table has no length: every slot the kernel reads must
-        # be there (inputs, the output, the flag when guarded; scales of
-        # integer inputs come between), or the launch would read a pointer
-        # past the table's end
-        need = self.n_inputs + 1 + (1 if self.guarded else 0)
+        # be there (inputs, the output, a scales pointer per integer input,
+        # the flag when guarded), or the launch would read a pointer past
+        # the table's end
+        need = self.n_inputs + 1 + self.n_quant + (1 if self.guarded else 0)
         if len(ptrs) < need or any(not p for p in ptrs):
             raise ValueError(f"a KernelFn table of {len(ptrs)} pointers for a kernel of {self.n_inputs} inputs"
+                             f"{f' ({self.n_quant} integer, with scales)' if self.n_quant else ''}"
                              f"{' and a flag' if self.guarded else ''}: {need} or more non-null pointers needed")
         return (ctypes.c_void_p * len(ptrs))(*ptrs)
 

@@ -138,6 +138,11 @@ def test_reader_prints_integer_types_back(bits, span):
         assert c.read_back() == text
         # EXACT: the generic printer's loads; FAST: the f32 MFMA kernel on them
         assert c.kind == ("generic" if mode == hip.EXACT else "gemm"), (mode, c.kind)
+        # the scales' slot after the output counts in the table's length: a
+        # table of the inputs and the output alone is refused on the host
+        assert c.n_inputs == 2 and c.n_quant == 1
+        with pytest.raises(ValueError, match="1 integer, with scales"):
+            c.run([0x1000, 0x2000, 0x3000])
 
 
 def test_integer_output_is_malformed():
