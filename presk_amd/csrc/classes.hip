@@ -295,6 +295,7 @@ void apply_override(GemmArgs& g) {
     TileOverride t;
     std::string err;
     if (!tile_override(&t, &err) || t.bm == 0) return;
+    g.stream = false;     // the named tiles, not the streamed panels
     if (t.bm == 128 || g.storage != kF32) {
         g.bm = t.bm;
         g.bn = t.bn;
@@ -314,6 +315,7 @@ void apply_override(GemmArgs& g) {
 
 void plan_tiles(GemmArgs& g) {
     g.bm = 128;
+    g.stream = true;
     g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
     long long best = -1;
     if (g.storage == kF32) {

@@ -864,6 +864,178 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
 
+// Products with K of at most two k-blocks (the attention's scores, K 64 or
+// 128), 16-bit storage, both operands k-contiguous: a workgroup keeps its
+// 128-row panel of A in LDS for the whole K and streams the 64-column tiles
+// of B across it.  Each tile's B is loaded into registers while the
+// previous tile is multiplied and stored, and the output leaves through the
+// B buffer the tile has finished with, so a workgroup's loads, MFMAs and
+// stores overlap across its tiles instead of each tile paying its own
+// prologue and epilogue.  The products are the 128 x 64 tiles' own: the
+// same 32x32x16 MFMAs over the same k-steps in the same order, with the
+// operands' roles exchanged (D = B A^T: lane l then holds output row
+// l & 31 and four consecutive columns, which leave as 8-byte LDS writes).
+// The launcher takes it only where every tile is whole (M % 128, N % 64,
+// K % 64) and no bias or split applies.
+template <int ST, int NK>
+__global__ void __launch_bounds__(NT) stream_kernel(GemmArgs g, int tiles_per_item, int chunks) {
+    typedef unsigned short S;
+    typedef Loader<ST, true, 128> LA;
+    typedef Loader<ST, true, 64> LB;
+    constexpr int BK = St<ST>::BK, LD = LA::LD, ASZ = LA::SIZE, BSZ = LB::SIZE;
+    constexpr int CLD = 64 + 8;                      // the staged output's row stride (elements)
+    static_assert(128 * CLD <= 2 * BSZ, "a tile's output fits the B buffer it finished with");
+    __shared__ __attribute__((aligned(16))) S smem[2 * ASZ + 4 * BSZ];
+    S* const As = smem;                              // A's k-blocks, [2][128][LD]
+    S* const Bs = smem + 2 * ASZ;                    // two buffers of B's k-blocks, [2][2][64][LD]
+
+    // the item: a batch entry, a 128-row panel, a run of column tiles;
+    // each XCD (workgroup id mod 8) takes a contiguous run of items, so the
+    // panels of one batch entry share its L2 and B
+    const unsigned total = gridDim.x, xcd = blockIdx.x % 8, local = blockIdx.x / 8;
+    const unsigned q8 = total / 8, r8 = total % 8;
+    const unsigned item = xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    const unsigned tiles_m = (unsigned)(g.M / 128), tiles_n = (unsigned)(g.N / 64);
+    const unsigned chunk = item % (unsigned)chunks, panel = item / (unsigned)chunks;
+    const unsigned tm = panel % tiles_m, batch = panel / tiles_m;
+    long long a_off = 0, b_off = 0, c_off = 0;
+    {
+        unsigned rest = batch;
+        for (int d = g.nbatch - 1; d >= 0; --d) {
+            const unsigned dim = (unsigned)g.bdim[d], q = rest / dim, i = rest - q * dim;
+            rest = q;
+            a_off += (long long)i * g.sa_b[d];
+            b_off += (long long)i * g.sb_b[d];
+            c_off += (long long)i * g.sc_b[d];
+        }
+    }
+    const S* A = (const S*)g.A + a_off;
+    const S* B = (const S*)g.B + b_off;
+    S* C = (S*)g.C + c_off;
+    const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
+    const int sa_m = (int)g.sa_m, sb_n = (int)g.sb_n;
+    const int m0 = (int)tm * 128;
+    const unsigned t_first = chunk * (unsigned)tiles_per_item;
+    const unsigned t_end = t_first + (unsigned)tiles_per_item < tiles_n ? t_first + (unsigned)tiles_per_item : tiles_n;
+    if (t_first >= t_end) return;                    // the whole workgroup: no barrier is skipped by some threads
+    // the item's tiles from a rotated start (panel p begins at its p-th
+    // tile): workgroups that run side by side then write different column
+    // blocks of their rows rather than all the same 128-byte strip of every
+    // row at once
+    const unsigned cnt = t_end - t_first, rot = panel % cnt;
+    auto tile_of = [&](unsigned i) { return t_first + (i + rot) % cnt; };
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 32;
+
+    // A's panel, and the first tile's B, once
+    {
+        LA la;
+        LB lb;
+#pragma unroll
+        for (int kb = 0; kb < NK; ++kb) {
+            la.load(A, M, K, sa_m, 1, m0, kb * BK);
+            la.store(As + kb * ASZ);
+            lb.load(B, N, K, sb_n, 1, (int)tile_of(0) * 64, kb * BK);
+            lb.store(Bs + kb * BSZ);
+        }
+    }
+    __syncthreads();
+
+    bool ovf = false;
+    LB next[NK];
+    for (unsigned i = 0; i < cnt; ++i) {
+        const unsigned t = tile_of(i);
+        const int cur = (int)(i & 1);
+        S* const bcur = Bs + cur * 2 * BSZ;
+        const bool more = i + 1 < cnt;
+        if (more) {
+#pragma unroll
+            for (int kb = 0; kb < NK; ++kb) next[kb].load(B, N, K, sb_n, 1, (int)tile_of(i + 1) * 64, kb * BK);
+        }
+        f32x16 acc[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int kb = 0; kb < NK; ++kb) {
+            const S* as = As + kb * ASZ;
+            const S* bs = bcur + kb * BSZ;
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 16) {
+                const u16x8 b = frag32<true, LD>(bs, wn, kk, lane);
+                const u16x8 a0 = frag32<true, LD>(as, wm, kk, lane);
+                const u16x8 a1 = frag32<true, LD>(as, wm + 32, kk, lane);
+                acc[0] = mfma32<ST>(b, a0, acc[0]);
+                acc[1] = mfma32<ST>(b, a1, acc[1]);
+            }
+        }
+        __syncthreads();                             // every wave is done with this tile's B
+        // the tile's outputs, rounded, into the B buffer: acc[i] holds
+        // output row wm + 32 i + (lane & 31), columns wn + 8 (r >> 2) +
+        // 4 (lane >> 5) + (r & 3)
+        S* const cs = bcur;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                u16x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = round_out<ST>(acc[i][4 * q + e], false, 0.f, ovf);
+                *(u16x4*)&cs[(wm + 32 * i + (lane & 31)) * CLD + wn + 8 * q + 4 * (lane >> 5)] = w;
+            }
+        __syncthreads();
+        // 16 contiguous bytes of one output row a thread, four rows apart
+        const int n0 = (int)t * 64;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = threadIdx.x + u * NT, row = c >> 3, col = (c & 7) * 8;
+            *(u16x8*)&C[(long long)(m0 + row) * g.sc_m + n0 + col] = *(const u16x8*)&cs[row * CLD + col];
+        }
+        if (more) {
+            // the next tile's B into the other buffer (its last reads, the
+            // previous tile's outputs, finished before the barrier above)
+            S* const bnext = Bs + (cur ^ 1) * 2 * BSZ;
+#pragma unroll
+            for (int kb = 0; kb < NK; ++kb) next[kb].store(bnext + kb * BSZ);
+        }
+        __syncthreads();
+    }
+    if (ovf && g.flag) atomicOr(g.flag, 1u);
+}
+
+// every batch entry's output starts on a 16-byte boundary
+bool sc_b_whole(const GemmArgs& g) {
+    for (int d = 0; d < g.nbatch; ++d)
+        if (g.sc_b[d] % 8) return false;
+    return true;
+}
+
+// Whether stream_kernel computes `g` (the tiles the plan chose, every tile
+// whole, k-contiguous aligned operands, no bias, no split, a 16-byte
+// aligned output)
+bool stream_fits(const GemmArgs& g) {
+    return g.stream && g.storage != kF32 && g.bm == 128 && g.bn == 64 && g.splits <= 1 && !g.bias &&
+           g.a_kcontig && g.b_kcontig && g.a_vec && g.b_vec && g.K > 0 && g.K % 64 == 0 && g.K <= 128 &&
+           g.M > 0 && g.M % 128 == 0 && g.N > 0 && g.N % 64 == 0 && g.sc_m % 8 == 0 &&
+           (uintptr_t)g.C % 16 == 0 && g.batch * (g.M / 128) < 0x7fffffffLL && sc_b_whole(g);
+}
+
+template <int ST>
+hipError_t stream_launch(const GemmArgs& g, hipStream_t stream) {
+    const long long panels = g.batch * (g.M / 128), tiles_n = g.N / 64;
+    // enough items to fill two workgroups a CU: each panel's columns split
+    // into `chunks` runs where there are fewer panels than that
+    long long chunks = panels >= 512 ? 1 : (512 + panels - 1) / panels;
+    if (chunks > tiles_n) chunks = tiles_n;
+    const long long per = (tiles_n + chunks - 1) / chunks;
+    chunks = (tiles_n + per - 1) / per;
+    const long long items = panels * chunks;
+    if (items > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (g.K == 64)
+        stream_kernel<ST, 1><<<(unsigned)items, NT, 0, stream>>>(g, (int)per, (int)chunks);
+    else
+        stream_kernel<ST, 2><<<(unsigned)items, NT, 0, stream>>>(g, (int)per, (int)chunks);
+    return hipGetLastError();
+}
+
 template <int ST, int WM, int WN, bool SAFE, bool DL = false, int MF = 16>
 hipError_t launch_shape(const GemmArgs& g, hipStream_t stream) {
     const long long items = (long long)g.tiles_m * g.tiles_n * g.batch * g.splits;
@@ -883,6 +1055,8 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     // contiguous, else the rows) to hold whole aligned vectors
     const bool fast = g.a_vec && g.b_vec;
     hipError_t e;
+    if constexpr (ST != kF32)
+        if (stream_fits(g)) return stream_launch<ST>(g, stream);
     if (ST == kF32 && fast && g.K % St<kF32>::BK == 0) {
         // whole k-blocks of whole vectors: the f32 tiles load straight into LDS
         if (g.bn == 96) e = launch_shape<ST, 4, 3, false, ST == kF32>(g, stream);

@@ -30,6 +30,7 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     int bm;                         // tile rows: 128, or 256 (16-bit storage, 32x32 MFMA tiles)
     int bn;                         // tile columns: 128, 96 or 64
+    bool stream;                    // K of at most two k-blocks may stream B's tiles across a kept A panel
 };
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream);
