@@ -864,27 +864,32 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(GemmArgs g) {
     if (ovf && g.flag) atomicOr(g.flag, 1u);
 }
 
-// Products with K of at most two k-blocks (the attention's scores, K 64 or
-// 128), 16-bit storage, both operands k-contiguous: a workgroup keeps its
-// 128-row panel of A in LDS for the whole K and streams the 64-column tiles
-// of B across it.  Each tile's B is loaded into registers while the
-// previous tile is multiplied and stored, and the output leaves through the
-// B buffer the tile has finished with, so a workgroup's loads, MFMAs and
-// stores overlap across its tiles instead of each tile paying its own
-// prologue and epilogue.  The products are the 128 x 64 tiles' own: the
-// same 32x32x16 MFMAs over the same k-steps in the same order, with the
-// operands' roles exchanged (D = B A^T: lane l then holds output row
-// l & 31 and four consecutive columns, which leave as 8-byte LDS writes).
-// The launcher takes it only where every tile is whole (M % 128, N % 64,
-// K % 64) and no bias or split applies.
+// Products with K of at most two k-blocks (the attention's scores: K 64 or
+// 128 in 16-bit storage, 32 or 64 in f32), both operands k-contiguous: a
+// workgroup keeps its 128-row panel of A in LDS for the whole K and streams
+// the 64-column tiles of B across it.  Each tile's B is loaded into
+// registers while the previous tile is multiplied and stored, and the
+// output leaves through the B buffer the tile has finished with (in f32 in
+// two halves of 64 rows), so a workgroup's loads, MFMAs and stores overlap
+// across its tiles instead of each tile paying its own prologue and
+// epilogue.  The products are the 128 x 64 tiles' own: the same MFMAs
+// (32x32x16 for 16-bit storage, 16x16x4 for f32) over the same k-steps in
+// the same order, with the operands' roles exchanged (D = B A^T: a lane
+// then holds four consecutive columns of one output row, which leave as one
+// LDS write).  The launcher takes it only where every tile is whole (M %
+// 128, N % 64, K a whole number of k-blocks) and no bias or split applies.
 template <int ST, int NK>
 __global__ void __launch_bounds__(NT) stream_kernel(GemmArgs g, int tiles_per_item, int chunks) {
-    typedef unsigned short S;
+    typedef typename St<ST>::S S;
     typedef Loader<ST, true, 128> LA;
     typedef Loader<ST, true, 64> LB;
+    constexpr bool F32 = ST == kF32;
     constexpr int BK = St<ST>::BK, LD = LA::LD, ASZ = LA::SIZE, BSZ = LB::SIZE;
-    constexpr int CLD = 64 + 8;                      // the staged output's row stride (elements)
-    static_assert(128 * CLD <= 2 * BSZ, "a tile's output fits the B buffer it finished with");
+    constexpr int CLD = 64 + (F32 ? 4 : 8);           // the staged output's row stride (elements)
+    constexpr int HALVES = F32 ? 2 : 1, HROWS = 128 / HALVES;
+    constexpr int EPC = 16 / (int)sizeof(S), CPR = 64 / EPC;   // elements a 16-byte chunk, chunks a row
+    static_assert(HROWS * CLD <= 2 * BSZ, "a tile's output (or half of it) fits the B buffer it finished with");
+    static_assert(HROWS * CPR == 4 * NT, "four 16-byte chunks a thread a half");
     __shared__ __attribute__((aligned(16))) S smem[2 * ASZ + 4 * BSZ];
     S* const As = smem;                              // A's k-blocks, [2][128][LD]
     S* const Bs = smem + 2 * ASZ;                    // two buffers of B's k-blocks, [2][2][64][LD]
@@ -953,45 +958,75 @@ __global__ void __launch_bounds__(NT) stream_kernel(GemmArgs g, int tiles_per_it
 #pragma unroll
             for (int kb = 0; kb < NK; ++kb) next[kb].load(B, N, K, sb_n, 1, (int)tile_of(i + 1) * 64, kb * BK);
         }
-        f32x16 acc[2] = {f32x16{}, f32x16{}};
+        // 16-bit: acc16[i] holds output row wm + 32 i + (lane & 31), columns
+        // wn + 8 q + 4 (lane >> 5) + e at element 4 q + e; f32: acc32[i][j]
+        // row wm + 16 i + (lane & 15), columns wn + 16 j + 4 (lane >> 4) + e
+        f32x16 acc16[2] = {f32x16{}, f32x16{}};
+        f32x4 acc32[4][2] = {};
 #pragma unroll
         for (int kb = 0; kb < NK; ++kb) {
             const S* as = As + kb * ASZ;
             const S* bs = bcur + kb * BSZ;
+            if constexpr (F32) {
 #pragma unroll
-            for (int kk = 0; kk < BK; kk += 16) {
-                const u16x8 b = frag32<true, LD>(bs, wn, kk, lane);
-                const u16x8 a0 = frag32<true, LD>(as, wm, kk, lane);
-                const u16x8 a1 = frag32<true, LD>(as, wm + 32, kk, lane);
-                acc[0] = mfma32<ST>(b, a0, acc[0]);
-                acc[1] = mfma32<ST>(b, a1, acc[1]);
+                for (int kk = 0; kk < BK; kk += 4) {
+                    float bf[2], af[4];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) bf[j] = frag<ST, true, LD>(bs, wn + 16 * j, kk, lane);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) af[q] = frag<ST, true, LD>(as, wm + 16 * q, kk, lane);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) acc32[q][j] = mfma<ST>(bf[j], af[q], acc32[q][j]);
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < BK; kk += 16) {
+                    const u16x8 b = frag32<true, LD>((const unsigned short*)bs, wn, kk, lane);
+                    const u16x8 a0 = frag32<true, LD>((const unsigned short*)as, wm, kk, lane);
+                    const u16x8 a1 = frag32<true, LD>((const unsigned short*)as, wm + 32, kk, lane);
+                    acc16[0] = mfma32<ST>(b, a0, acc16[0]);
+                    acc16[1] = mfma32<ST>(b, a1, acc16[1]);
+                }
             }
         }
-        __syncthreads();                             // every wave is done with this tile's B
-        // the tile's outputs, rounded, into the B buffer: acc[i] holds
-        // output row wm + 32 i + (lane & 31), columns wn + 8 (r >> 2) +
-        // 4 (lane >> 5) + (r & 3)
+        // the tile's outputs, rounded, through the B buffer, half by half
         S* const cs = bcur;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                u16x4 w;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = round_out<ST>(acc[i][4 * q + e], false, 0.f, ovf);
-                *(u16x4*)&cs[(wm + 32 * i + (lane & 31)) * CLD + wn + 8 * q + 4 * (lane >> 5)] = w;
-            }
-        __syncthreads();
-        // 16 contiguous bytes of one output row a thread, four rows apart
         const int n0 = (int)t * 64;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int c = threadIdx.x + u * NT, row = c >> 3, col = (c & 7) * 8;
-            *(u16x8*)&C[(long long)(m0 + row) * g.sc_m + n0 + col] = *(const u16x8*)&cs[row * CLD + col];
+        for (int h = 0; h < HALVES; ++h) {
+            __syncthreads();                         // every wave is done with this tile's B (or the last half's reads)
+            if (HALVES == 1 || wm / HROWS == h) {
+                if constexpr (F32) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            *(f32x4*)&cs[(wm - h * HROWS + 16 * q + (lane & 15)) * CLD + wn + 16 * j + 4 * (lane >> 4)] = acc32[q][j];
+                } else {
+#pragma unroll
+                    for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            u16x4 w;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) w[e] = round_out<ST>(acc16[q2][4 * q + e], false, 0.f, ovf);
+                            *(u16x4*)&cs[(wm + 32 * q2 + (lane & 31)) * CLD + wn + 8 * q + 4 * (lane >> 5)] = w;
+                        }
+                }
+            }
+            __syncthreads();
+            // 16 contiguous bytes of one output row a thread, four chunks
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = threadIdx.x + u * NT, row = c / CPR, col = (c % CPR) * EPC;
+                *(uint4*)&C[(long long)(m0 + h * HROWS + row) * g.sc_m + n0 + col] = *(const uint4*)&cs[row * CLD + col];
+            }
         }
         if (more) {
             // the next tile's B into the other buffer (its last reads, the
-            // previous tile's outputs, finished before the barrier above)
+            // previous tile's outputs, finished before the barriers above)
             S* const bnext = Bs + (cur ^ 1) * 2 * BSZ;
 #pragma unroll
             for (int kb = 0; kb < NK; ++kb) next[kb].store(bnext + kb * BSZ);
@@ -1009,11 +1044,12 @@ bool sc_b_whole(const GemmArgs& g) {
 }
 
 // Whether stream_kernel computes `g` (the tiles the plan chose, every tile
-// whole, k-contiguous aligned operands, no bias, no split, a 16-byte
-// aligned output)
+// whole, at most two k-blocks, k-contiguous aligned operands, no bias, no
+// split, a 16-byte aligned output)
 bool stream_fits(const GemmArgs& g) {
-    return g.stream && g.storage != kF32 && g.bm == 128 && g.bn == 64 && g.splits <= 1 && !g.bias &&
-           g.a_kcontig && g.b_kcontig && g.a_vec && g.b_vec && g.K > 0 && g.K % 64 == 0 && g.K <= 128 &&
+    const int bk = g.storage == kF32 ? St<kF32>::BK : St<kBF16>::BK;
+    return g.stream && g.bm == 128 && g.bn == 64 && g.splits <= 1 && !g.bias &&
+           g.a_kcontig && g.b_kcontig && g.a_vec && g.b_vec && g.K > 0 && g.K % bk == 0 && g.K <= 2 * bk &&
            g.M > 0 && g.M % 128 == 0 && g.N > 0 && g.N % 64 == 0 && g.sc_m % 8 == 0 &&
            (uintptr_t)g.C % 16 == 0 && g.batch * (g.M / 128) < 0x7fffffffLL && sc_b_whole(g);
 }
@@ -1029,7 +1065,7 @@ hipError_t stream_launch(const GemmArgs& g, hipStream_t stream) {
     chunks = (tiles_n + per - 1) / per;
     const long long items = panels * chunks;
     if (items > 0x7fffffffLL) return hipErrorInvalidValue;
-    if (g.K == 64)
+    if (g.K == St<ST>::BK)
         stream_kernel<ST, 1><<<(unsigned)items, NT, 0, stream>>>(g, (int)per, (int)chunks);
     else
         stream_kernel<ST, 2><<<(unsigned)items, NT, 0, stream>>>(g, (int)per, (int)chunks);
@@ -1055,8 +1091,7 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     // contiguous, else the rows) to hold whole aligned vectors
     const bool fast = g.a_vec && g.b_vec;
     hipError_t e;
-    if constexpr (ST != kF32)
-        if (stream_fits(g)) return stream_launch<ST>(g, stream);
+    if (stream_fits(g)) return stream_launch<ST>(g, stream);
     if (ST == kF32 && fast && g.K % St<kF32>::BK == 0) {
         // whole k-blocks of whole vectors: the f32 tiles load straight into LDS
         if (g.bn == 96) e = launch_shape<ST, 4, 3, false, ST == kF32>(g, stream);

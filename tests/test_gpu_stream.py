@@ -1,9 +1,10 @@
 """The streamed-panel contraction (gemm.hip's stream_kernel: a 128-row panel
 of A kept in LDS, B's 64-column tiles streamed across it) for products with
-K of at most two k-blocks in 16-bit storage, the attention's scores.  It
-computes each output with the same 32x32x16 MFMAs over the same k-steps as
-the 128 x 64 tiles' kernel, so the two must agree bit for bit; the tiles'
-kernel is the one the plan takes under PRESK_HIP_GEMM_TILE=128x64.  Both
+K of at most two k-blocks, the attention's scores.  It computes each output
+with the same MFMAs (32x32x16 in 16-bit storage, 16x16x4 in f32) over the
+same k-steps as the 128 x 64 tiles' kernel, so the two must agree bit for
+bit; the tiles' kernel is the one the plan takes under
+PRESK_HIP_GEMM_TILE=128x64.  Both
 are also held to the oracle's band on sampled rows (as tests/test_gpu_gemm.py
 bounds a reassociated sum)."""
 import os
@@ -18,7 +19,8 @@ from tests import fmt
 pytestmark = pytest.mark.gpu
 A, O = L.ax, L.Operand
 
-UNIT = {"bf16": 2.0 ** -8, "f16": 2.0 ** -11}
+UNIT = {"bf16": 2.0 ** -8, "f16": 2.0 ** -11, "f32": 2.0 ** -24}
+ESZ = {"bf16": 2, "f16": 2, "f32": 4}
 
 
 def scores(dt, B, H, T, T2, HD):
@@ -36,6 +38,9 @@ CASES = [
     ("few-panels-bf16", "bf16", (1, 2, 256, 2048, 128), 1.0),
     # sums past f16's range: infinities and the overflow flag, as the tiles give them
     ("overflow-f16", "f16", (2, 2, 128, 256, 128), 40.0),
+    # f32 (k-blocks of 32): the course's scores (K 64, the headline's), and K 32
+    ("course-scores-f32", "f32", (64, 6, 256, 256, 64), 1.0),
+    ("k32-f32", "f32", (2, 4, 256, 512, 32), 1.0),
 ]
 
 
@@ -48,20 +53,21 @@ def run(low, ins, tile):
         c = hip.Compiled(low.text, low.dtype, low.lanes, hip.FAST)
     finally:
         os.environ.pop("PRESK_HIP_GEMM_TILE", None)
-    assert c.kind == "gemm" and c.order == "mfma-k16", (c.kind, c.order)
+    assert c.kind == "gemm" and c.order == ("mfma-f32-k4" if low.dtype == "f32" else "mfma-k16"), (c.kind, c.order)
     bufs = [hip.DeviceBuffer.of(a) for a in ins]
     n_out = 1
     for a in low.out_axes:
         n_out *= a.len
-    out = hip.DeviceBuffer(2 * n_out)
-    out.upload(np.full(2 * n_out, 0xFF, np.uint8))
+    esz = ESZ[low.dtype]
+    out = hip.DeviceBuffer(esz * n_out)
+    out.upload(np.full(esz * n_out, 0xFF, np.uint8))
     flag = hip.DeviceBuffer(4)
     flag.zero()
     ptrs = [b.ptr for b in bufs] + [out.ptr] + ([flag.ptr] if c.guarded else [])
     c.run(ptrs)
     hip.sync()
     f = int(flag.download(np.uint32)[0]) if c.guarded else 0
-    return out.download(np.uint16), f
+    return out.download(np.uint16 if esz == 2 else np.float32), f
 
 
 @pytest.mark.parametrize("name,dt,shape,scale", CASES, ids=[c[0] for c in CASES])
@@ -77,7 +83,8 @@ def test_streamed_panels_equal_the_tiles(name, dt, shape, scale):
     got, f_got = run(low, ins, None)
     want, f_want = run(low, ins, "128x64")
     assert f_got == f_want
-    differ = np.count_nonzero(got != want)
+    bits = np.uint16 if dt != "f32" else np.uint32
+    differ = np.count_nonzero(got.view(bits) != want.view(bits))
     assert differ == 0, f"{differ} of {got.size} outputs differ from the 128 x 64 tiles'"
     # the band of a reassociated sum on sampled rows, against float64
     out = fmt.decode(got, dt).astype(np.float64).reshape(B, H, T, T2)
