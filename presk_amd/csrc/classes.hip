@@ -393,12 +393,15 @@ void plan_tiles(GemmArgs& g) {
             g.k_per_split = (nkb + s - 1) / s * bk;  // the longest split
         }
     }
-    // 16-bit storage without a k-split, whole k-blocks, K of 3072 or more
-    // and strides of whole 16-byte vectors: 256 x 256 tiles (a wave 128 x
-    // 128, half the operand bytes a flop of a 128 x 128 tile, one workgroup a
-    // CU) where they fill three rounds of the CUs or more -- measured 5 %
-    // faster than 128 x 128 tiles at [2048 x 4096] . [4096 x 32000], slower
-    // at fewer tiles
+    // 16-bit storage without a k-split, whole k-blocks and strides of whole
+    // 16-byte vectors: 256-row tiles of eight waves (two a SIMD, one
+    // workgroup a CU).  256 x 256 (a wave 128 x 64, half the operand bytes a
+    // flop of a 128 x 128 tile) at K of 3072 or more where they fill three
+    // rounds of the CUs -- [2048 x 4096] . [4096 x 32000] 652 -> 524 us
+    // against 128 x 128 tiles; else 256 x 128 (a wave 64 x 64) at K of 768
+    // or more -- the Llama projections and the MLP block's products 4-18 %
+    // faster than on 128 x 128 tiles (e.g. 2048 x 4096 x 4096 80.6 -> 70.7
+    // us), the course step's K of 384 not
     auto vec_strides = [&](long long other, const long long* bs) {
         if (other % 8) return false;
         for (int d = 0; d < g.nbatch; ++d)
@@ -413,6 +416,13 @@ void plan_tiles(GemmArgs& g) {
         g.bn = 256;
         g.tiles_m = (int)((g.M + 255) / 256);
         g.tiles_n = (int)((g.N + 255) / 256);
+    } else if (g.storage != kF32 && g.splits == 1 && g.K >= 768 && g.K % gemm_block_k(g.storage) == 0 && a_rows_vec &&
+               b_rows_vec && vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) &&
+               vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b)) {
+        g.bm = 256;
+        g.bn = 128;
+        g.tiles_m = (int)((g.M + 255) / 256);
+        g.tiles_n = (int)((g.N + 127) / 128);
     }
     apply_override(g);
 }

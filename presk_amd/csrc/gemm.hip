@@ -17,16 +17,19 @@
 // (deterministic).
 //
 // 16-bit storage, whole k-blocks and strides of whole 16-byte vectors:
-// 256 x 128 or 256 x 256 tiles (K of 3072 or more, no split), each wave
-// 128 x 64 or 128 x 128 as MFMAs of 32x32x16, operands loaded straight into
-// LDS three (two) k-blocks deep (D16Loader), the fragments of each 16-k step
-// read while the previous step's MFMAs run, one workgroup a CU; 128 x 128
-// and 128 x 64 tiles the same way in two stages, two workgroups a CU.
-// Operands off 16 bytes or partial k-blocks take the same tiles and MFMAs
-// from register-staged operands; 128 x 96 tiles take the 16x16 MFMAs below.
+// 256 x 128 tiles (K of 768 or more, no split) or 256 x 256 (K of 3072 or
+// more, three rounds of the CUs), eight waves a workgroup (two a SIMD, one
+// workgroup a CU), each wave 64 x 64 or 128 x 64 as MFMAs of 32x32x16,
+// operands loaded straight into LDS three (two) k-blocks deep (D16Loader),
+// the fragments of each 16-k step read while the previous step's MFMAs run;
+// 128 x 128 and 128 x 64 tiles the same way with four waves in two stages,
+// two or three workgroups a CU.  Operands off 16 bytes or partial k-blocks
+// take four-wave tiles and the same MFMAs from register-staged operands;
+// 128 x 96 tiles take the 16x16 MFMAs below.
 //
-// Workgroup: 256 threads (4 waves as 2x2), tile (2*WM*16) x (2*WN*16), each
-// wave WM x WN MFMA tiles of 16x16.  Operands are staged through LDS,
+// Workgroup: 256 threads (4 waves as 2x2; the 16-bit direct tiles 512, 8
+// waves as 2x4 or 4x2), tile (2*WM*16) x (2*WN*16), each wave WM x WN MFMA
+// tiles of 16x16.  Operands are staged through LDS,
 // double-buffered (one barrier per k-block), each as it lies in memory: a
 // k-contiguous operand as [row][k], an m- or n-contiguous one as [k][row]
 // (16-byte writes either way).  MFMA fragments hold consecutive k of one
@@ -41,6 +44,7 @@
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "devfmt.hpp"
 #include "gemm.hpp"
@@ -242,10 +246,10 @@ __device__ __forceinline__ float frag_dl(const float* xs, int base, int kk, int 
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
-// 16-bit operand tiles (64 k) loaded straight into LDS, three stages deep, in
-// 16-byte chunks placed by an XOR swizzle (lane i of a wave's load fills slot
-// i of the wave's 1 KB segment; the swizzle picks which chunk each lane
-// fetches):
+// 16-bit operand tiles (64 k) loaded straight into LDS, two or three stages
+// deep, in 16-byte chunks placed by an XOR swizzle (lane i of a wave's load
+// fills slot i of the wave's 1 KB segment; the swizzle picks which chunk each
+// lane fetches):
 //   k-contiguous, [row][8 chunks of 8 k]: chunk c of row r in slot
 //     8 r + (c ^ ((r ^ (r >> 3)) & 7))
 //   m/n-contiguous, [k][ROWS / 8 chunks of 8 rows]: chunk j of k-row r in slot
@@ -264,14 +268,14 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 // blocks in flight; the kernel waits for them itself (wait_vm) before the
 // barrier that precedes every read of a stage.  The lane offsets are fixed
 // for the whole k-loop; a block moves the uniform base only.
-template <bool KCONTIG, int ROWS>
+template <bool KCONTIG, int ROWS, int NTH = NT>
 struct D16Loader {
     static constexpr int BK = 64;
     static constexpr int CPR = KCONTIG ? 8 : ROWS / 8;    // chunks per LDS row
     static constexpr int SLOTS = ROWS * BK / 8;           // chunks per tile
-    static constexpr int ROUNDS = SLOTS / NT;             // loads per thread
+    static constexpr int ROUNDS = SLOTS / NTH;            // loads per thread
     static constexpr int BYTES = SLOTS * 16;
-    static_assert(SLOTS % NT == 0, "whole rounds");
+    static_assert(SLOTS % NTH == 0, "whole rounds");
     unsigned voff[ROUNDS];      // byte offsets of this thread's chunks from the origin
     const char* origin;         // the operand's first k-block (uniform)
     long long block_bytes;      // how far one k-block moves the origin (uniform)
@@ -289,7 +293,7 @@ struct D16Loader {
         block_bytes = KCONTIG ? 2LL * BK : 2LL * BK * ks;
 #pragma unroll
         for (int q = 0; q < ROUNDS; ++q) {
-            const int slot = q * NT + t;
+            const int slot = q * NTH + t;
             const int r = slot / CPR, c = (slot % CPR) ^ swz(r);
             long long e;
             if (KCONTIG) {
@@ -311,7 +315,7 @@ struct D16Loader {
 #pragma unroll
         for (int q = 0; q < ROUNDS; ++q)
             asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-                         : : "v"(voff[q]), "s"(src), "s"(lds0 + stage + (unsigned)(q * NT * 16)) : "memory", "m0");
+                         : : "v"(voff[q]), "s"(src), "s"(lds0 + stage + (unsigned)(q * NTH * 16)) : "memory", "m0");
     }
     // the 32x32x16 fragment: lane holds k = kk + 8 (lane >> 5) .. + 8 of row
     // base + (lane & 31) -- one 16-byte read from [row][k], or two
@@ -465,16 +469,43 @@ __device__ __forceinline__ float load_bias(const void* p, long long off) {
     return pk_f16_to_f32(((const unsigned short*)p)[off]);
 }
 
-template <int ST, bool AK, bool BK_, int WM, int WN, bool SAFE, bool DL, int MF>
-__global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
+// Wait until the k-block a stage is about to be read from has landed, with
+// `later` blocks issued after it (NL loads a thread each) still in flight.
+template <int NL, int L>
+__device__ __forceinline__ void wait_blocks(int later) {
+    if constexpr (L == 0) {
+        wait_vm<0>();
+    } else {
+        if (later >= L) wait_vm<L * NL>();
+        else wait_blocks<NL, L - 1>(later);
+    }
+}
+
+// Blocks kt .. kt + sizeof(I) - 1 in stages I (straight-line, so that the
+// accumulators stay in place); the tail takes only the blocks below n.
+template <typename F, int... I>
+__device__ __forceinline__ void stage_round(F& f, int kt, std::integer_sequence<int, I...>) {
+    (f(kt + I, std::integral_constant<int, I>{}), ...);
+}
+template <typename F, int... I>
+__device__ __forceinline__ void stage_tail(F& f, int kt, int n, std::integer_sequence<int, I...>) {
+    ((kt + I < n ? f(kt + I, std::integral_constant<int, I>{}) : void()), ...);
+}
+
+// Workgroups of NW waves (4, or 8: two a SIMD), WAN of them along the tile's
+// columns, each wave WM x WN MFMA tiles of MF x MF.
+template <int ST, bool AK, bool BK_, int WM, int WN, bool SAFE, bool DL, int MF, int NW = 4, int WAN = 2>
+__global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     static_assert(!DL || !SAFE, "direct loads: whole vectors");
     static_assert(MF == 16 || ST != kF32, "32x32 tiles: 16-bit storage");
     constexpr bool D16 = DL && MF == 32;
+    static_assert(NW == 4 || D16, "eight waves: 16-bit tiles loaded straight into LDS");
+    constexpr int NTH = 64 * NW, WAM = NW / WAN;
     typedef typename St<ST>::S S;
     typedef typename St<ST>::Frag Frag;
     typedef typename std::conditional<MF == 32, f32x16, f32x4>::type Acc;
     constexpr int BK = St<ST>::BK, LD = BK + St<ST>::PAD, KSTEP = MF == 32 ? 16 : St<ST>::KSTEP, KPL = St<ST>::KPL;
-    constexpr int BM = 2 * WM * MF, BN = 2 * WN * MF;
+    constexpr int BM = WAM * WM * MF, BN = WAN * WN * MF;
     // LDS: the double-buffered operand tiles, reused by the epilogue for the
     // tile's f32 sums
     typedef Loader<ST, AK, BM> LA;
@@ -484,8 +515,8 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     constexpr int ASZ = DL ? DA::SIZE : LA::SIZE, BSZ = DL ? DB::SIZE : LB::SIZE;
     constexpr int LDA = AK ? LD : LA::LDR, LDB = BK_ ? LD : LB::LDR;
     constexpr int CLD = BN + 4;
-    typedef D16Loader<AK, BM> QA;
-    typedef D16Loader<BK_, BN> QB;
+    typedef D16Loader<AK, BM, NTH> QA;
+    typedef D16Loader<BK_, BN, NTH> QB;
     constexpr int STAGE = QA::BYTES + QB::BYTES;
     // straight-into-LDS stages: three where they fit (256 x 128 tiles, 144 KB),
     // else two (256 x 256, 128 KB); two for 128-row tiles (64 or 48 KB), so
@@ -506,8 +537,10 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     // one batch entry and neighbouring row-tiles share its L2.  With a k-split
     // the panels of one k-range outgrow an L2 anyway, and spreading each
     // range over all XCDs measures faster: items go in plain order.  Within a
-    // run, tiles go 8 row-tiles at a time across the columns, so that
-    // concurrent tiles share A rows.
+    // run, tiles go GROUP row-tiles at a time across the columns, so that
+    // concurrent tiles share A rows: 8 for 128-row tiles (64 a XCD at once,
+    // 8 x 8), 4 for 256-row ones (32 at once: 4 x 8, a block of the output
+    // as tall as it is wide for 256 x 128 tiles).
     // The arithmetic is 32-bit: the launcher keeps the items below 2^31 and
     // the plan the batch below 2^16 (64-bit divisions cost hundreds of scalar
     // instructions a wave, before the first load is issued).
@@ -521,7 +554,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     const int split = (int)(tb / nb);
     const unsigned batch = tb - (unsigned)split * nb;
     const unsigned bid = item - tb * tiles;
-    constexpr unsigned GROUP = 8;
+    constexpr unsigned GROUP = BM == 256 ? 4 : 8;
     const unsigned tiles_m = (unsigned)g.tiles_m;
     const unsigned group_size = GROUP * (unsigned)g.tiles_n;
     const unsigned grp = bid / group_size;
@@ -555,7 +588,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     const int sa_m = (int)g.sa_m, sa_k = (int)g.sa_k, sb_k = (int)g.sb_k, sb_n = (int)g.sb_n;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * (WM * MF), wn = (wave & 1) * (WN * MF);
+    const int wm = (wave / WAN) * (WM * MF), wn = (wave % WAN) * (WN * MF);
     Acc acc[WM][WN];
 #pragma unroll
     for (int i = 0; i < WM; ++i)
@@ -564,15 +597,17 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
 
     const int nk = (kend - kbeg + BK - 1) / BK;
     if constexpr (D16) {
-        // NS stages: block kt + NS - 1 streams into LDS while block kt is
-        // multiplied.  The fragments of each 16-k step are read while the
-        // previous step's MFMAs run; before the last step of a block, the
+        // NS stages: blocks kt + 1 .. kt + NS - 1 stream into LDS while block
+        // kt is multiplied.  The fragments of each 16-k step are read while
+        // the previous step's MFMAs run; before the last step of a block, the
         // next block's first fragments are read once this thread's loads of
-        // that block have landed (those of the block after may still be in
-        // flight) and a barrier has seen every thread's -- the barrier also
-        // retires every read of the stage the next loads overwrite.
+        // that block have landed (those of the blocks after it may still be
+        // in flight) and a barrier has seen every thread's -- the barrier
+        // also retires every read of the stage the next loads overwrite.
         constexpr int NL = QA::ROUNDS + QB::ROUNDS;   // loads a thread issues per block
         constexpr int LA = NS - 1;                    // blocks in flight ahead
+        static_assert((LA - 1) * NL < 64, "vmcnt holds the loads in flight");
+        const int nd = (kend - kbeg) / BK;            // whole blocks (the launcher checks)
         QA qa;
         QB qb;
         unsigned char* const st0 = (unsigned char*)smem;
@@ -590,20 +625,16 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int j = 0; j < WN; ++j) b[j] = QB::frag(st + QA::BYTES, wn + j * 32, kk, lane);
         };
-        if (nk > 0) {
-            fetch(0, 0);
-            if (LA == 2 && nk > 1) {
-                fetch(1, 1);
-                wait_vm<NL>();
-            } else {
-                wait_vm<0>();
-            }
+        if (nd > 0) {
+            const int pre = nd < LA ? nd : LA;
+            for (int kb = 0; kb < pre; ++kb) fetch(kb, kb);
+            wait_blocks<NL, LA - 1>(pre - 1);
             __syncthreads();
             read(st0, 0);
         }
         auto block = [&](int kt, auto stage) {
             constexpr int S = decltype(stage)::value;
-            if (kt + LA < nk) fetch(kt + LA, (S + LA) % NS);
+            if (kt + LA < nd) fetch(kt + LA, (S + LA) % NS);
             const unsigned char* const st = st0 + S * STAGE;
 #pragma unroll
             for (int kk = 0; kk < BK; kk += KSTEP) {
@@ -614,9 +645,9 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
                 for (int j = 0; j < WN; ++j) cb[j] = b[j];
                 if (kk + KSTEP < BK) {
                     read(st, kk + KSTEP);
-                } else if (kt + 1 < nk) {
-                    if (LA == 2 && kt + 2 < nk) wait_vm<NL>();
-                    else wait_vm<0>();
+                } else if (kt + 1 < nd) {
+                    const int last = kt + LA < nd - 1 ? kt + LA : nd - 1;   // the last block issued
+                    wait_blocks<NL, LA - 1>(last - (kt + 1));
                     __syncthreads();
                     read(st0 + ((S + 1) % NS) * STAGE, 0);
                 }
@@ -630,26 +661,10 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
-        // whole rounds of the stages, then the last blocks (straight-line
-        // rounds keep the accumulators in place)
+        // whole rounds of the stages, then the last blocks
         int kt = 0;
-        if constexpr (NS == 3) {
-            for (; kt + 3 <= nk; kt += 3) {
-                block(kt, std::integral_constant<int, 0>{});
-                block(kt + 1, std::integral_constant<int, 1>{});
-                block(kt + 2, std::integral_constant<int, 2>{});
-            }
-            if (kt < nk) {
-                block(kt, std::integral_constant<int, 0>{});
-                if (kt + 1 < nk) block(kt + 1, std::integral_constant<int, 1>{});
-            }
-        } else {
-            for (; kt + 2 <= nk; kt += 2) {
-                block(kt, std::integral_constant<int, 0>{});
-                block(kt + 1, std::integral_constant<int, 1>{});
-            }
-            if (kt < nk) block(kt, std::integral_constant<int, 0>{});
-        }
+        for (; kt + NS <= nd; kt += NS) stage_round(block, kt, std::make_integer_sequence<int, NS>{});
+        stage_tail(block, kt, nd, std::make_integer_sequence<int, NS - 1>{});
     } else if constexpr (DL && MF == 16) {
         // One k-block ahead: block kt+1 streams into one LDS buffer while
         // block kt is multiplied out of the other; a block ends with this
@@ -746,7 +761,7 @@ __global__ void __launch_bounds__(NT) gemm_kernel(GemmArgs g) {
     // 16 contiguous bytes of one output row.
     float* const cs = (float*)smem;
     constexpr int OV = 16 / (int)sizeof(S);  // output elements per 16-byte store
-    constexpr int TPR = BN / OV, RPR = NT / TPR;  // threads past TPR*RPR store nothing
+    constexpr int TPR = BN / OV, RPR = NTH / TPR;  // threads past TPR*RPR store nothing
     bool ovf = false;
     const long long cbase = c_off;
     S* C = (S*)g.C + cbase;
@@ -1072,16 +1087,17 @@ hipError_t stream_launch(const GemmArgs& g, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int ST, int WM, int WN, bool SAFE, bool DL = false, int MF = 16>
+template <int ST, int WM, int WN, bool SAFE, bool DL = false, int MF = 16, int NW = 4, int WAN = 2>
 hipError_t launch_shape(const GemmArgs& g, hipStream_t stream) {
     const long long items = (long long)g.tiles_m * g.tiles_n * g.batch * g.splits;
     if (items <= 0) return hipSuccess;
     if (items > 0x7fffffffLL) return hipErrorInvalidValue;
     dim3 grid((unsigned)items, 1, 1);
-    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
-    else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
-    else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
-    else gemm_kernel<ST, false, false, WM, WN, SAFE, DL, MF><<<grid, NT, 0, stream>>>(g);
+    constexpr int T = 64 * NW;
+    if (g.a_kcontig && g.b_kcontig) gemm_kernel<ST, true, true, WM, WN, SAFE, DL, MF, NW, WAN><<<grid, T, 0, stream>>>(g);
+    else if (g.a_kcontig) gemm_kernel<ST, true, false, WM, WN, SAFE, DL, MF, NW, WAN><<<grid, T, 0, stream>>>(g);
+    else if (g.b_kcontig) gemm_kernel<ST, false, true, WM, WN, SAFE, DL, MF, NW, WAN><<<grid, T, 0, stream>>>(g);
+    else gemm_kernel<ST, false, false, WM, WN, SAFE, DL, MF, NW, WAN><<<grid, T, 0, stream>>>(g);
     return hipGetLastError();
 }
 
@@ -1104,10 +1120,13 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
         // register-staged tiles, element-wise loads
         if constexpr (ST != kF32) {
             const bool whole = fast && g.K % St<ST>::BK == 0 && (g.splits <= 1 || g.k_per_split % St<ST>::BK == 0);
-            if (g.bn == 256)  // 256 x 256 tiles, a wave 128 x 128
-                e = whole ? launch_shape<ST, 4, 4, false, true, 32>(g, stream) : launch_shape<ST, 4, 4, true, false, 32>(g, stream);
+            // whole k-blocks: eight waves (two a SIMD), a wave 128 x 64 of
+            // the 256 x 256 tiles (2 x 4 waves) or 64 x 64 of the 256 x 128
+            // ones (4 x 2); else four waves of register-staged operands
+            if (g.bn == 256)
+                e = whole ? launch_shape<ST, 4, 2, false, true, 32, 8, 4>(g, stream) : launch_shape<ST, 4, 4, true, false, 32>(g, stream);
             else
-                e = whole ? launch_shape<ST, 4, 2, false, true, 32>(g, stream) : launch_shape<ST, 4, 2, true, false, 32>(g, stream);
+                e = whole ? launch_shape<ST, 2, 2, false, true, 32, 8, 2>(g, stream) : launch_shape<ST, 4, 2, true, false, 32>(g, stream);
         } else {
             e = hipErrorInvalidValue;
         }

@@ -142,11 +142,11 @@ def test_fast_contraction_within_band(ex, case):
     assert np.median(err / bound) < 1 / 64, f"{name}: median error {np.median(err / bound):.3g} of the band"
 
 
-# K >= 3072, whole k-blocks, aligned vectors, no k-split: 128 x 128 and
-# 128 x 64 tiles of 32x32x16 MFMAs loaded straight into LDS two k-blocks
-# deep, 256 x 256 tiles (two k-blocks deep, the sums staged in two halves)
-# where they make three rounds of the CUs, and, under PRESK_HIP_GEMM_TILE,
-# the 256 x 128 tiles (three k-blocks deep).  Each operand layout
+# K >= 3072, whole k-blocks, aligned vectors, no k-split: the eight-wave
+# 256-row tiles of 32x32x16 MFMAs loaded straight into LDS -- 256 x 128
+# (three k-blocks deep) and, where they make three rounds of the CUs,
+# 256 x 256 (two k-blocks deep, the sums staged in two halves) -- and, under
+# PRESK_HIP_GEMM_TILE, the four-wave 128 x 128 tiles.  Each operand layout
 # (k-contiguous or not), every remainder of the stage rounds, rows past a
 # tile, the bias.  Every output must be written (the buffer is poisoned with
 # NaNs) and 20 000 sampled elements must lie within gamma_K S plus the
@@ -171,7 +171,7 @@ D16 = {
 # the 256 x 256 tiles are the same code in f16 as in bf16: bf16 covers them at size
 @pytest.mark.parametrize("layout,dt,tiles", [(lay, dt, None) for lay in D16 for dt in ("bf16", "f16")
                                              if dt == "bf16" or D16[lay][2] <= 256 * 128]
-                         + [("nn", "bf16", "256x128"), ("tt", "bf16", "256x128"), ("tn", "f16", "256x128")])
+                         + [("nn", "bf16", "128x128"), ("tt", "bf16", "128x128"), ("tn", "f16", "128x128")])
 def test_d16_tiles_within_band(ex, layout, dt, tiles, monkeypatch):
     from oracle import kernel_text as kt
     mk, form, tile = D16[layout]
@@ -207,3 +207,45 @@ def test_d16_tiles_within_band(ex, layout, dt, tiles, monkeypatch):
     err = np.abs(g - exact)
     assert np.all(err <= bound), f"{np.count_nonzero(err > bound)} sampled elements outside the band"
     assert np.median(err / bound) < 1 / 16, f"median error {np.median(err / bound):.3g} of the band"
+
+
+# The eight-wave 256-row tiles (two waves a SIMD) compute each output with
+# the same 32x32x16 MFMAs over the same k-steps as the four-wave 128 x 128
+# tiles, so the two must agree bit for bit -- in every operand layout, with
+# rows and columns past the last tile, and with the bias.
+EIGHT = {
+    "nn": lambda dt: L.dot([O(A(("batch", 1040), 1024)), O(A(1024, 392))], dt),
+    "nt": lambda dt: L.dot_vjp_l([O(A(("batch", 520), 768)), O(A(648, 768))], dt),
+    "tn": lambda dt: L.dot_vjp_r([O(A(("batch", 1024), 264)), O(A(("batch", 1024), 520))], dt),
+    "tt": lambda dt: L.ein([O(A(("k", 832), ("m", 776))), O(A(("n", 264), ("k", 832)))], [["k", "m"], ["n", "k"]],
+                           ["m", "n"], dt),
+    "bias": lambda dt: L.dot([O(A(("batch", 1288), 768)), O(A(768, 520)), O(A(520))], dt,
+                             epilogue=(True, A(("batch", 1288), 520))),
+}
+
+
+@pytest.mark.parametrize("layout,dt,tiles", [(lay, "bf16", t) for lay in EIGHT for t in ("256x128", "256x256")]
+                         + [("nn", "f16", "256x128"), ("tt", "f16", "256x256")])
+def test_eight_wave_tiles_equal_the_128_row_tiles(layout, dt, tiles, monkeypatch):
+    from oracle import kernel_text as kt
+    low = EIGHT[layout](dt)
+    print(f"[gemm] eight waves {layout} {dt} {tiles}", flush=True)
+    k = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(9)
+    ins = [hip.DeviceBuffer.of(fmt.encode(fmt.roundtrip(rng.standard_normal(b.dims, dtype=np.float32), dt), dt))
+           for b in k.inputs]
+    outs = []
+    # (the 128 x 128 tiles unsplit: a k-split adds its partials in another order)
+    for t in (tiles, "128x128/1"):
+        monkeypatch.setenv("PRESK_HIP_GEMM_TILE", t)
+        c = hip.Compiled(low.text, dt, low.lanes, hip.FAST)
+        assert c.kind == "gemm" and c.order == "mfma-k16", (c.kind, c.order)
+        out = hip.DeviceBuffer(k.output.numel * 2)
+        out.upload(np.full(k.output.numel * 2, 0xFF, np.uint8))
+        flag = hip.DeviceBuffer(4)
+        flag.zero()
+        c.run([b.ptr for b in ins] + [out.ptr] + ([flag.ptr] if c.guarded else []))
+        hip.sync()
+        outs.append(out.download(np.uint16))
+    differ = np.count_nonzero(outs[0] != outs[1])
+    assert differ == 0, f"{differ} of {outs[0].size} outputs differ from the 128 x 128 tiles'"
