@@ -501,6 +501,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     constexpr bool D16 = DL && MF == 32;
     static_assert(NW == 4 || D16, "eight waves: 16-bit tiles loaded straight into LDS");
     constexpr int NTH = 64 * NW, WAM = NW / WAN;
+    // f32 storage: the MFMAs take the operands' roles exchanged (D = B^T A^T,
+    // the same products over the same k-steps, so the same sums bit for
+    // bit), and a lane then holds four consecutive columns of one output
+    // row, which leave as one 16-byte store straight from the registers
+    constexpr bool SWAP = ST == kF32 && MF == 16;
     typedef typename St<ST>::S S;
     typedef typename St<ST>::Frag Frag;
     typedef typename std::conditional<MF == 32, f32x16, f32x4>::type Acc;
@@ -527,7 +532,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     constexpr int EH = BM * CLD * 4 <= 150 * 1024 ? 1 : 2, EROWS = BM / EH;
     constexpr int OPER = D16 ? NS * STAGE : 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = EROWS * CLD * 4;
     static_assert(EH == 1 || (WM * MF) % EROWS == 0, "each wave's rows lie in one half");
-    __shared__ __attribute__((aligned(16))) char smem[OPER > CTILE ? OPER : CTILE];
+    // (the exchanged-roles f32 tiles store their sums from the registers)
+    __shared__ __attribute__((aligned(16))) char smem[SWAP || OPER > CTILE ? OPER : CTILE];
     S* const As0 = (S*)smem;
     S* const Bs0 = As0 + 2 * ASZ;
 
@@ -693,7 +699,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int i = 0; i < WM; ++i)
 #pragma unroll
-                    for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
+                    for (int j = 0; j < WN; ++j) acc[i][j] = SWAP ? mfma<ST>(b[j], a[i], acc[i][j]) : mfma<ST>(a[i], b[j], acc[i][j]);
             }
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
@@ -745,7 +751,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
 #pragma unroll
                     for (int i = 0; i < WM; ++i)
 #pragma unroll
-                        for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(a[i], b[j], acc[i][j]);
+                        for (int j = 0; j < WN; ++j) acc[i][j] = SWAP ? mfma<ST>(b[j], a[i], acc[i][j]) : mfma<ST>(a[i], b[j], acc[i][j]);
                 }
             }
             if (kt + 1 < nk) {
@@ -756,6 +762,60 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
         }
     }
 
+    if constexpr (SWAP) {
+        // lane holds row (lane & 15) and columns 4 (lane >> 4) .. + 3 of each
+        // 16 x 16 tile; no overflow guard in f32.  A per-column bias is read
+        // once a column group, for every row the lane stores.
+        float* const C = (float*)g.C + c_off;
+        const bool cvec = g.sc_m % 4 == 0 && (uintptr_t)C % 16 == 0;
+        const bool wvec = N % 4 == 0;
+        const bool has_bias = g.bias && g.splits <= 1;
+        const float bscalar = has_bias && g.bias_kind == 3 ? load_bias<ST>(g.bias, 0) : 0.f;
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int n = (int)n0 + wn + j * 16 + 4 * (lane >> 4);
+            if (n >= N) continue;
+            const bool full = n + 4 <= N;
+            f32x4 bc = {bscalar, bscalar, bscalar, bscalar};
+            if (has_bias && g.bias_kind == 1) {
+                if (full && (uintptr_t)g.bias % 16 == 0) {
+                    bc = *(const f32x4*)((const float*)g.bias + n);
+                } else {
+                    for (int e = 0; e < 4 && n + e < N; ++e) bc[e] = load_bias<ST>(g.bias, n + e);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const int m = (int)m0 + wm + i * 16 + (lane & 15);
+                if (m >= M) continue;
+                f32x4 v = acc[i][j];
+                if (g.splits > 1) {
+                    float* w = g.work + ((long long)split * M + m) * N + n;
+                    if (full && wvec) {
+                        *(f32x4*)w = v;
+                    } else {
+                        for (int e = 0; e < 4 && n + e < N; ++e) w[e] = v[e];
+                    }
+                    continue;
+                }
+                if (has_bias) {
+                    if (g.bias_kind == 2) {
+                        for (int e = 0; e < 4 && n + e < N; ++e) v[e] = v[e] + load_bias<ST>(g.bias, (long long)m * N + n + e);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = v[e] + bc[e];
+                    }
+                }
+                float* c = C + (long long)m * g.sc_m + n;
+                if (full && cvec) {
+                    *(f32x4*)c = v;
+                } else {
+                    for (int e = 0; e < 4 && n + e < N; ++e) c[e] = v[e];
+                }
+            }
+        }
+        return;
+    } else {
     // The tile's sums go through LDS (lane holds column lane & 15, rows
     // 4*(lane >> 4) + r of each 16x16 tile) so that each thread then stores
     // 16 contiguous bytes of one output row.
@@ -844,6 +904,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     }
     }
     if (ovf && g.flag) atomicOr(g.flag, 1u);
+    }
 }
 
 // The split partial sums added in increasing split order, then the epilogue.
