@@ -17,6 +17,7 @@
 #include <sstream>
 #include <unordered_map>
 
+#include "branches.hpp"
 #include "convert.hpp"
 #include "synth.hpp"
 #include "executor.hpp"
@@ -539,92 +540,22 @@ namespace {
 constexpr int kMaxBranches = 8;
 constexpr bool kBranchesOn = false;
 
-// The byte ranges a step reads and writes.  The overflow flag is left out:
-// every store into it writes the same nonzero word and only the host reads
-// it, after the sequence, so steps that share it commute.
-struct Span {
-    uintptr_t lo, hi;
-};
-
-size_t spec_bytes(const BufSpec& s) {
-    return s.ty == Ty::Q4 ? (size_t)((s.numel() + 1) / 2) : (size_t)s.numel() * (size_t)ty_bytes(s.ty);
-}
-
-size_t code_bytes(int t) { return t == 0 ? 8 : t == 1 ? 4 : t == 5 ? 3 : 2; }
-
-void step_spans(const presk_hip_batch::Item& it, std::vector<Span>* rd, std::vector<Span>* wr) {
-    auto add = [](std::vector<Span>* v, const void* p, size_t bytes) {
-        if (p && bytes) v->push_back({(uintptr_t)p, (uintptr_t)p + bytes});
-    };
-    if (it.k) {
-        const Kernel& k = *it.k->k;
-        for (int b = 0; b < k.out_buf(); ++b) {
-            add(rd, it.bufs[b], spec_bytes(k.inputs[b]));
-            const int s = k.scale_slot(b);
-            if (s >= 0) add(rd, it.bufs[s], (size_t)k.inputs[b].scale_count() * sizeof(float));
-        }
-        add(wr, it.bufs[k.out_buf()], spec_bytes(k.output));
-    } else if (it.rate >= 0.0) {
-        add(rd, it.bufs[0], 32);   // the ChaCha20 key
-        add(wr, it.bufs[1], (size_t)it.n * code_bytes(it.to));
-    } else {
-        add(rd, it.bufs[0], (size_t)it.n * code_bytes(it.from));
-        add(wr, it.bufs[1], (size_t)it.n * code_bytes(it.to));
+// The batch's items as the branch planner (branches.hpp) reads them.
+std::vector<BranchStep> branch_steps(const presk_hip_batch& b) {
+    std::vector<BranchStep> out;
+    out.reserve(b.items.size());
+    for (const auto& it : b.items) {
+        BranchStep st;
+        st.k = it.k ? it.k->k.get() : nullptr;
+        st.handle = it.k;
+        st.bufs = it.bufs;
+        st.from = it.from;
+        st.to = it.to;
+        st.n = it.n;
+        st.rate = it.rate;
+        out.push_back(std::move(st));
     }
-}
-
-bool meet(const std::vector<Span>& a, const std::vector<Span>& b) {
-    for (const Span& x : a)
-        for (const Span& y : b)
-            if (x.lo < y.hi && y.lo < x.hi) return true;
-    return false;
-}
-
-// Streams for a branched capture of the sequence.  Step j depends on an
-// earlier step i when one writes bytes the other reads or writes, or when
-// both launch the same compiled kernel (its workspace is one per handle).
-// Each step goes on the stream whose last step it depends on (no wait), else
-// on an idle stream, else behind the oldest stream's last step; it then waits
-// for the latest step it depends on on each other stream, unless that stream
-// is already known to be done up to there.  One stream: program order.
-void plan_branches(const presk_hip_batch& b, int branches, std::vector<int>* lane,
-                   std::vector<std::vector<std::pair<int, int>>>* waits) {
-    const int n = (int)b.items.size();
-    lane->assign(n, 0);
-    waits->assign(n, {});
-    if (branches <= 1) return;
-    std::vector<std::vector<Span>> rd(n), wr(n);
-    for (int i = 0; i < n; ++i) step_spans(b.items[i], &rd[i], &wr[i]);
-    std::vector<int> last(branches, -1);                                  // each stream's last step
-    std::vector<std::vector<int>> known(branches, std::vector<int>(branches, -1));   // known[s][t]: t done up to this step before s's end
-    for (int j = 0; j < n; ++j) {
-        std::vector<int> dep(branches, -1);   // the latest step j depends on, per stream
-        for (int i = j - 1; i >= 0; --i) {
-            const int t = (*lane)[i];
-            if (dep[t] >= i) continue;
-            const bool same = b.items[i].k && b.items[i].k == b.items[j].k;
-            if (same || meet(wr[i], rd[j]) || meet(wr[i], wr[j]) || meet(rd[i], wr[j])) dep[t] = i;
-        }
-        int s = -1;
-        for (int t = 0; t < branches; ++t)   // continue the chain of the latest dependency
-            if (last[t] >= 0 && last[t] == dep[t] && (s < 0 || dep[t] > dep[s])) s = t;
-        if (s < 0)
-            for (int t = 0; t < branches && s < 0; ++t)
-                if (last[t] < 0) s = t;
-        if (s < 0) {
-            s = 0;
-            for (int t = 1; t < branches; ++t)
-                if (last[t] < last[s]) s = t;
-        }
-        (*lane)[j] = s;
-        for (int t = 0; t < branches; ++t) {
-            if (t == s || dep[t] < 0 || known[s][t] >= dep[t]) continue;
-            (*waits)[j].push_back({t, dep[t]});
-            known[s][t] = dep[t];
-        }
-        last[s] = j;
-        known[s][s] = j;
-    }
+    return out;
 }
 
 }  // namespace
@@ -710,7 +641,7 @@ int presk_hip_batch_graph_branches(presk_hip_batch* b, int branches) {
     const int n = (int)b->items.size();
     std::vector<int> lane;       // each step's capture stream
     std::vector<std::vector<std::pair<int, int>>> waits;   // (stream, step) events each step waits for
-    plan_branches(*b, branches, &lane, &waits);
+    plan_branches(branch_steps(*b), branches, &lane, &waits);
     int used = 1;
     for (int s : lane) used = std::max(used, s + 1);
     std::vector<hipStream_t> cs(used, nullptr);
