@@ -112,6 +112,49 @@ def _traffic_table() -> dict:
         return {}
 
 
+def measured_peaks() -> dict:
+    """The peaks measured on this device, reported beside the vendor's
+    nominal ones: the matrix cores' rate in independent MFMA loops (eight
+    waves on every CU, nothing else issued; presk_hip_mfma_probe) and the
+    HBM rate of a plain copy nest (neg over 64 Mi f32: 256 MiB read and 256
+    MiB written a launch, more than the Infinity Cache holds; HIP events over
+    10 launches after 2)."""
+    import ctypes
+    from presk_amd import hip, lower as L
+    hip.init(0)
+    lib = hip.lib()
+    out = {}
+    for ty in ("bf16", "f32"):
+        ms, fl = ctypes.c_double(), ctypes.c_double()
+        hip.check(lib.presk_hip_mfma_probe(ty.encode(), 20000, None, ctypes.byref(ms), ctypes.byref(fl)))
+        out[f"mfma_{ty}_tflops"] = round(fl.value / (ms.value * 1e-3) / 1e12, 1)
+    x = L.Operand(L.ax(("rows", 16384), ("cols", 4096)))
+    low = L.unary("neg", [x], "f32")
+    c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+    n = 16384 * 4096
+    a, b = hip.DeviceBuffer(4 * n), hip.DeviceBuffer(4 * n)
+    a.zero()
+    tab = (ctypes.c_void_p * 2)(a.ptr, b.ptr)
+    ms = ctypes.c_double()
+    hip.check(lib.presk_hip_time(c.handle, tab, 0, max(c.split_bound, 0), None, 2, 10, ctypes.byref(ms)))
+    out["hbm_copy_gbs"] = round(8 * n / (ms.value * 1e-3) / 1e9, 1)
+    out["probe"] = ("MFMA: v_mfma_f32_32x32x16_bf16 / v_mfma_f32_16x16x4_f32 loops, 8 waves a CU, 8 accumulators "
+                    "a wave; HBM: neg over f32[16384, 4096], bytes read + written over time")
+    return out
+
+
+def with_measured(roof: dict, storage: str, peaks) -> dict:
+    """The roofline beside the measured peak of its bound (the vendor figure
+    stays `peak` and `frac`)."""
+    if not peaks:
+        return roof
+    if roof["bound"] == "mfma":
+        pm = peaks["mfma_bf16_tflops" if storage in ("bf16", "f16") else "mfma_f32_tflops"]
+    else:
+        pm = peaks["hbm_copy_gbs"]
+    return dict(roof, peak_measured=pm, frac_of_measured=round(roof["achieved"] / pm, 4))
+
+
 def copy_probe():
     """neg over 64 Mi f32 (256 MiB read, 256 MiB written), three launches."""
     from presk_amd import hip, lower as L
@@ -210,7 +253,8 @@ def cpu_baseline(name, dtype, rows_all, rows_one, realize=None, dropout=0.0, ada
                                    f"({secs1} s a call)"}}
 
 
-def measure(name, dtype, steps, warmup, realize=None, dropout=0.0, adamw=False, eager=False, dominant_match=None):
+def measure(name, dtype, steps, warmup, realize=None, dropout=0.0, adamw=False, eager=False, dominant_match=None,
+            peaks=None):
     """Times one workload: its launches as one HIP graph (or eager), W untimed
     calls, K timed between synchronizations; then each launch alone with HIP
     events on its stream, the slowest giving the roofline.  Returns
@@ -263,6 +307,7 @@ def measure(name, dtype, steps, warmup, realize=None, dropout=0.0, adamw=False, 
                 "ms_per_launch": round(ms, 5), "algorithmic_bytes": c.bytes}
     if traffic is None:
         roof["traffic_note"] = "no counter measurement of this kernel on these device sources (profiles/traffic.json)"
+    roof = with_measured(roof, ln.low.dtype, peaks)
     agg = {}
     for l, m in times:
         e = agg.setdefault(l.low.name, {"kernel": l.low.name, "kind": l.compiled.kind, "launches": 0, "ms": 0.0})
@@ -613,6 +658,8 @@ def main():
     ap.add_argument("--dominant-match", default=None, metavar="TEXT",
                     help="take the dominant launch among those whose key contains TEXT (counter runs distort "
                          "the timings the choice is made on)")
+    ap.add_argument("--peaks", action="store_true",
+                    help="measure the device's MFMA rate (bf16, f32) and a copy nest's HBM rate, print them and exit")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain copy-like nest (neg over 64 Mi f32) 3 times and exit: the counters' calibration")
     ap.add_argument("--per-launch", default=None, metavar="FILE",
@@ -643,7 +690,8 @@ def main():
         return
     # the CPU baseline first, in child processes, before the GPU is touched
     cpu = None
-    if not args.no_cpu and not args.copy_probe and not args.dominant_only and not args.yardstick and not args.traffic_run:
+    if not args.no_cpu and not args.copy_probe and not args.dominant_only and not args.yardstick and not args.traffic_run \
+            and not args.peaks:
         # gpt-step: B 16 x T 256, the batch of the reference's own published rows
         rows_all = args.cpu_rows or {"mlp": 2048, "linear": 512, "gpt-step": 4096, "gpt-forward": 4096}.get(args.workload)
         rows_one = {"mlp": 256, "linear": 64, "gpt-step": 256, "gpt-forward": 256}.get(args.workload)
@@ -661,8 +709,13 @@ def main():
     if args.traffic_run:
         traffic_run(args.traffic_run)
         return
+    if args.peaks:
+        print(json.dumps({"measured_peaks": measured_peaks()}), flush=True)
+        return
+    # the measured peaks beside the vendor's (not in the counter runs of one launch)
+    peaks = None if args.dominant_only else measured_peaks()
     rec, p, (ln, c) = measure(args.workload, dtype, args.steps, args.warmup, args.realize, args.dropout, args.adamw,
-                              args.eager, args.dominant_match)
+                              args.eager, args.dominant_match, peaks)
     if args.per_launch:
         per_launch_table(p, args.per_launch)
     if args.dominant_only:
@@ -681,6 +734,8 @@ def main():
            "data": DATA.get(args.workload, "synthetic (seeded N(0,1) inputs, xavier weights)"),
            "config": rec["config"], "matmul_tflops": rec["matmul_tflops"], "matmul_frac_of_peak": rec["matmul_frac_of_peak"],
            "roofline": rec["roofline"], "kernels": rec["kernels"], "kernel_ms_sum": rec["kernel_ms_sum"]}
+    if peaks:
+        out["measured_peaks"] = peaks
     if cpu is not None:
         out["cpu_baseline"] = cpu
     del p
@@ -689,7 +744,7 @@ def main():
         for name, dt, real in SUPPLEMENTARY:
             if (name, dt) == (args.workload, dtype):
                 continue
-            r, q, _ = measure(name, dt, 10 if name != "llama" else 5, 3 if name != "llama" else 2, real)
+            r, q, _ = measure(name, dt, 10 if name != "llama" else 5, 3 if name != "llama" else 2, real, peaks=peaks)
             del q
             gc.collect()
             sup.append({k: r[k] for k in ("value", "unit", "ms_per_step", "dtype", "config", "matmul_tflops",

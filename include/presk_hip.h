@@ -240,6 +240,14 @@ int presk_hip_dropout_mask(const void *key, double rate, const char *type, int64
  * the reference's draws.  std = 0 fills the constant `mean`. */
 int presk_hip_fill_normal(void *dst, const char *type, int64_t n, uint64_t seed, double mean, double std, void *stream);
 
+/* A measurement aid with no counterpart in the reference: the matrix cores'
+ * rate measured on this device, reported beside the vendor's nominal peak.
+ * One timed launch (after an untimed one) of independent MFMA loops, eight
+ * waves on every CU, each wave `iters` rounds of eight MFMAs: `type` "bf16"
+ * (32x32x16) or "f32" (16x16x4).  *ms the launch's duration (HIP events on
+ * `stream`), *flops the flops it performed. */
+int presk_hip_mfma_probe(const char *type, int64_t iters, void *stream, double *ms, double *flops);
+
 /* Self-test of the device's scalar functions over a domain block: the digest
  * (sum of splitmix64 finalizers of (i << 32 | out_i)) of function `fn` over
  * inputs [lo, hi), as tests/golden/digests.json holds the reference's.  For

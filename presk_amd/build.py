@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG, "csrc")
 OUT = os.path.join(PKG, "libpresk_hip.so")
 BUILD = os.path.join(PKG, "_build")
 
-SOURCES = ["ir.cpp", "hipgen.cpp", "presk_hip.cpp", "selftest.hip", "classes.hip", "gemm.hip", "reduce.hip", "rows.hip", "wrows.hip", "scatter.hip", "convert.hip", "synth.hip"]
+SOURCES = ["ir.cpp", "hipgen.cpp", "presk_hip.cpp", "selftest.hip", "classes.hip", "gemm.hip", "reduce.hip", "rows.hip", "wrows.hip", "scatter.hip", "convert.hip", "synth.hip", "probe.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # f32 semantics the parity rests on: no contraction into FMA, IEEE denormals,

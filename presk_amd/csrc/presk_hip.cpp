@@ -19,6 +19,7 @@
 
 #include "branches.hpp"
 #include "convert.hpp"
+#include "probe.hpp"
 #include "synth.hpp"
 #include "executor.hpp"
 
@@ -728,6 +729,15 @@ int presk_hip_fill_normal(void* dst, const char* type, int64_t n, uint64_t seed,
     if (n < 0 || (n > 0 && !dst)) return fail(PRESK_HIP_ERR, "E10001: bad fill arguments");
     hipError_t e = synth_normal_launch(dst, t, n, seed, (float)mean, (float)std, (hipStream_t)stream);
     return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "fill");
+}
+
+int presk_hip_mfma_probe(const char* type, int64_t iters, void* stream, double* ms, double* flops) {
+    const std::string t = type ? type : "";
+    if ((t != "bf16" && t != "f32") || iters <= 0 || !ms || !flops)
+        return fail(PRESK_HIP_ERR, "E10001: an MFMA probe of type `" + t + "` (bf16 or f32) and iters > 0");
+    if (g_device < 0) return fail(PRESK_HIP_ERR, "E10001: no device (presk_hip_init)");
+    hipError_t e = mfma_probe(t == "bf16" ? 0 : 1, iters, (hipStream_t)stream, ms, flops);
+    return e == hipSuccess ? PRESK_HIP_OK : hip_fail(e, "MFMA probe");
 }
 
 }  // extern "C"

@@ -28,7 +28,7 @@ SYMBOLS = ["presk_hip_init", "presk_hip_last_error", "presk_hip_compile", "presk
            "presk_hip_scalar_digest", "presk_hip_batch_create", "presk_hip_batch_add", "presk_hip_batch_graph", "presk_hip_batch_graph_branches",
            "presk_hip_batch_run", "presk_hip_batch_release", "presk_hip_convert", "presk_hip_batch_add_convert",
            "presk_hip_fill_normal", "presk_hip_dropout_mask", "presk_hip_batch_add_dropout",
-           "presk_hip_pskd_decode", "presk_hip_pskd_decode_idx"]
+           "presk_hip_pskd_decode", "presk_hip_pskd_decode_idx", "presk_hip_mfma_probe"]
 
 
 class HipError(RuntimeError):
@@ -87,6 +87,7 @@ def lib():
         L.presk_hip_batch_release.restype = None
         L.presk_hip_convert.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_char_p, i64, vp, vp]
         L.presk_hip_fill_normal.argtypes = [vp, ctypes.c_char_p, i64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]
+        L.presk_hip_mfma_probe.argtypes = [ctypes.c_char_p, i64, vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         L.presk_hip_pskd_decode.argtypes = [vp, ctypes.c_int, vp, i64, vp, ctypes.c_char_p, vp, vp]
         L.presk_hip_pskd_decode_idx.argtypes = [vp, ctypes.c_uint64, i64, vp, vp]
         L.presk_hip_dropout_mask.argtypes = [vp, ctypes.c_double, ctypes.c_char_p, i64, vp, vp]

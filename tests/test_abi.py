@@ -119,3 +119,14 @@ def test_short_kernelfn_tables_refused_on_the_host():
     ex.mode, ex._cache = hip.FAST, {}
     with pytest.raises(ValueError, match="1 input buffers for a kernel of 2 inputs"):
         ex.run(low.text, "f32", [Buf()], Buf())
+
+
+def test_mfma_probe_refuses_other_types():
+    """presk_hip_mfma_probe measures bf16 and f32 MFMA loops only; any other
+    type (or no iterations) is E10001 before a device is needed."""
+    import ctypes
+    from presk_amd import hip
+    ms, fl = ctypes.c_double(), ctypes.c_double()
+    for ty, it in ((b"f64", 10), (b"bf16", 0)):
+        rc = hip.lib().presk_hip_mfma_probe(ty, it, None, ctypes.byref(ms), ctypes.byref(fl))
+        assert rc != 0 and b"E10001" in hip.lib().presk_hip_last_error()
