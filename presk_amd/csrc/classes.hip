@@ -274,17 +274,23 @@ bool tile_override(TileOverride* t, std::string* err) {
     int bm = 0, bn = 0, splits = 0, used = 0;
     bool ok = std::sscanf(env, "%dx%d%n", &bm, &bn, &used) == 2;
     const char* rest = env + used;
+    bool eight = false;
+    if (ok && rest[0] == 'w' && rest[1] == '8') {
+        eight = true;
+        rest += 2;
+    }
     if (ok && *rest == '/') {
         ok = std::sscanf(rest, "/%d%n", &splits, &used) == 1 && splits >= 1 && splits <= 64;
         rest += ok ? used : 0;
     }
-    const bool shape = (bm == 128 && (bn == 64 || bn == 96 || bn == 128)) || (bm == 256 && (bn == 128 || bn == 256));
-    if (!ok || *rest != '\0' || !shape) {
+    const bool shape = (bm == 128 && (bn == 64 || bn == 96 || bn == 128)) || (bm == 256 && (bn == 96 || bn == 128 || bn == 256));
+    if (!ok || *rest != '\0' || !shape || (eight && !(bm == 128 && bn == 128))) {
         *err = std::string("PRESK_HIP_GEMM_TILE=") + env +
-               ": expected <bm>x<bn>[/<splits>] with bm 128 (bn 64, 96, 128) or 256 (bn 128, 256) and splits 1-64";
+               ": expected <bm>x<bn>[w8][/<splits>] with bm 128 (bn 64, 96, 128) or 256 (bn 96, 128, 256), w8 only "
+               "after 128x128, and splits 1-64";
         return false;
     }
-    *t = TileOverride{bm, bn, splits};
+    *t = TileOverride{bm, bn, splits, eight};
     return true;
 }
 
@@ -295,13 +301,15 @@ void apply_override(GemmArgs& g) {
     TileOverride t;
     std::string err;
     if (!tile_override(&t, &err) || t.bm == 0) return;
+    // 256-row tiles: 256 x 96 and 256 x 128 in f32, 256 x 128 and 256 x 256
+    // in 16-bit storage; another storage's shape leaves the plan as it is
+    if (t.bm == 256 && (g.storage == kF32 ? t.bn == 256 : t.bn == 96)) return;
     g.stream = false;     // the named tiles, not the streamed panels
-    if (t.bm == 128 || g.storage != kF32) {
-        g.bm = t.bm;
-        g.bn = t.bn;
-        g.tiles_m = (int)((g.M + g.bm - 1) / g.bm);
-        g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
-    }
+    g.bm = t.bm;
+    g.bn = t.bn;
+    g.eight = t.eight && g.storage == kF32;
+    g.tiles_m = (int)((g.M + g.bm - 1) / g.bm);
+    g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
     const int bk = gemm_block_k(g.storage);
     const long long nkb = (g.K + bk - 1) / bk;
     if (g.bm == 256) {
@@ -315,6 +323,7 @@ void apply_override(GemmArgs& g) {
 
 void plan_tiles(GemmArgs& g) {
     g.bm = 128;
+    g.eight = false;
     g.stream = true;
     g.tiles_m = (int)((g.M + gemm_tile_m() - 1) / gemm_tile_m());
     long long best = -1;
@@ -358,11 +367,45 @@ void plan_tiles(GemmArgs& g) {
     g.k_per_split = g.K;
     const long long tiles = (long long)g.tiles_m * g.tiles_n * g.batch;
     const int bk = gemm_block_k(g.storage);
+    // operands whose strides keep whole 16-byte vectors along the loaded
+    // axis (k when contiguous, else the rows), as the tiles loaded straight
+    // into LDS need (the pointers' alignment is checked at launch)
+    const int vec = g.storage == kF32 ? 4 : 8;
+    auto vec_strides = [&](long long other, const long long* bs) {
+        if (other % vec) return false;
+        for (int d = 0; d < g.nbatch; ++d)
+            if (bs[d] % vec) return false;
+        return true;
+    };
+    const bool a_rows_vec = g.a_kcontig || g.M % vec == 0, b_rows_vec = g.b_kcontig || g.N % vec == 0;
+    const bool all_vec = a_rows_vec && b_rows_vec && vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) &&
+                         vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b);
     // fewer tiles than compute units and a long K: split K across workgroups
     // (as many splits as fill one round of two workgroups per CU, each split
     // at least 4 k-blocks; split s takes k-blocks [s*nkb/S, (s+1)*nkb/S))
     if (g.batch == 1 && tiles < 256 && g.K >= 8 * bk) {
         const long long nkb = (g.K + bk - 1) / bk;
+        // f32 of whole k-blocks and whole vectors: 128 x 128 tiles of eight
+        // waves (two a SIMD, four k-blocks in flight, one workgroup a CU),
+        // as many splits as fill one round of the CUs -- the course step's
+        // weight gradients [384 x 1536] and [1536 x 384] over K 16384 179 ->
+        // 161 us (split 7 against the four-wave tiles' 14), [384 x 384] 60 ->
+        // 54 us (split 28 both); at fewer than two splits, the four-wave tiles
+        if (g.storage == kF32 && g.K % bk == 0 && all_vec) {
+            const long long t8 = (long long)g.tiles_m * ((g.N + 127) / 128);
+            long long s8 = 256 / t8;
+            if (s8 > nkb / 4) s8 = nkb / 4;
+            if (s8 > 64) s8 = 64;
+            if (s8 > 1) {
+                g.bn = 128;
+                g.tiles_n = (int)((g.N + 127) / 128);
+                g.eight = true;
+                g.splits = (int)s8;
+                g.k_per_split = (nkb + s8 - 1) / s8 * bk;
+                apply_override(g);
+                return;
+            }
+        }
         // f32 of whole k-blocks (its tiles load straight into LDS): the
         // widest tiles whenever each split still runs 16 k-blocks or more --
         // [1536 x 384] and [1152 x 384] over K 16384 measure 10-15 % faster
@@ -402,23 +445,44 @@ void plan_tiles(GemmArgs& g) {
     // or more -- the Llama projections and the MLP block's products 4-18 %
     // faster than on 128 x 128 tiles (e.g. 2048 x 4096 x 4096 80.6 -> 70.7
     // us), the course step's K of 384 not
-    auto vec_strides = [&](long long other, const long long* bs) {
-        if (other % 8) return false;
-        for (int d = 0; d < g.nbatch; ++d)
-            if (bs[d] % 8) return false;
-        return true;
-    };
-    const bool a_rows_vec = g.a_kcontig || g.M % 8 == 0, b_rows_vec = g.b_kcontig || g.N % 8 == 0;
+    //
+    // f32 likewise (no k-split, K of 384 or more, whole 32-deep k-blocks,
+    // the 128-row plan's columns 96 or 128): 256 x 96 or 256 x 128 tiles of
+    // eight waves, three k-blocks deep, whichever finishes first in rounds of
+    // 256 (one workgroup a CU), the wider on a tie, where they still fill the
+    // CUs once -- the course step's [16384 x 384] products 55 -> 51 us at K
+    // 384 and 188 -> 169 us at K 1536, [16384 x 1536] 197 -> 189 us; the 128
+    // tiles of [4096 x 1024] would leave half the CUs idle (86 -> 130 us)
+    if (g.storage == kF32) {
+        if (g.splits == 1 && g.K >= 384 && g.K % gemm_block_k(kF32) == 0 && (g.bn == 96 || g.bn == 128) && all_vec) {
+            long long best_cost = -1, best_t = 0;
+            int best_bn = 0;
+            for (int bn : {128, 96}) {
+                const long long t = (long long)((g.M + 255) / 256) * ((g.N + bn - 1) / bn) * g.batch;
+                const long long cost = (t + 255) / 256 * bn;
+                if (best_cost < 0 || cost < best_cost) {
+                    best_cost = cost;
+                    best_bn = bn;
+                    best_t = t;
+                }
+            }
+            if (best_t >= 256) {
+                g.bm = 256;
+                g.bn = best_bn;
+                g.tiles_m = (int)((g.M + 255) / 256);
+                g.tiles_n = (int)((g.N + best_bn - 1) / best_bn);
+            }
+        }
+        apply_override(g);
+        return;
+    }
     const long long t256 = (long long)((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
-    if (g.storage != kF32 && g.splits == 1 && g.K >= 3072 && g.K % gemm_block_k(g.storage) == 0 && a_rows_vec && b_rows_vec &&
-        vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) && vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b) && t256 >= 768) {
+    if (g.splits == 1 && g.K >= 3072 && g.K % gemm_block_k(g.storage) == 0 && all_vec && t256 >= 768) {
         g.bm = 256;
         g.bn = 256;
         g.tiles_m = (int)((g.M + 255) / 256);
         g.tiles_n = (int)((g.N + 255) / 256);
-    } else if (g.storage != kF32 && g.splits == 1 && g.K >= 768 && g.K % gemm_block_k(g.storage) == 0 && a_rows_vec &&
-               b_rows_vec && vec_strides(g.a_kcontig ? g.sa_m : g.sa_k, g.sa_b) &&
-               vec_strides(g.b_kcontig ? g.sb_n : g.sb_k, g.sb_b)) {
+    } else if (g.splits == 1 && g.K >= 768 && g.K % gemm_block_k(g.storage) == 0 && all_vec) {
         g.bm = 256;
         g.bn = 128;
         g.tiles_m = (int)((g.M + 255) / 256);

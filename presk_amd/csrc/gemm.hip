@@ -341,6 +341,68 @@ struct D16Loader {
     }
 };
 
+// f32 operand tiles (32 k) loaded straight into LDS for the eight-wave tiles,
+// in DLoader's swizzled layout (frag_dl reads them), by the same saddr-form
+// inline assembly as D16Loader: the kernel waits for its own loads, so two
+// k-blocks stay in flight while one is multiplied.  A tile of SLOTS chunks
+// that is not a whole number of the workgroup's rounds (96 rows: 1.5) has its
+// last round issued by the first SLOTS % NTH / 64 waves only, so those waves
+// count one load more a block (loads_of).  Byte offsets from the uniform base
+// are 32-bit: the launcher takes these tiles only for operands whose rows
+// span less than 4 GiB.
+template <bool KCONTIG, int ROWS, int NTH>
+struct F32Loader {
+    static constexpr int BK = 32;
+    static constexpr int CPR = KCONTIG ? 8 : ROWS / 4;    // chunks per LDS row
+    static constexpr int SLOTS = ROWS * BK / 4;           // chunks per tile
+    static constexpr int FULL = SLOTS / NTH;              // rounds every wave issues
+    static constexpr int PW = SLOTS % NTH / 64;           // waves issuing one round more
+    static constexpr int ROUNDS = FULL + (PW > 0 ? 1 : 0);
+    static constexpr int BYTES = SLOTS * 16;
+    static_assert(SLOTS % 64 == 0, "whole waves a round");
+    static_assert(KCONTIG || ROWS % 8 == 0, "the swizzle stays inside a k-row");
+    unsigned voff[ROUNDS];
+    const char* origin;
+    long long block_bytes;
+    unsigned lds0;
+    int wave;                   // this wave's index (uniform)
+
+    __device__ static constexpr int loads_of(bool extra) { return FULL + (extra ? 1 : 0); }
+    __device__ __forceinline__ void init(const float* p, int rows, long long rs, long long ks, int row0, int k0,
+                                         unsigned tile) {
+        const int t = threadIdx.x;
+        wave = __builtin_amdgcn_readfirstlane(t >> 6);
+        origin = (const char*)(p + (KCONTIG ? (long long)k0 : (long long)k0 * ks));
+        block_bytes = KCONTIG ? 4LL * BK : 4LL * BK * ks;
+#pragma unroll
+        for (int q = 0; q < ROUNDS; ++q) {
+            const int slot = q * NTH + t;
+            long long e;
+            if (KCONTIG) {
+                const int r = slot >> 3, kc = (slot & 7) ^ (r & 7);
+                int row = row0 + r;
+                row = row < rows ? row : rows - 1;
+                e = row * rs + kc * 4;
+            } else {
+                const int k = slot / CPR, cc = (slot % CPR) ^ ((k & 1) * 4);
+                int row = row0 + cc * 4;
+                row = row + 4 <= rows ? row : rows - 4;
+                e = k * ks + row;
+            }
+            voff[q] = (unsigned)(4 * e);
+        }
+        lds0 = __builtin_amdgcn_readfirstlane(tile + (unsigned)(t & ~63) * 16u);
+    }
+    __device__ __forceinline__ void issue(int kb, unsigned stage) const {
+        const char* const src = origin + kb * block_bytes;
+#pragma unroll
+        for (int q = 0; q < ROUNDS; ++q)
+            if (q < FULL || wave < PW)
+                asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                             : : "v"(voff[q]), "s"(src), "s"(lds0 + stage + (unsigned)(q * NTH * 16)) : "memory", "m0");
+    }
+};
+
 // wait until at most N of this thread's vector-memory operations are
 // outstanding (expcnt and lgkmcnt not waited on)
 template <int N>
@@ -499,7 +561,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     static_assert(!DL || !SAFE, "direct loads: whole vectors");
     static_assert(MF == 16 || ST != kF32, "32x32 tiles: 16-bit storage");
     constexpr bool D16 = DL && MF == 32;
-    static_assert(NW == 4 || D16, "eight waves: 16-bit tiles loaded straight into LDS");
+    // f32 eight-wave tiles (two waves a SIMD): operands straight into LDS,
+    // three stages deep like the 16-bit ones
+    constexpr bool F8 = DL && MF == 16 && NW == 8;
+    static_assert(NW == 4 || D16 || F8, "eight waves: tiles loaded straight into LDS");
     constexpr int NTH = 64 * NW, WAM = NW / WAN;
     // f32 storage: the MFMAs take the operands' roles exchanged (D = B^T A^T,
     // the same products over the same k-steps, so the same sums bit for
@@ -520,17 +585,19 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     constexpr int ASZ = DL ? DA::SIZE : LA::SIZE, BSZ = DL ? DB::SIZE : LB::SIZE;
     constexpr int LDA = AK ? LD : LA::LDR, LDB = BK_ ? LD : LB::LDR;
     constexpr int CLD = BN + 4;
-    typedef D16Loader<AK, BM, NTH> QA;
-    typedef D16Loader<BK_, BN, NTH> QB;
+    typedef typename std::conditional<F8, F32Loader<AK, BM, NTH>, D16Loader<AK, BM, NTH>>::type QA;
+    typedef typename std::conditional<F8, F32Loader<BK_, BN, NTH>, D16Loader<BK_, BN, NTH>>::type QB;
     constexpr int STAGE = QA::BYTES + QB::BYTES;
     // straight-into-LDS stages: three where they fit (256 x 128 tiles, 144 KB),
     // else two (256 x 256, 128 KB); two for 128-row tiles (64 or 48 KB), so
     // that two workgroups share a CU
-    constexpr int NS = BM == 128 ? 2 : 3 * STAGE <= 150 * 1024 ? 3 : 2;
+    // f32 eight-wave tiles: as many stages as fit, at most four (128 x 128: 4
+    // x 32 KB; 256 x 128 and 256 x 96: 3 x 48 and 3 x 44 KB)
+    constexpr int NS = F8 ? (4 * STAGE <= 150 * 1024 ? 4 : 3) : BM == 128 ? 2 : 3 * STAGE <= 150 * 1024 ? 3 : 2;
     // the epilogue stages the tile's f32 sums in LDS whole, or in two halves
     // of rows when the whole would not fit beside nothing else (256 x 256)
     constexpr int EH = BM * CLD * 4 <= 150 * 1024 ? 1 : 2, EROWS = BM / EH;
-    constexpr int OPER = D16 ? NS * STAGE : 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = EROWS * CLD * 4;
+    constexpr int OPER = D16 || F8 ? NS * STAGE : 2 * (ASZ + BSZ) * (int)sizeof(S), CTILE = EROWS * CLD * 4;
     static_assert(EH == 1 || (WM * MF) % EROWS == 0, "each wave's rows lie in one half");
     // (the exchanged-roles f32 tiles store their sums from the registers)
     __shared__ __attribute__((aligned(16))) char smem[SWAP || OPER > CTILE ? OPER : CTILE];
@@ -668,6 +735,76 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
             }
         };
         // whole rounds of the stages, then the last blocks
+        int kt = 0;
+        for (; kt + NS <= nd; kt += NS) stage_round(block, kt, std::make_integer_sequence<int, NS>{});
+        stage_tail(block, kt, nd, std::make_integer_sequence<int, NS - 1>{});
+    } else if constexpr (F8) {
+        // The 16-bit stages' order of loads, waits and barriers over 32-deep
+        // f32 blocks: blocks kt + 1 and kt + 2 stream into LDS while block kt
+        // is multiplied; each 4-k step's fragments are read while the
+        // previous step's MFMAs run.  A's tile is whole rounds of loads; a
+        // 96-row B tile's last round is issued by the first waves only, which
+        // then count one load more a block.
+        static_assert(QA::PW == 0, "A: whole rounds");
+        constexpr int NLL = QA::FULL + QB::FULL, NLH = NLL + (QB::PW > 0 ? 1 : 0);
+        constexpr int LA = NS - 1;
+        static_assert((LA - 1) * NLH < 64, "vmcnt holds the loads in flight");
+        const int nd = (kend - kbeg) / BK;
+        QA qa;
+        QB qb;
+        unsigned char* const st0 = (unsigned char*)smem;
+        const unsigned lds = (unsigned)(size_t)(lds_void_t*)st0;
+        qa.init((const float*)A, M, sa_m, sa_k, (int)m0, kbeg, lds);
+        qb.init((const float*)B, N, sb_n, sb_k, (int)n0, kbeg, lds + QA::BYTES);
+        auto fetch = [&](int kb, int s) {
+            qa.issue(kb, (unsigned)(s * STAGE));
+            qb.issue(kb, (unsigned)(s * STAGE));
+        };
+        auto wait_for = [&](int later) {
+            if (NLH != NLL && qb.wave < QB::PW) wait_blocks<NLH, LA - 1>(later);
+            else wait_blocks<NLL, LA - 1>(later);
+        };
+        float a[WM], b[WN];
+        auto read = [&](const unsigned char* st, int kk) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i) a[i] = frag_dl<AK, BM>((const float*)st, wm + i * 16, kk, lane);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) b[j] = frag_dl<BK_, BN>((const float*)(st + QA::BYTES), wn + j * 16, kk, lane);
+        };
+        if (nd > 0) {
+            const int pre = nd < LA ? nd : LA;
+            for (int kb = 0; kb < pre; ++kb) fetch(kb, kb);
+            wait_for(pre - 1);
+            __syncthreads();
+            read(st0, 0);
+        }
+        auto block = [&](int kt, auto stage) {
+            constexpr int S = decltype(stage)::value;
+            if (kt + LA < nd) fetch(kt + LA, (S + LA) % NS);
+            const unsigned char* const st = st0 + S * STAGE;
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += KSTEP) {
+                float ca[WM], cb[WN];
+#pragma unroll
+                for (int i = 0; i < WM; ++i) ca[i] = a[i];
+#pragma unroll
+                for (int j = 0; j < WN; ++j) cb[j] = b[j];
+                if (kk + KSTEP < BK) {
+                    read(st, kk + KSTEP);
+                } else if (kt + 1 < nd) {
+                    const int last = kt + LA < nd - 1 ? kt + LA : nd - 1;
+                    wait_for(last - (kt + 1));
+                    __syncthreads();
+                    read(st0 + ((S + 1) % NS) * STAGE, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j) acc[i][j] = mfma<ST>(cb[j], ca[i], acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
         int kt = 0;
         for (; kt + NS <= nd; kt += NS) stage_round(block, kt, std::make_integer_sequence<int, NS>{});
         stage_tail(block, kt, nd, std::make_integer_sequence<int, NS - 1>{});
@@ -1169,6 +1306,27 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     const bool fast = g.a_vec && g.b_vec;
     hipError_t e;
     if (stream_fits(g)) return stream_launch<ST>(g, stream);
+    if (ST == kF32 && (g.bm == 256 || g.eight)) {
+        // 256 x 128 or 256 x 96 tiles of eight waves (4 x 2 waves of 64 x 64
+        // or 64 x 48), three stages straight into LDS, or 128 x 128 ones (4 x
+        // 2 waves of 32 x 64) four stages deep; operands that do not allow it
+        // (alignment is known only here) take the four-wave 128-row tiles of
+        // the same columns and split -- the same MFMAs over the same k-steps
+        if (gemm_f32_wide_fits(g)) {
+            if (g.bm == 256 && g.bn == 96) e = launch_shape<ST, 4, 3, false, true, 16, 8, 2>(g, stream);
+            else if (g.bm == 256 && g.bn == 128) e = launch_shape<ST, 4, 4, false, true, 16, 8, 2>(g, stream);
+            else if (g.bm == 128 && g.bn == 128) e = launch_shape<ST, 2, 4, false, true, 16, 8, 2>(g, stream);
+            else return hipErrorInvalidValue;
+            if (e != hipSuccess || g.splits <= 1) return e;
+            split_reduce_kernel<ST><<<(unsigned)((g.M * g.N + 255) / 256), 256, 0, stream>>>(g);
+            return hipGetLastError();
+        }
+        GemmArgs h = g;
+        h.bm = 128;
+        h.eight = false;
+        h.tiles_m = (int)((g.M + 127) / 128);
+        return launch_typed<ST>(h, stream);
+    }
     if (ST == kF32 && fast && g.K % St<kF32>::BK == 0) {
         // whole k-blocks of whole vectors: the f32 tiles load straight into LDS
         if (g.bn == 96) e = launch_shape<ST, 4, 3, false, ST == kF32>(g, stream);
@@ -1330,6 +1488,16 @@ hipError_t gemm_e8_narrow(const GemmArgs& g, void* out, const void* bias, hipStr
 
 int gemm_block_k(int storage) { return storage == kF32 ? St<kF32>::BK : St<kBF16>::BK; }
 int gemm_tile_m() { return 128; }
+bool gemm_f32_wide_fits(const GemmArgs& g) {
+    if (g.storage != kF32 || !g.a_vec || !g.b_vec || g.K % St<kF32>::BK) return false;
+    // the loads' 32-bit byte offsets from a k-block's base: rows x row stride
+    // (k-contiguous), else 32 k-rows x k stride plus the rows
+    auto span = [](bool kc, long long rows, long long rs, long long ks) {
+        return kc ? (double)rows * (double)rs + 32.0 : 32.0 * (double)ks + (double)rows;
+    };
+    return 4.0 * span(g.a_kcontig, g.M, g.sa_m, g.sa_k) < 4294967296.0 &&
+           4.0 * span(g.b_kcontig, g.N, g.sb_n, g.sb_k) < 4294967296.0;
+}
 int gemm_tile_m_of(const GemmArgs& g) { return g.bm == 256 ? 256 : 128; }
 
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream) {

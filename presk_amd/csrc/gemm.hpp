@@ -28,8 +28,9 @@ struct GemmArgs {
     int splits;
     long long k_per_split;
     int tiles_m, tiles_n;
-    int bm;                         // tile rows: 128, or 256 (16-bit storage, 32x32 MFMA tiles)
-    int bn;                         // tile columns: 128, 96 or 64
+    int bm;                         // tile rows: 128, or 256 (eight-wave tiles)
+    int bn;                         // tile columns: 256, 128, 96 or 64
+    bool eight;                     // f32 128 x 128 tiles of eight waves (256-row tiles always have eight)
     bool stream;                    // K of at most two k-blocks may stream B's tiles across a kept A panel
 };
 
@@ -65,5 +66,9 @@ hipError_t gemm_narrow16(const GemmArgs& g, int st, void* out, const void* bias,
 int gemm_block_k(int storage);
 int gemm_tile_m();
 int gemm_tile_m_of(const GemmArgs& g);
+// f32 operands the eight-wave tiles can take: whole aligned vectors, whole
+// 32-deep k-blocks (a k-split's ranges are whole blocks), 32-bit byte
+// offsets within a k-block
+bool gemm_f32_wide_fits(const GemmArgs& g);
 
 }  // namespace presk

@@ -38,7 +38,10 @@ def test_tile_override(monkeypatch):
     assert compiled(bf).order == "mfma-k32"          # 128 x 96 tiles of 16x16x32 MFMAs
     monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "256x256")
     assert compiled(bf).order == "mfma-k16"
-    assert compiled(f32).order.startswith("mfma-f32-k4")  # no 256-row f32 tiles: the planner's
+    assert compiled(f32).order.startswith("mfma-f32-k4")  # no 256 x 256 f32 tiles: the planner's
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "256x96")
+    assert compiled(f32).order == "mfma-f32-k4"      # f32 256-row tiles: never split
+    assert compiled(bf).order == "mfma-k16"          # no 256 x 96 16-bit tiles: the planner's
     monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x64/4")
     assert compiled(f32).order == "mfma-f32-k4-split4"
     assert compiled(bf).order == "mfma-k16-split4"

@@ -249,3 +249,86 @@ def test_eight_wave_tiles_equal_the_128_row_tiles(layout, dt, tiles, monkeypatch
         outs.append(out.download(np.uint16))
     differ = np.count_nonzero(outs[0] != outs[1])
     assert differ == 0, f"{differ} of {outs[0].size} outputs differ from the 128 x 128 tiles'"
+
+
+# The f32 eight-wave tiles (256 x 128 and 256 x 96, three 32-deep k-blocks
+# straight into LDS, a 96-row B tile's last round of loads issued by half the
+# waves) run the 16x16x4 MFMAs over the same k-steps as the four-wave 128-row
+# tiles, so the two agree bit for bit -- in every operand layout, with rows
+# and columns past the last tile, every remainder of the stage rounds, and
+# with the bias.  Operands that the wide tiles cannot take (a row off 16
+# bytes) run the 128-row tiles of the same columns, the same bits again.
+@pytest.mark.parametrize("layout,tiles", [(lay, t) for lay in EIGHT for t in ("256x128", "256x96")])
+def test_f32_eight_wave_tiles_equal_the_128_row_tiles(layout, tiles, monkeypatch):
+    from oracle import kernel_text as kt
+    low = EIGHT[layout]("f32")
+    print(f"[gemm] f32 eight waves {layout} {tiles}", flush=True)
+    k = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(11)
+    ins = [hip.DeviceBuffer.of(rng.standard_normal(b.dims, dtype=np.float32)) for b in k.inputs]
+    outs = []
+    for t in (tiles, "128x128/1"):
+        monkeypatch.setenv("PRESK_HIP_GEMM_TILE", t)
+        c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+        assert c.kind == "gemm" and c.order == "mfma-f32-k4", (c.kind, c.order)
+        out = hip.DeviceBuffer(k.output.numel * 4)
+        out.upload(np.full(k.output.numel * 4, 0xFF, np.uint8))
+        c.run([b.ptr for b in ins] + [out.ptr])
+        hip.sync()
+        outs.append(out.download(np.uint32))
+    assert not np.any(outs[1] == 0xFFFFFFFF), "unwritten outputs"
+    differ = np.count_nonzero(outs[0] != outs[1])
+    assert differ == 0, f"{differ} of {outs[0].size} outputs differ from the 128 x 128 tiles'"
+
+
+def test_f32_eight_wave_tiles_on_a_misaligned_operand(monkeypatch):
+    # the A operand one element past a 16-byte boundary: the 256-row plan
+    # falls back to 128-row tiles at launch, and the bits stay those of the
+    # aligned run
+    from oracle import kernel_text as kt
+    low = EIGHT["nn"]("f32")
+    k = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal(k.inputs[0].numel, dtype=np.float32)
+    b = rng.standard_normal(k.inputs[1].numel, dtype=np.float32)
+    big = hip.DeviceBuffer(4 * (a.size + 4))
+    big.upload(np.concatenate([np.zeros(1, np.float32), a, np.zeros(3, np.float32)]))
+    a_al, b_d = hip.DeviceBuffer.of(a), hip.DeviceBuffer.of(b)
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "256x96")
+    c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+    outs = []
+    for ptr in (a_al.ptr, big.ptr + 4):
+        out = hip.DeviceBuffer(k.output.numel * 4)
+        out.upload(np.full(k.output.numel * 4, 0xFF, np.uint8))
+        c.run([ptr, b_d.ptr, out.ptr])
+        hip.sync()
+        outs.append(out.download(np.uint32))
+    assert not np.any(outs[1] == 0xFFFFFFFF), "unwritten outputs"
+    assert np.array_equal(outs[0], outs[1])
+
+
+# The f32 128 x 128 tiles of eight waves (four 32-deep k-blocks in flight,
+# for split-K weight gradients), against the four-wave tiles at the same
+# split: the same partial sums, added in the same order, so the same bits.
+@pytest.mark.parametrize("layout,splits", [("tn", 1), ("tn", 5), ("nn", 3), ("nt", 1), ("tt", 4), ("bias", 2)])
+def test_f32_eight_wave_128_tiles_equal_the_four_wave_tiles(layout, splits, monkeypatch):
+    from oracle import kernel_text as kt
+    low = EIGHT[layout]("f32")
+    print(f"[gemm] f32 eight waves 128x128 {layout} split {splits}", flush=True)
+    k = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(13)
+    ins = [hip.DeviceBuffer.of(rng.standard_normal(b.dims, dtype=np.float32)) for b in k.inputs]
+    outs = []
+    for t in (f"128x128w8/{splits}", f"128x128/{splits}"):
+        monkeypatch.setenv("PRESK_HIP_GEMM_TILE", t)
+        c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
+        want = "mfma-f32-k4" + (f"-split{splits}" if splits > 1 else "")
+        assert c.kind == "gemm" and c.order == want, (c.kind, c.order)
+        out = hip.DeviceBuffer(k.output.numel * 4)
+        out.upload(np.full(k.output.numel * 4, 0xFF, np.uint8))
+        c.run([b.ptr for b in ins] + [out.ptr])
+        hip.sync()
+        outs.append(out.download(np.uint32))
+    assert not np.any(outs[1] == 0xFFFFFFFF), "unwritten outputs"
+    differ = np.count_nonzero(outs[0] != outs[1])
+    assert differ == 0, f"{differ} of {outs[0].size} outputs differ from the four-wave tiles'"

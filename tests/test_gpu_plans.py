@@ -38,9 +38,9 @@ PLANS = [
     ("attn-proj-384x384", lambda dt: vjp_r(384, 384, dt), "bf16", 28),
     ("head-384x65", lambda dt: vjp_r(384, 65, dt), "f32", 64),
     ("head-384x65", lambda dt: vjp_r(384, 65, dt), "bf16", 64),
-    ("mlp-up-384x1536", lambda dt: vjp_r(384, 1536, dt), "f32", 14),
+    ("mlp-up-384x1536", lambda dt: vjp_r(384, 1536, dt), "f32", 7),
     ("mlp-up-384x1536", lambda dt: vjp_r(384, 1536, dt), "bf16", 7),
-    ("mlp-down-1536x384", lambda dt: vjp_r(1536, 384, dt), "f32", 14),
+    ("mlp-down-1536x384", lambda dt: vjp_r(1536, 384, dt), "f32", 7),
     ("mlp-down-1536x384", lambda dt: vjp_r(1536, 384, dt), "bf16", 7),
 ]
 
