@@ -563,7 +563,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     constexpr bool D16 = DL && MF == 32;
     // f32 eight-wave tiles (two waves a SIMD): operands straight into LDS,
     // three stages deep like the 16-bit ones
-    constexpr bool F8 = DL && MF == 16 && NW == 8;
+    constexpr bool F8 = ST == kF32 && DL && MF == 16 && NW == 8;
     static_assert(NW == 4 || D16 || F8, "eight waves: tiles loaded straight into LDS");
     constexpr int NTH = 64 * NW, WAM = NW / WAN;
     // f32 storage: the MFMAs take the operands' roles exchanged (D = B^T A^T,
@@ -1306,7 +1306,8 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     const bool fast = g.a_vec && g.b_vec;
     hipError_t e;
     if (stream_fits(g)) return stream_launch<ST>(g, stream);
-    if (ST == kF32 && (g.bm == 256 || g.eight)) {
+    if constexpr (ST == kF32) {
+    if (g.bm == 256 || g.eight) {
         // 256 x 128 or 256 x 96 tiles of eight waves (4 x 2 waves of 64 x 64
         // or 64 x 48), three stages straight into LDS, or 128 x 128 ones (4 x
         // 2 waves of 32 x 64) four stages deep; operands that do not allow it
@@ -1326,6 +1327,7 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
         h.eight = false;
         h.tiles_m = (int)((g.M + 127) / 128);
         return launch_typed<ST>(h, stream);
+    }
     }
     if (ST == kF32 && fast && g.K % St<kF32>::BK == 0) {
         // whole k-blocks of whole vectors: the f32 tiles load straight into LDS
