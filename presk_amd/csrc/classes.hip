@@ -446,31 +446,35 @@ void plan_tiles(GemmArgs& g) {
     // faster than on 128 x 128 tiles (e.g. 2048 x 4096 x 4096 80.6 -> 70.7
     // us), the course step's K of 384 not
     //
-    // f32 likewise (no k-split, K of 384 or more, whole 32-deep k-blocks,
-    // the 128-row plan's columns 96 or 128): 256 x 96 or 256 x 128 tiles of
-    // eight waves, three k-blocks deep, whichever finishes first in rounds of
-    // 256 (one workgroup a CU), the wider on a tie, where they still fill the
-    // CUs once -- the course step's [16384 x 384] products 55 -> 51 us at K
-    // 384 and 188 -> 169 us at K 1536, [16384 x 1536] 197 -> 189 us; the 128
-    // tiles of [4096 x 1024] would leave half the CUs idle (86 -> 130 us)
+    // f32 likewise (no k-split, K of 384 or more, whole 32-deep k-blocks, N
+    // of 128 or more): 256 x 128, 256 x 96 (three k-blocks deep) or 128 x 128
+    // (four deep) tiles of eight waves, one workgroup a CU, whichever does
+    // the least work a CU over its rounds of 256 (the larger tile on a tie),
+    // where they still fill the CUs once -- the course step's [16384 x 384]
+    // products 55 -> 51 us at K 384 (256 x 96) and 188 -> 169 us at K 1536,
+    // [16384 x 1536] 197 -> 189 us (256 x 128), the Linear module's [4096 x
+    // 1024] 88 -> 74 us (128 x 128), each the fastest of the three measured
     if (g.storage == kF32) {
-        if (g.splits == 1 && g.K >= 384 && g.K % gemm_block_k(kF32) == 0 && (g.bn == 96 || g.bn == 128) && all_vec) {
+        if (g.splits == 1 && g.K >= 384 && g.K % gemm_block_k(kF32) == 0 && g.N >= 128 && all_vec) {
+            static const int shapes[3][2] = {{256, 128}, {256, 96}, {128, 128}};
             long long best_cost = -1, best_t = 0;
-            int best_bn = 0;
-            for (int bn : {128, 96}) {
-                const long long t = (long long)((g.M + 255) / 256) * ((g.N + bn - 1) / bn) * g.batch;
-                const long long cost = (t + 255) / 256 * bn;
+            int bi = 0;
+            for (int i = 0; i < 3; ++i) {
+                const int bm = shapes[i][0], bn = shapes[i][1];
+                const long long t = (long long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch;
+                const long long cost = (t + 255) / 256 * bm * bn;
                 if (best_cost < 0 || cost < best_cost) {
                     best_cost = cost;
-                    best_bn = bn;
                     best_t = t;
+                    bi = i;
                 }
             }
             if (best_t >= 256) {
-                g.bm = 256;
-                g.bn = best_bn;
-                g.tiles_m = (int)((g.M + 255) / 256);
-                g.tiles_n = (int)((g.N + best_bn - 1) / best_bn);
+                g.bm = shapes[bi][0];
+                g.bn = shapes[bi][1];
+                g.eight = g.bm == 128;
+                g.tiles_m = (int)((g.M + g.bm - 1) / g.bm);
+                g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
             }
         }
         apply_override(g);
