@@ -605,15 +605,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     S* const Bs0 = As0 + 2 * ASZ;
 
     // Work order.  The grid is one line of (split, batch, tile) items.  The
-    // hardware deals workgroups to the 8 XCDs round robin (id mod 8).  Without
-    // a k-split each XCD is given one contiguous run of items, so the tiles of
-    // one batch entry and neighbouring row-tiles share its L2.  With a k-split
-    // the panels of one k-range outgrow an L2 anyway, and spreading each
-    // range over all XCDs measures faster: items go in plain order.  Within a
-    // run, tiles go GROUP row-tiles at a time across the columns, so that
-    // concurrent tiles share A rows: 8 for 128-row tiles (64 a XCD at once,
-    // 8 x 8), 4 for 256-row ones (32 at once: 4 x 8, a block of the output
-    // as tall as it is wide for 256 x 128 tiles).
+    // hardware deals workgroups to the 8 XCDs round robin (id mod 8).  Each
+    // XCD is given one contiguous run of items, so the tiles of one batch
+    // entry and neighbouring row-tiles share its L2 -- but for the four-wave
+    // tiles with a k-split, whose k-ranges' panels outgrow an L2, spreading
+    // each range over all XCDs measures faster: their items go in plain
+    // order.  (The eight-wave f32 split tiles, one workgroup a CU and each
+    // XCD's tiles streaming one k-range together, keep the runs: 1-3 %
+    // faster.)  Within a run, tiles go GROUP row-tiles at a time across the
+    // columns, so that concurrent tiles share A rows: 8 for 128-row tiles (64
+    // a XCD at once, 8 x 8), 4 for 256-row ones (32 at once: 4 x 8, a block
+    // of the output as tall as it is wide for 256 x 128 tiles).
     // The arithmetic is 32-bit: the launcher keeps the items below 2^31 and
     // the plan the batch below 2^16 (64-bit divisions cost hundreds of scalar
     // instructions a wave, before the first load is issued).
@@ -622,7 +624,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     const unsigned nb = (unsigned)g.batch;
     const unsigned xcd = blockIdx.x % 8, local = blockIdx.x / 8;
     const unsigned q8 = total / 8, r8 = total % 8;
-    const unsigned item = g.splits > 1 ? blockIdx.x : xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    const unsigned item = g.splits > 1 && !F8 ? blockIdx.x : xcd * q8 + (xcd < r8 ? xcd : r8) + local;
     const unsigned tb = item / tiles;
     const int split = (int)(tb / nb);
     const unsigned batch = tb - (unsigned)split * nb;
