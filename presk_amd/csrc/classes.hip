@@ -307,7 +307,7 @@ void apply_override(GemmArgs& g) {
     g.stream = false;     // the named tiles, not the streamed panels
     g.bm = t.bm;
     g.bn = t.bn;
-    g.eight = t.eight && g.storage == kF32;
+    g.eight = t.eight;
     g.tiles_m = (int)((g.M + g.bm - 1) / g.bm);
     g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
     const int bk = gemm_block_k(g.storage);
@@ -385,16 +385,21 @@ void plan_tiles(GemmArgs& g) {
     // at least 4 k-blocks; split s takes k-blocks [s*nkb/S, (s+1)*nkb/S))
     if (g.batch == 1 && tiles < 256 && g.K >= 8 * bk) {
         const long long nkb = (g.K + bk - 1) / bk;
-        // f32 of whole k-blocks and whole vectors: 128 x 128 tiles of eight
-        // waves (two a SIMD, four k-blocks in flight, one workgroup a CU),
-        // as many splits as fill one round of the CUs -- the course step's
+        // Whole k-blocks and whole vectors: 128 x 128 tiles of eight waves
+        // (two a SIMD, four k-blocks in flight, one workgroup a CU), as many
+        // splits as fill one round of the CUs -- in f32 the course step's
         // weight gradients [384 x 1536] and [1536 x 384] over K 16384 179 ->
         // 161 us (split 7 against the four-wave tiles' 14), [384 x 384] 60 ->
-        // 54 us (split 28 both); at fewer than two splits, the four-wave tiles
-        if (g.storage == kF32 && g.K % bk == 0 && all_vec) {
+        // 54 us (split 28 both); in 16-bit storage with each split at least
+        // 18 k-blocks long (fewer, longer splits: the partials' round trip
+        // halves), [384 x 384] 27.0 -> 23.3 us (split 14 against the
+        // four-wave 128 x 64 tiles' 28), [1536 x 384] 47.3 -> 46.0 us (split
+        // 7 both).  At fewer than two splits, the four-wave tiles below.
+        if (g.K % bk == 0 && all_vec) {
             const long long t8 = (long long)g.tiles_m * ((g.N + 127) / 128);
             long long s8 = 256 / t8;
-            if (s8 > nkb / 4) s8 = nkb / 4;
+            const long long min_blocks = g.storage == kF32 ? 4 : 18;
+            if (s8 > nkb / min_blocks) s8 = nkb / min_blocks;
             if (s8 > 64) s8 = 64;
             if (s8 > 1) {
                 g.bn = 128;

@@ -593,7 +593,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     // that two workgroups share a CU
     // f32 eight-wave tiles: as many stages as fit, at most four (128 x 128: 4
     // x 32 KB; 256 x 128 and 256 x 96: 3 x 48 and 3 x 44 KB)
-    constexpr int NS = F8 ? (4 * STAGE <= 150 * 1024 ? 4 : 3) : BM == 128 ? 2 : 3 * STAGE <= 150 * 1024 ? 3 : 2;
+    // 16-bit: two stages for four-wave 128-row tiles (two workgroups a CU),
+    // four for eight-wave ones (one a CU), else three where they fit
+    constexpr int NS = F8 ? (4 * STAGE <= 150 * 1024 ? 4 : 3)
+                          : BM == 128 ? (NW == 8 ? 4 : 2) : 3 * STAGE <= 150 * 1024 ? 3 : 2;
     // the epilogue stages the tile's f32 sums in LDS whole, or in two halves
     // of rows when the whole would not fit beside nothing else (256 x 256)
     constexpr int EH = BM * CLD * 4 <= 150 * 1024 ? 1 : 2, EROWS = BM / EH;
@@ -1371,7 +1374,9 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
         // the MLP block's and the Llama attention scores' shapes).
         if constexpr (ST != kF32) {
             const bool whole = fast && g.K % St<ST>::BK == 0 && (g.splits <= 1 || g.k_per_split % St<ST>::BK == 0);
-            if (g.bn == 128)
+            if (g.bn == 128 && g.eight && whole)
+                e = launch_shape<ST, 1, 2, false, true, 32, 8, 2>(g, stream);
+            else if (g.bn == 128)
                 e = whole ? launch_shape<ST, 2, 2, false, true, 32>(g, stream) : launch_shape<ST, 2, 2, true, false, 32>(g, stream);
             else
                 e = whole ? launch_shape<ST, 2, 1, false, true, 32>(g, stream) : launch_shape<ST, 2, 1, true, false, 32>(g, stream);

@@ -307,28 +307,35 @@ def test_f32_eight_wave_tiles_on_a_misaligned_operand(monkeypatch):
     assert np.array_equal(outs[0], outs[1])
 
 
-# The f32 128 x 128 tiles of eight waves (four 32-deep k-blocks in flight,
-# for split-K weight gradients), against the four-wave tiles at the same
+# The 128 x 128 tiles of eight waves (four k-blocks in flight, for split-K
+# weight gradients), f32 and 16-bit, against the four-wave tiles at the same
 # split: the same partial sums, added in the same order, so the same bits.
-@pytest.mark.parametrize("layout,splits", [("tn", 1), ("tn", 5), ("nn", 3), ("nt", 1), ("tt", 4), ("bias", 2)])
-def test_f32_eight_wave_128_tiles_equal_the_four_wave_tiles(layout, splits, monkeypatch):
+@pytest.mark.parametrize("layout,splits,dt", [("tn", 1, "f32"), ("tn", 5, "f32"), ("nn", 3, "f32"), ("nt", 1, "f32"),
+                                              ("tt", 4, "f32"), ("bias", 2, "f32"), ("tn", 1, "bf16"),
+                                              ("tn", 3, "bf16"), ("nn", 2, "bf16"), ("nt", 1, "f16"),
+                                              ("tt", 2, "bf16"), ("bias", 2, "f16")])
+def test_eight_wave_128_tiles_equal_the_four_wave_tiles(layout, splits, dt, monkeypatch):
     from oracle import kernel_text as kt
-    low = EIGHT[layout]("f32")
-    print(f"[gemm] f32 eight waves 128x128 {layout} split {splits}", flush=True)
+    low = EIGHT[layout](dt)
+    print(f"[gemm] eight waves 128x128 {layout} {dt} split {splits}", flush=True)
     k = kt.parse_kernel(low.text)
     rng = np.random.default_rng(13)
-    ins = [hip.DeviceBuffer.of(rng.standard_normal(b.dims, dtype=np.float32)) for b in k.inputs]
+    vals = [rng.standard_normal(b.dims, dtype=np.float32) for b in k.inputs]
+    ins = [hip.DeviceBuffer.of(v if dt == "f32" else fmt.encode(fmt.roundtrip(v, dt), dt)) for v in vals]
+    esz, code = (4, np.uint32) if dt == "f32" else (2, np.uint16)
     outs = []
     for t in (f"128x128w8/{splits}", f"128x128/{splits}"):
         monkeypatch.setenv("PRESK_HIP_GEMM_TILE", t)
-        c = hip.Compiled(low.text, "f32", low.lanes, hip.FAST)
-        want = "mfma-f32-k4" + (f"-split{splits}" if splits > 1 else "")
+        c = hip.Compiled(low.text, dt, low.lanes, hip.FAST)
+        want = ("mfma-f32-k4" if dt == "f32" else "mfma-k16") + (f"-split{splits}" if splits > 1 else "")
         assert c.kind == "gemm" and c.order == want, (c.kind, c.order)
-        out = hip.DeviceBuffer(k.output.numel * 4)
-        out.upload(np.full(k.output.numel * 4, 0xFF, np.uint8))
-        c.run([b.ptr for b in ins] + [out.ptr])
+        out = hip.DeviceBuffer(k.output.numel * esz)
+        out.upload(np.full(k.output.numel * esz, 0xFF, np.uint8))
+        flag = hip.DeviceBuffer(4)
+        flag.zero()
+        c.run([b.ptr for b in ins] + [out.ptr] + ([flag.ptr] if c.guarded else []))
         hip.sync()
-        outs.append(out.download(np.uint32))
-    assert not np.any(outs[1] == 0xFFFFFFFF), "unwritten outputs"
+        outs.append(out.download(code))
+    assert not np.any(outs[1] == code(-1 & (0xFFFFFFFF if dt == "f32" else 0xFFFF))), "unwritten outputs"
     differ = np.count_nonzero(outs[0] != outs[1])
     assert differ == 0, f"{differ} of {outs[0].size} outputs differ from the four-wave tiles'"

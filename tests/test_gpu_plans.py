@@ -35,7 +35,7 @@ def vjp_r(n_x, n_ct, dt):
 # (name, lowering, storage type, the split the plan must take)
 PLANS = [
     ("attn-proj-384x384", lambda dt: vjp_r(384, 384, dt), "f32", 28),
-    ("attn-proj-384x384", lambda dt: vjp_r(384, 384, dt), "bf16", 28),
+    ("attn-proj-384x384", lambda dt: vjp_r(384, 384, dt), "bf16", 14),
     ("head-384x65", lambda dt: vjp_r(384, 65, dt), "f32", 64),
     ("head-384x65", lambda dt: vjp_r(384, 65, dt), "bf16", 64),
     ("mlp-up-384x1536", lambda dt: vjp_r(384, 1536, dt), "f32", 7),
