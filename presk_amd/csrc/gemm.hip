@@ -613,12 +613,13 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     // entry and neighbouring row-tiles share its L2 -- but for the four-wave
     // tiles with a k-split, whose k-ranges' panels outgrow an L2, spreading
     // each range over all XCDs measures faster: their items go in plain
-    // order.  (The eight-wave f32 split tiles, one workgroup a CU and each
-    // XCD's tiles streaming one k-range together, keep the runs: 1-3 %
-    // faster.)  Within a run, tiles go GROUP row-tiles at a time across the
-    // columns, so that concurrent tiles share A rows: 8 for 128-row tiles (64
-    // a XCD at once, 8 x 8), 4 for 256-row ones (32 at once: 4 x 8, a block
-    // of the output as tall as it is wide for 256 x 128 tiles).
+    // order.  (The eight-wave split tiles, one workgroup a CU and each XCD's
+    // tiles streaming one k-range together, keep the runs: 1-3 % faster in
+    // f32, up to 20 % in bf16.)  Within a run, tiles go GROUP row-tiles at a
+    // time across the columns, so that concurrent tiles share A rows: 8 for
+    // 128-row tiles (64 a XCD at once, 8 x 8), 4 for 256-row ones (32 at
+    // once: 4 x 8, a block of the output as tall as it is wide for 256 x 128
+    // tiles).
     // The arithmetic is 32-bit: the launcher keeps the items below 2^31 and
     // the plan the batch below 2^16 (64-bit divisions cost hundreds of scalar
     // instructions a wave, before the first load is issued).
@@ -627,7 +628,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     const unsigned nb = (unsigned)g.batch;
     const unsigned xcd = blockIdx.x % 8, local = blockIdx.x / 8;
     const unsigned q8 = total / 8, r8 = total % 8;
-    const unsigned item = g.splits > 1 && !F8 ? blockIdx.x : xcd * q8 + (xcd < r8 ? xcd : r8) + local;
+    const unsigned item = g.splits > 1 && NW == 4 ? blockIdx.x : xcd * q8 + (xcd < r8 ? xcd : r8) + local;
     const unsigned tb = item / tiles;
     const int split = (int)(tb / nb);
     const unsigned batch = tb - (unsigned)split * nb;
