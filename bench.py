@@ -678,7 +678,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
-              "multi-GPU sharding is a design (DESIGN.md), not a run.", file=sys.stderr)
+              "the executor runs on one device, and sharding across GPUs is not built.", file=sys.stderr)
         sys.exit(2)
     dtype = args.dtype or ("bf16" if args.workload in ("mlp", "llama") else "f32")
     if args.traffic_table:
