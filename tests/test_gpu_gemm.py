@@ -221,6 +221,9 @@ EIGHT = {
                            ["m", "n"], dt),
     "bias": lambda dt: L.dot([O(A(("batch", 1288), 768)), O(A(768, 520)), O(A(520))], dt,
                              epilogue=(True, A(("batch", 1288), 520))),
+    # a batched ein: each batch entry's tiles at its own offsets
+    "batched": lambda dt: L.ein([O(A(("b", 3), ("m", 520), ("k", 384))), O(A(("b", 3), ("k", 384), ("n", 264)))],
+                                [["b", "m", "k"], ["b", "k", "n"]], ["b", "m", "n"], dt),
 }
 
 

@@ -67,6 +67,16 @@ def cases():
     out.append(("dot+add-e8m15", L.dot([x, w, O(A(136))], "e8m15", epilogue=(True, d.out_axes)), hip.FAST, "gemm"))
     out.append(("dot_vjp_r-split-e8m15", L.dot_vjp_r([O(A(("batch", 4), ("seq", 600), 96)),
                                                        O(A(("batch", 4), ("seq", 600), 80))], "e8m15"), hip.FAST, "gemm"))
+    # f32 products the planner puts on eight-wave tiles: the course step's
+    # [16384 x 384] with a bias (256 x 96), the Linear module's [4096 x 1024]
+    # (128 x 128), a batched ein over 16 entries (256 x 96)
+    xc = O(A(("batch", 64), ("seq", 256), ("model", 384)))
+    dc = L.dot([xc, O(A(384, 384))], "f32")
+    out.append(("dot+add-f32-256x96", L.dot([xc, O(A(384, 384)), O(A(384))], "f32", epilogue=(True, dc.out_axes)),
+                hip.FAST, "gemm"))
+    out.append(("dot-f32-128x128-eight", L.dot([O(A(("batch", 4096), 1024)), O(A(1024, 1024))], "f32"), hip.FAST, "gemm"))
+    out.append(("ein-batched-f32-256x96", L.ein([O(A(("b", 16), ("m", 1024), ("k", 384))), O(A(("b", 16), ("k", 384), ("n", 384)))],
+                                                [["b", "m", "k"], ["b", "k", "n"]], ["b", "m", "n"], "f32"), hip.FAST, "gemm"))
     return out
 
 
