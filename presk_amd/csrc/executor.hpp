@@ -60,7 +60,7 @@ std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode);
 // malformed; an unset or empty variable is no override (bm 0).
 struct TileOverride {
     int bm = 0, bn = 0, splits = 0;
-    bool eight = false;     // f32 128 x 128 tiles of eight waves
+    bool eight = false;     // 128 x 128 tiles of eight waves
 };
 bool tile_override(TileOverride* t, std::string* err);
 

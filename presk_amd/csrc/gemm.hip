@@ -23,13 +23,20 @@
 // operands loaded straight into LDS three (two) k-blocks deep (D16Loader),
 // the fragments of each 16-k step read while the previous step's MFMAs run;
 // 128 x 128 and 128 x 64 tiles the same way with four waves in two stages,
-// two or three workgroups a CU.  Operands off 16 bytes or partial k-blocks
-// take four-wave tiles and the same MFMAs from register-staged operands;
-// 128 x 96 tiles take the 16x16 MFMAs below.
+// two or three workgroups a CU, and 128 x 128 tiles of eight waves four
+// stages deep for split weight gradients.  Operands off 16 bytes or partial
+// k-blocks take four-wave tiles and the same MFMAs from register-staged
+// operands; 128 x 96 tiles take the 16x16 MFMAs below.
 //
-// Workgroup: 256 threads (4 waves as 2x2; the 16-bit direct tiles 512, 8
-// waves as 2x4 or 4x2), tile (2*WM*16) x (2*WN*16), each wave WM x WN MFMA
-// tiles of 16x16.  Operands are staged through LDS,
+// f32 storage, whole 32-deep k-blocks and strides of whole vectors: eight-wave
+// tiles too (F32Loader), 256 x 128 and 256 x 96 three k-blocks deep and
+// 128 x 128 four deep (split weight gradients among them), each wave's
+// 16x16x4 MFMAs taking the operands' roles exchanged so that its sums leave
+// as 16-byte row stores from the registers.
+//
+// Workgroup: 256 threads (4 waves as 2x2; the eight-wave tiles 512, as 2x4
+// or 4x2), tile (2*WM*16) x (2*WN*16), each wave WM x WN MFMA tiles of
+// 16x16 (of 32x32 in the 16-bit direct tiles).  Operands are staged through LDS,
 // double-buffered (one barrier per k-block), each as it lies in memory: a
 // k-contiguous operand as [row][k], an m- or n-contiguous one as [k][row]
 // (16-byte writes either way).  MFMA fragments hold consecutive k of one
@@ -746,9 +753,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
         stage_tail(block, kt, nd, std::make_integer_sequence<int, NS - 1>{});
     } else if constexpr (F8) {
         // The 16-bit stages' order of loads, waits and barriers over 32-deep
-        // f32 blocks: blocks kt + 1 and kt + 2 stream into LDS while block kt
-        // is multiplied; each 4-k step's fragments are read while the
-        // previous step's MFMAs run.  A's tile is whole rounds of loads; a
+        // f32 blocks: blocks kt + 1 .. kt + NS - 1 (two or three) stream into
+        // LDS while block kt is multiplied; each 4-k step's fragments are
+        // read while the previous step's MFMAs run.  A's tile is whole rounds of loads; a
         // 96-row B tile's last round is issued by the first waves only, which
         // then count one load more a block.
         static_assert(QA::PW == 0, "A: whole rounds");
@@ -1369,8 +1376,10 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     } else if (ST != kF32 && (g.bn == 128 || g.bn == 64)) {
         // 128 x 128 and 128 x 64 tiles of 32x32x16 MFMAs (a wave 64 x 64 or
         // 64 x 32), operands straight into LDS in two stages (two workgroups
-        // a CU); operands off 16 bytes or partial k-blocks: the same products
-        // from register-staged tiles.  Measured 10-20 % faster than the
+        // a CU), or 128 x 128 tiles of eight waves (a wave 32 x 64, four
+        // stages, one workgroup a CU: the split weight gradients); operands
+        // off 16 bytes or partial k-blocks: the same products from
+        // register-staged tiles.  Measured 10-20 % faster than the
         // register-staged 16x16x32 tiles at K 128-1536 (the course step's,
         // the MLP block's and the Llama attention scores' shapes).
         if constexpr (ST != kF32) {
