@@ -51,7 +51,23 @@ def test_tile_override(monkeypatch):
     assert compiled(f32).order == "mfma-f32-k4"
 
 
+def test_eight_wave_tile_override(monkeypatch):
+    # `w8` after 128x128: the eight-wave 128 x 128 tiles, split or not, in
+    # both storage families; the order names the same MFMAs and split
+    f32, bf = dot(256, 8192, 256, "f32"), dot(256, 8192, 256, "bf16")
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x128w8/7")
+    assert compiled(f32).order == "mfma-f32-k4-split7"
+    assert compiled(bf).order == "mfma-k16-split7"
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x128w8/1")
+    assert compiled(f32).order == "mfma-f32-k4"
+    monkeypatch.setenv("PRESK_HIP_GEMM_TILE", "128x128w8")      # no split named: the planner's
+    assert compiled(f32).order.startswith("mfma-f32-k4-split")
+    assert hip.lib().presk_hip_init(-1) == 0
+
+
 @pytest.mark.parametrize("var,value", [("PRESK_HIP_GEMM_TILE", "256x64"), ("PRESK_HIP_GEMM_TILE", "128x128/0"),
+                                       ("PRESK_HIP_GEMM_TILE", "128x64w8"), ("PRESK_HIP_GEMM_TILE", "256x128w8"),
+                                       ("PRESK_HIP_GEMM_TILE", "128x128w4"),
                                        ("PRESK_HIP_GEMM_TILE", "128x128x"), ("PRESK_HIP_MODE", "fastest"),
                                        ("PRESK_HIP_DEVICE", "one")])
 def test_malformed_switch_fails_init(monkeypatch, var, value):
