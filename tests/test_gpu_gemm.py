@@ -342,3 +342,40 @@ def test_eight_wave_128_tiles_equal_the_four_wave_tiles(layout, splits, dt, monk
     assert not np.any(outs[1] == code(-1 & (0xFFFFFFFF if dt == "f32" else 0xFFFF))), "unwritten outputs"
     differ = np.count_nonzero(outs[0] != outs[1])
     assert differ == 0, f"{differ} of {outs[0].size} outputs differ from the four-wave tiles'"
+
+
+# Short K (one, two and three k-blocks: fewer than the stages in flight) and
+# operands smaller than a tile on the eight-wave tiles, against the
+# four-wave 128 x 128 tiles, bit for bit.
+SHORT = [(100, 32, 72, "f32"), (300, 64, 200, "f32"), (520, 96, 136, "f32"), (40, 128, 392, "f32"),
+         (100, 64, 72, "bf16"), (300, 128, 200, "bf16"), (520, 192, 136, "f16")]
+
+
+@pytest.mark.parametrize("m,k,n,dt", SHORT)
+@pytest.mark.parametrize("tiles", ["256x128", "256x96", "128x128w8/1"])
+def test_eight_wave_tiles_short_k_and_small_operands(m, k, n, dt, tiles, monkeypatch):
+    from oracle import kernel_text as kt
+    if dt != "f32" and tiles == "256x96":
+        pytest.skip("256 x 96 tiles are f32 only")
+    low = L.dot([O(A(("batch", m), k)), O(A(k, n)), O(A(n))], dt, epilogue=(True, A(("batch", m), n)))
+    print(f"[gemm] short {m}x{k}x{n} {dt} {tiles}", flush=True)
+    kn = kt.parse_kernel(low.text)
+    rng = np.random.default_rng(m + k + n)
+    vals = [rng.standard_normal(b.dims, dtype=np.float32) for b in kn.inputs]
+    ins = [hip.DeviceBuffer.of(v if dt == "f32" else fmt.encode(fmt.roundtrip(v, dt), dt)) for v in vals]
+    esz, code = (4, np.uint32) if dt == "f32" else (2, np.uint16)
+    outs = []
+    for t in (tiles, "128x128/1"):
+        monkeypatch.setenv("PRESK_HIP_GEMM_TILE", t)
+        c = hip.Compiled(low.text, dt, low.lanes, hip.FAST)
+        assert c.kind == "gemm" and "split" not in c.order, (c.kind, c.order)
+        out = hip.DeviceBuffer(kn.output.numel * esz)
+        out.upload(np.full(kn.output.numel * esz, 0xFF, np.uint8))
+        flag = hip.DeviceBuffer(4)
+        flag.zero()
+        c.run([b.ptr for b in ins] + [out.ptr] + ([flag.ptr] if c.guarded else []))
+        hip.sync()
+        outs.append(out.download(code))
+    assert not np.any(outs[1] == code(0xFFFFFFFF if dt == "f32" else 0xFFFF)), "unwritten outputs"
+    differ = np.count_nonzero(outs[0] != outs[1])
+    assert differ == 0, f"{differ} of {outs[0].size} outputs differ from the four-wave tiles'"
