@@ -81,11 +81,13 @@ typedef struct {
  *   PRESK_HIP_MODE=exact|fast       every kernel compiled in that mode, whatever
  *                                   presk_hip_compile is asked (exact: the
  *                                   interpreter's order in every kernel);
- *   PRESK_HIP_GEMM_TILE=<bm>x<bn>[/<splits>]
- *                                   contraction tiles (128 x 64/96/128, or
- *                                   256 x 128/256 on 16-bit storage) and k
- *                                   splits (1-64, single-entry contractions)
- *                                   in place of the planner's, where they apply;
+ *   PRESK_HIP_GEMM_TILE=<bm>x<bn>[w8][/<splits>]
+ *                                   contraction tiles (128 x 64/96/128, w8
+ *                                   after 128x128 for eight waves; 256 x
+ *                                   96/128 on f32 storage, 256 x 128/256 on
+ *                                   16-bit) and k splits (1-64, single-entry
+ *                                   contractions) in place of the planner's,
+ *                                   where they apply;
  *   PRESK_HIP_CACHE, PRESK_HIP_DUMP  the generated kernels' code-object cache
  *                                   and a directory to keep their sources in. */
 int presk_hip_init(int device);
