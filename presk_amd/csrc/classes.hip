@@ -284,10 +284,10 @@ bool tile_override(TileOverride* t, std::string* err) {
         rest += ok ? used : 0;
     }
     const bool shape = (bm == 128 && (bn == 64 || bn == 96 || bn == 128)) || (bm == 256 && (bn == 96 || bn == 128 || bn == 256));
-    if (!ok || *rest != '\0' || !shape || (eight && !(bm == 128 && bn == 128))) {
+    if (!ok || *rest != '\0' || !shape || (eight && !(bm == 128 && (bn == 128 || bn == 96)))) {
         *err = std::string("PRESK_HIP_GEMM_TILE=") + env +
                ": expected <bm>x<bn>[w8][/<splits>] with bm 128 (bn 64, 96, 128) or 256 (bn 96, 128, 256), w8 only "
-               "after 128x128, and splits 1-64";
+               "after 128x128 or 128x96, and splits 1-64";
         return false;
     }
     *t = TileOverride{bm, bn, splits, eight};
@@ -307,7 +307,8 @@ void apply_override(GemmArgs& g) {
     g.stream = false;     // the named tiles, not the streamed panels
     g.bm = t.bm;
     g.bn = t.bn;
-    g.eight = t.eight;
+    // (eight-wave 128 x 96 tiles are f32's only)
+    g.eight = t.eight && (t.bn == 128 || g.storage == kF32);
     g.tiles_m = (int)((g.M + g.bm - 1) / g.bm);
     g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
     const int bk = gemm_block_k(g.storage);
@@ -461,26 +462,29 @@ void plan_tiles(GemmArgs& g) {
     // 1024] 88 -> 74 us (128 x 128), each the fastest of the three measured
     if (g.storage == kF32) {
         if (g.splits == 1 && g.K >= 384 && g.K % gemm_block_k(kF32) == 0 && g.N >= 128 && all_vec) {
-            static const int shapes[3][2] = {{256, 128}, {256, 96}, {128, 128}};
+            // {rows, columns, workgroups a CU}; on a tie the earlier
+            static const int shapes[4][3] = {{256, 128, 1}, {128, 96, 2}, {256, 96, 1}, {128, 128, 1}};
             long long best_cost = -1, best_t = 0;
             int bi = 0;
-            for (int i = 0; i < 3; ++i) {
-                const int bm = shapes[i][0], bn = shapes[i][1];
+            for (int i = 0; i < 4; ++i) {
+                const int bm = shapes[i][0], bn = shapes[i][1], per = shapes[i][2];
                 const long long t = (long long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch;
-                const long long cost = (t + 255) / 256 * bm * bn;
-                if (best_cost < 0 || cost < best_cost) {
+                const long long slots = 256LL * per;
+                const long long cost = (t + slots - 1) / slots * per * bm * bn;
+                if (t >= slots && (best_cost < 0 || cost < best_cost)) {
                     best_cost = cost;
                     best_t = t;
                     bi = i;
                 }
             }
-            if (best_t >= 256) {
+            if (best_cost >= 0) {
                 g.bm = shapes[bi][0];
                 g.bn = shapes[bi][1];
                 g.eight = g.bm == 128;
                 g.tiles_m = (int)((g.M + g.bm - 1) / g.bm);
                 g.tiles_n = (int)((g.N + g.bn - 1) / g.bn);
             }
+            (void)best_t;
         }
         apply_override(g);
         return;

@@ -599,10 +599,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs g) {
     // else two (256 x 256, 128 KB); two for 128-row tiles (64 or 48 KB), so
     // that two workgroups share a CU
     // f32 eight-wave tiles: as many stages as fit, at most four (128 x 128: 4
-    // x 32 KB; 256 x 128 and 256 x 96: 3 x 48 and 3 x 44 KB)
+    // x 32 KB; 256 x 128 and 256 x 96: 3 x 48 and 3 x 44 KB), but two for
+    // 128 x 96 (2 x 28 KB: two workgroups a CU, four waves a SIMD)
     // 16-bit: two stages for four-wave 128-row tiles (two workgroups a CU),
     // four for eight-wave ones (one a CU), else three where they fit
-    constexpr int NS = F8 ? (4 * STAGE <= 150 * 1024 ? 4 : 3)
+    constexpr int NS = F8 ? (BM == 128 && BN == 96 ? 2 : 4 * STAGE <= 150 * 1024 ? 4 : 3)
                           : BM == 128 ? (NW == 8 ? 4 : 2) : 3 * STAGE <= 150 * 1024 ? 3 : 2;
     // the epilogue stages the tile's f32 sums in LDS whole, or in two halves
     // of rows when the whole would not fit beside nothing else (256 x 256)
@@ -1331,14 +1332,16 @@ hipError_t launch_typed(const GemmArgs& g, hipStream_t stream) {
     if constexpr (ST == kF32) {
     if (g.bm == 256 || g.eight) {
         // 256 x 128 or 256 x 96 tiles of eight waves (4 x 2 waves of 64 x 64
-        // or 64 x 48), three stages straight into LDS, or 128 x 128 ones (4 x
-        // 2 waves of 32 x 64) four stages deep; operands that do not allow it
+        // or 64 x 48), three stages straight into LDS, 128 x 128 ones (4 x 2
+        // waves of 32 x 64) four stages deep, or 128 x 96 ones (32 x 48) two
+        // stages deep, two workgroups a CU; operands that do not allow it
         // (alignment is known only here) take the four-wave 128-row tiles of
         // the same columns and split -- the same MFMAs over the same k-steps
         if (gemm_f32_wide_fits(g)) {
             if (g.bm == 256 && g.bn == 96) e = launch_shape<ST, 4, 3, false, true, 16, 8, 2>(g, stream);
             else if (g.bm == 256 && g.bn == 128) e = launch_shape<ST, 4, 4, false, true, 16, 8, 2>(g, stream);
             else if (g.bm == 128 && g.bn == 128) e = launch_shape<ST, 2, 4, false, true, 16, 8, 2>(g, stream);
+            else if (g.bm == 128 && g.bn == 96) e = launch_shape<ST, 2, 3, false, true, 16, 8, 2>(g, stream);
             else return hipErrorInvalidValue;
             if (e != hipSuccess || g.splits <= 1) return e;
             split_reduce_kernel<ST><<<(unsigned)((g.M * g.N + 255) / 256), 256, 0, stream>>>(g);

@@ -261,7 +261,7 @@ def test_eight_wave_tiles_equal_the_128_row_tiles(layout, dt, tiles, monkeypatch
 # and columns past the last tile, every remainder of the stage rounds, and
 # with the bias.  Operands that the wide tiles cannot take (a row off 16
 # bytes) run the 128-row tiles of the same columns, the same bits again.
-@pytest.mark.parametrize("layout,tiles", [(lay, t) for lay in EIGHT for t in ("256x128", "256x96")])
+@pytest.mark.parametrize("layout,tiles", [(lay, t) for lay in EIGHT for t in ("256x128", "256x96", "128x96w8/1")])
 def test_f32_eight_wave_tiles_equal_the_128_row_tiles(layout, tiles, monkeypatch):
     from oracle import kernel_text as kt
     low = EIGHT[layout]("f32")
@@ -352,11 +352,11 @@ SHORT = [(100, 32, 72, "f32"), (300, 64, 200, "f32"), (520, 96, 136, "f32"), (40
 
 
 @pytest.mark.parametrize("m,k,n,dt", SHORT)
-@pytest.mark.parametrize("tiles", ["256x128", "256x96", "128x128w8/1"])
+@pytest.mark.parametrize("tiles", ["256x128", "256x96", "128x128w8/1", "128x96w8/1"])
 def test_eight_wave_tiles_short_k_and_small_operands(m, k, n, dt, tiles, monkeypatch):
     from oracle import kernel_text as kt
-    if dt != "f32" and tiles == "256x96":
-        pytest.skip("256 x 96 tiles are f32 only")
+    if dt != "f32" and tiles in ("256x96", "128x96w8/1"):
+        pytest.skip("256 x 96 and eight-wave 128 x 96 tiles are f32 only")
     low = L.dot([O(A(("batch", m), k)), O(A(k, n)), O(A(n))], dt, epilogue=(True, A(("batch", m), n)))
     print(f"[gemm] short {m}x{k}x{n} {dt} {tiles}", flush=True)
     kn = kt.parse_kernel(low.text)
