@@ -83,7 +83,8 @@ typedef struct {
  *                                   interpreter's order in every kernel);
  *   PRESK_HIP_GEMM_TILE=<bm>x<bn>[w8][/<splits>]
  *                                   contraction tiles (128 x 64/96/128, w8
- *                                   after 128x128 for eight waves; 256 x
+ *                                   after 128x128 or 128x96 (f32) for eight
+ *                                   waves; 256 x
  *                                   96/128 on f32 storage, 256 x 128/256 on
  *                                   16-bit) and k splits (1-64, single-entry
  *                                   contractions) in place of the planner's,

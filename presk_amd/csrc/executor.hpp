@@ -60,7 +60,7 @@ std::unique_ptr<ClassPlan> classify(const Kernel& k, int mode);
 // malformed; an unset or empty variable is no override (bm 0).
 struct TileOverride {
     int bm = 0, bn = 0, splits = 0;
-    bool eight = false;     // 128 x 128 tiles of eight waves
+    bool eight = false;     // 128-row tiles of eight waves (128 x 128, or 128 x 96 in f32)
 };
 bool tile_override(TileOverride* t, std::string* err);
 

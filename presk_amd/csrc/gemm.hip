@@ -29,8 +29,9 @@
 // operands; 128 x 96 tiles take the 16x16 MFMAs below.
 //
 // f32 storage, whole 32-deep k-blocks and strides of whole vectors: eight-wave
-// tiles too (F32Loader), 256 x 128 and 256 x 96 three k-blocks deep and
-// 128 x 128 four deep (split weight gradients among them), each wave's
+// tiles too (F32Loader), 256 x 128 and 256 x 96 three k-blocks deep, 128 x
+// 128 four deep (split weight gradients among them) and 128 x 96 two deep
+// (two workgroups a CU), each wave's
 // 16x16x4 MFMAs taking the operands' roles exchanged so that its sums leave
 // as 16-byte row stores from the registers.
 //

@@ -30,7 +30,7 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     int bm;                         // tile rows: 128, or 256 (eight-wave tiles)
     int bn;                         // tile columns: 256, 128, 96 or 64
-    bool eight;                     // 128 x 128 tiles of eight waves (256-row tiles always have eight)
+    bool eight;                     // 128-row tiles of eight waves: 128 x 128, or 128 x 96 in f32 (256-row tiles always have eight)
     bool stream;                    // K of at most two k-blocks may stream B's tiles across a kept A panel
 };
 
